@@ -1,0 +1,374 @@
+// cbq_dequant.hip - FP8 E4M3 / INT8 dequantization kernels for gfx950 and
+// their C-ABI entry points: y = T(float(q) * scale), rounded to nearest even.
+//
+// Kernels (reference kernels they replace, kernels/cuda/quantization/...):
+//   k_deq_tensor     one scale: 16 codes per thread step, one 16-byte load
+//                    and two 16-byte stores (dequantize_per_tensor_fp8.cu:23-66,
+//                    dequantize_int8.cu:29-64)
+//   k_deq_rows_sub   rows of 8..2048 codes (per-group, short per-channel rows)
+//                    owned by power-of-two lane groups; 8-byte loads, 16-byte
+//                    stores (dequantize_int8.cu:118-134, :70-109)
+//   k_deq_rows_wg    one workgroup per row of any length that is a multiple
+//                    of 8 (long per-channel rows)
+//   k_deq_rows_scalar any row length, element at a time
+//   k_deq_cols       per-column scales (axis 1): each thread keeps the scales
+//                    of its eight columns in registers while walking rows
+#include "cbq_device.h"
+#include "cbq_host.h"
+
+namespace cbq {
+namespace {
+
+constexpr int kDU = 2;   // 16-code chunks in flight per thread (per tensor)
+
+template <bool FP8>
+__device__ __forceinline__ void dec4(uint32_t w, float* f) {
+  if constexpr (FP8) fp8x4_to_f32(w, f);
+  else int8x4_to_f32(w, f);
+}
+
+template <bool FP8>
+__device__ __forceinline__ float dec1(uint8_t b) {
+  float f[4];
+  dec4<FP8>(static_cast<uint32_t>(b), f);
+  return f[0];
+}
+
+template <int OUT>
+__device__ __forceinline__ void st8(void* y, int64_t elem, const float (&f)[8]) {
+  *reinterpret_cast<uint4*>(static_cast<uint16_t*>(y) + elem) = pack8_out<OUT>(f);
+}
+
+template <int OUT>
+__device__ __forceinline__ void st1(void* y, int64_t i, float v) {
+  static_cast<uint16_t*>(y)[i] = out1<OUT>(v);
+}
+
+// ---------------------------------------------------------------------------
+// Per tensor
+// ---------------------------------------------------------------------------
+template <bool FP8, int OUT>
+__global__ __launch_bounds__(kBlock) void k_deq_tensor(
+    const uint8_t* __restrict__ q, const float* __restrict__ scale, int64_t n, int vec,
+    void* __restrict__ y) {
+  const float s = scale[0];
+  if (vec) {
+    const int64_t n16 = n >> 4;
+    const int64_t step = static_cast<int64_t>(gridDim.x) * kDU * kBlock;
+    for (int64_t c0 = static_cast<int64_t>(blockIdx.x) * kDU * kBlock + threadIdx.x; c0 < n16;
+         c0 += step) {
+      uint4 r[kDU];
+#pragma unroll
+      for (int u = 0; u < kDU; ++u) {
+        const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
+        if (c < n16) r[u] = reinterpret_cast<const uint4*>(q)[c];
+      }
+#pragma unroll
+      for (int u = 0; u < kDU; ++u) {
+        const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
+        if (c < n16) {
+          float f[8];
+          dec4<FP8>(r[u].x, f);
+          dec4<FP8>(r[u].y, f + 4);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) f[k] *= s;
+          st8<OUT>(y, c * 16, f);
+          dec4<FP8>(r[u].z, f);
+          dec4<FP8>(r[u].w, f + 4);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) f[k] *= s;
+          st8<OUT>(y, c * 16 + 8, f);
+        }
+      }
+    }
+    if (blockIdx.x == 0) {
+      const int64_t i = n16 * 16 + threadIdx.x;   // the < 16 trailing codes
+      if (i < n) st1<OUT>(y, i, dec1<FP8>(q[i]) * s);
+    }
+  } else {
+    const int64_t step = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += step)
+      st1<OUT>(y, i, dec1<FP8>(q[i]) * s);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Rows: scale[row] for rows of L codes
+// ---------------------------------------------------------------------------
+template <int OUT, int LPR, int VPL, int RI>
+__global__ __launch_bounds__(kBlock) void k_deq_rows_sub(
+    const int8_t* __restrict__ q, const float* __restrict__ scale, int64_t rows,
+    void* __restrict__ y) {
+  constexpr int RPW = kWave / LPR;
+  constexpr int64_t L = static_cast<int64_t>(LPR) * VPL * 8;
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int sub = lane / LPR;
+  const int lr = lane % LPR;
+  const int64_t row0 =
+      (static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + wave) * (RI * RPW) + sub;
+  uint2 r[RI][VPL];
+  float s[RI];
+#pragma unroll
+  for (int it = 0; it < RI; ++it) {
+    const int64_t row = row0 + static_cast<int64_t>(it) * RPW;
+    if (row < rows) {
+      s[it] = scale[row];
+#pragma unroll
+      for (int v = 0; v < VPL; ++v)
+        r[it][v] = *reinterpret_cast<const uint2*>(q + row * L + (v * LPR + lr) * 8);
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < RI; ++it) {
+    const int64_t row = row0 + static_cast<int64_t>(it) * RPW;
+    if (row < rows) {
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        float f[8];
+        int8x4_to_f32(r[it][v].x, f);
+        int8x4_to_f32(r[it][v].y, f + 4);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) f[k] *= s[it];
+        st8<OUT>(y, row * L + (v * LPR + lr) * 8, f);
+      }
+    }
+  }
+}
+
+// One workgroup per row (striding over rows); L % 8 == 0, aligned pointers.
+template <int OUT>
+__global__ __launch_bounds__(kBlock) void k_deq_rows_wg(
+    const int8_t* __restrict__ q, const float* __restrict__ scale, int64_t rows, int64_t L,
+    void* __restrict__ y) {
+  const int64_t nc = L >> 3;
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const float s = scale[row];
+    const int64_t base = row * L;
+    int64_t c = threadIdx.x;
+    for (; c + 3 * kBlock < nc; c += 4 * kBlock) {
+      uint2 r[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        r[u] = *reinterpret_cast<const uint2*>(q + base + (c + u * kBlock) * 8);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        float f[8];
+        int8x4_to_f32(r[u].x, f);
+        int8x4_to_f32(r[u].y, f + 4);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) f[k] *= s;
+        st8<OUT>(y, base + (c + u * kBlock) * 8, f);
+      }
+    }
+    for (; c < nc; c += kBlock) {
+      const uint2 r = *reinterpret_cast<const uint2*>(q + base + c * 8);
+      float f[8];
+      int8x4_to_f32(r.x, f);
+      int8x4_to_f32(r.y, f + 4);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) f[k] *= s;
+      st8<OUT>(y, base + c * 8, f);
+    }
+  }
+}
+
+template <int OUT>
+__global__ __launch_bounds__(kBlock) void k_deq_rows_scalar(
+    const int8_t* __restrict__ q, const float* __restrict__ scale, int64_t rows, int64_t L,
+    void* __restrict__ y) {
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const float s = scale[row];
+    const int64_t base = row * L;
+    for (int64_t i = threadIdx.x; i < L; i += kBlock)
+      st1<OUT>(y, base + i, static_cast<float>(q[base + i]) * s);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Columns: scale[col] (axis 1). Row block blockIdx.y of RB rows.
+// ---------------------------------------------------------------------------
+template <int OUT>
+__global__ __launch_bounds__(kBlock) void k_deq_cols(
+    const int8_t* __restrict__ q, const float* __restrict__ scale, int64_t rows, int64_t cols,
+    int64_t RB, int vec, void* __restrict__ y) {
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * RB;
+  const int64_t r1 = r0 + RB < rows ? r0 + RB : rows;
+  if (vec) {
+    const int64_t c = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * 8;
+    if (c >= cols) return;
+    float s[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s[k] = scale[c + k];
+    int64_t r = r0;
+    for (; r + 4 <= r1; r += 4) {
+      uint2 raw[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) raw[u] = *reinterpret_cast<const uint2*>(q + (r + u) * cols + c);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        float f[8];
+        int8x4_to_f32(raw[u].x, f);
+        int8x4_to_f32(raw[u].y, f + 4);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) f[k] *= s[k];
+        st8<OUT>(y, (r + u) * cols + c, f);
+      }
+    }
+    for (; r < r1; ++r) {
+      const uint2 raw = *reinterpret_cast<const uint2*>(q + r * cols + c);
+      float f[8];
+      int8x4_to_f32(raw.x, f);
+      int8x4_to_f32(raw.y, f + 4);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) f[k] *= s[k];
+      st8<OUT>(y, r * cols + c, f);
+    }
+  } else {
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (c >= cols) return;
+    const float s = scale[c];
+    for (int64_t r = r0; r < r1; ++r)
+      st1<OUT>(y, r * cols + c, static_cast<float>(q[r * cols + c]) * s);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch
+// ---------------------------------------------------------------------------
+bool valid_out(int dt) { return dt == kF16 || dt == kBF16; }
+
+unsigned rows_grid(int64_t rows) {
+  const int64_t cap = 1 << 20;
+  return static_cast<unsigned>(rows < cap ? rows : cap);
+}
+
+template <bool FP8, int OUT>
+int deq_tensor_t(const uint8_t* q, const float* scale, int64_t n, void* y, hipStream_t s,
+                 const char* what) {
+  const bool vec = aligned(q, 16) && aligned(y, 16);
+  const int64_t work = vec ? cdiv(n >> 4, static_cast<int64_t>(kDU) * kBlock) : cdiv(n, kBlock);
+  const int64_t cap = static_cast<int64_t>(device_cus()) * 8;
+  int64_t grid = work < cap ? work : cap;
+  if (grid < 1) grid = 1;
+  k_deq_tensor<FP8, OUT><<<dim3(static_cast<unsigned>(grid)), dim3(kBlock), 0, s>>>(
+      q, scale, n, vec ? 1 : 0, y);
+  return launch_status(what);
+}
+
+template <bool FP8>
+int deq_tensor(const uint8_t* q, const float* scale, int64_t n, void* y, int out, hipStream_t s,
+               const char* what) {
+  CBQ_REQUIRE(valid_out(out), "%s: out_dtype must be fp16 or bf16 (code %d)", what, out);
+  CBQ_REQUIRE(n >= 0, "%s: negative element count", what);
+  if (n == 0) return CBQ_OK;
+  CBQ_REQUIRE(q && scale && y, "%s: null pointer", what);
+  return out == kF16 ? deq_tensor_t<FP8, kF16>(q, scale, n, y, s, what)
+                     : deq_tensor_t<FP8, kBF16>(q, scale, n, y, s, what);
+}
+
+template <int OUT, int LPR, int VPL>
+void launch_deq_rows_sub(const int8_t* q, const float* scale, int64_t rows, void* y,
+                         hipStream_t s) {
+  constexpr int RI = (LPR * VPL >= 64) ? 2 : 4;
+  constexpr int64_t rows_per_wg = static_cast<int64_t>(kBlock / kWave) * RI * (kWave / LPR);
+  k_deq_rows_sub<OUT, LPR, VPL, RI><<<dim3(static_cast<unsigned>(cdiv(rows, rows_per_wg))),
+                                       dim3(kBlock), 0, s>>>(q, scale, rows, y);
+}
+
+template <int OUT>
+int deq_rows_t(const int8_t* q, const float* scale, int64_t rows, int64_t L, void* y,
+               hipStream_t s, const char* what) {
+  CBQ_REQUIRE(rows <= 0x7fffffffLL, "%s: too many rows (%lld)", what, (long long)rows);
+  const bool vec = (L % 8 == 0) && aligned(q, 8) && aligned(y, 16);
+  if (vec) {
+    switch (L) {
+      case 8: launch_deq_rows_sub<OUT, 1, 1>(q, scale, rows, y, s); return launch_status(what);
+      case 16: launch_deq_rows_sub<OUT, 2, 1>(q, scale, rows, y, s); return launch_status(what);
+      case 32: launch_deq_rows_sub<OUT, 4, 1>(q, scale, rows, y, s); return launch_status(what);
+      case 64: launch_deq_rows_sub<OUT, 8, 1>(q, scale, rows, y, s); return launch_status(what);
+      case 128: launch_deq_rows_sub<OUT, 16, 1>(q, scale, rows, y, s); return launch_status(what);
+      case 256: launch_deq_rows_sub<OUT, 32, 1>(q, scale, rows, y, s); return launch_status(what);
+      case 512: launch_deq_rows_sub<OUT, 64, 1>(q, scale, rows, y, s); return launch_status(what);
+      case 1024: launch_deq_rows_sub<OUT, 64, 2>(q, scale, rows, y, s); return launch_status(what);
+      case 2048: launch_deq_rows_sub<OUT, 64, 4>(q, scale, rows, y, s); return launch_status(what);
+      default:
+        k_deq_rows_wg<OUT><<<dim3(rows_grid(rows)), dim3(kBlock), 0, s>>>(q, scale, rows, L, y);
+        return launch_status(what);
+    }
+  }
+  k_deq_rows_scalar<OUT><<<dim3(rows_grid(rows)), dim3(kBlock), 0, s>>>(q, scale, rows, L, y);
+  return launch_status(what);
+}
+
+int deq_rows(const int8_t* q, const float* scale, int64_t rows, int64_t L, void* y, int out,
+             hipStream_t s, const char* what) {
+  return out == kF16 ? deq_rows_t<kF16>(q, scale, rows, L, y, s, what)
+                     : deq_rows_t<kBF16>(q, scale, rows, L, y, s, what);
+}
+
+template <int OUT>
+int deq_cols_t(const int8_t* q, const float* scale, int64_t rows, int64_t cols, void* y,
+               hipStream_t s) {
+  const bool vec = (cols % 8 == 0) && aligned(q, 8) && aligned(y, 16);
+  const int64_t col_blocks = vec ? cdiv(cdiv(cols, 8), kBlock) : cdiv(cols, kBlock);
+  int64_t nrb = 2048 / col_blocks;
+  const int64_t max_nrb = cdiv(rows, 16);
+  if (nrb > max_nrb) nrb = max_nrb;
+  if (nrb > 65535) nrb = 65535;
+  if (nrb < 1) nrb = 1;
+  const int64_t RB = cdiv(rows, nrb);
+  nrb = cdiv(rows, RB);
+  k_deq_cols<OUT><<<dim3(static_cast<unsigned>(col_blocks), static_cast<unsigned>(nrb)),
+                    dim3(kBlock), 0, s>>>(q, scale, rows, cols, RB, vec ? 1 : 0, y);
+  return launch_status("cbq_dequant_int8_channel");
+}
+
+}  // namespace
+}  // namespace cbq
+
+using namespace cbq;
+
+extern "C" int cbq_dequant_fp8_tensor(const uint8_t* q, const float* scale, int64_t n, void* y,
+                                      int out_dtype, cbq_stream_t stream) {
+  clear_error();
+  return deq_tensor<true>(q, scale, n, y, out_dtype, as_stream(stream), "cbq_dequant_fp8_tensor");
+}
+
+extern "C" int cbq_dequant_int8_tensor(const int8_t* q, const float* scale, int64_t n, void* y,
+                                       int out_dtype, cbq_stream_t stream) {
+  clear_error();
+  return deq_tensor<false>(reinterpret_cast<const uint8_t*>(q), scale, n, y, out_dtype,
+                           as_stream(stream), "cbq_dequant_int8_tensor");
+}
+
+extern "C" int cbq_dequant_int8_channel(const int8_t* q, const float* scale, int64_t rows,
+                                        int64_t cols, int axis, void* y, int out_dtype,
+                                        cbq_stream_t stream) {
+  clear_error();
+  const char* what = "cbq_dequant_int8_channel";
+  CBQ_REQUIRE(valid_out(out_dtype), "%s: out_dtype must be fp16 or bf16 (code %d)", what,
+              out_dtype);
+  CBQ_REQUIRE(axis == 0 || axis == 1, "%s: axis must be 0 or 1, got %d", what, axis);
+  CBQ_REQUIRE(rows >= 0 && cols >= 0, "%s: negative shape", what);
+  if (rows == 0 || cols == 0) return CBQ_OK;
+  CBQ_REQUIRE(q && scale && y, "%s: null pointer", what);
+  if (axis == 0) return deq_rows(q, scale, rows, cols, y, out_dtype, as_stream(stream), what);
+  return out_dtype == kF16 ? deq_cols_t<kF16>(q, scale, rows, cols, y, as_stream(stream))
+                           : deq_cols_t<kBF16>(q, scale, rows, cols, y, as_stream(stream));
+}
+
+extern "C" int cbq_dequant_int8_group(const int8_t* q, const float* scale, int64_t num_groups,
+                                      int64_t group_size, void* y, int out_dtype,
+                                      cbq_stream_t stream) {
+  clear_error();
+  const char* what = "cbq_dequant_int8_group";
+  CBQ_REQUIRE(valid_out(out_dtype), "%s: out_dtype must be fp16 or bf16 (code %d)", what,
+              out_dtype);
+  CBQ_REQUIRE(group_size > 0 && group_size <= 4096, "%s: group_size must be in (0, 4096], got %lld",
+              what, (long long)group_size);
+  CBQ_REQUIRE(num_groups >= 0, "%s: negative group count", what);
+  if (num_groups == 0) return CBQ_OK;
+  CBQ_REQUIRE(q && scale && y, "%s: null pointer", what);
+  return deq_rows(q, scale, num_groups, group_size, y, out_dtype, as_stream(stream), what);
+}

@@ -1,0 +1,236 @@
+// cbq_device.h - gfx950 device primitives shared by the quantization kernels.
+//
+// Element conversions, 8-element chunk loads/stores, the INT8 / FP8 E4M3
+// encoders and wave64 cross-lane max reductions. Numerics restate the
+// reference's shared headers:
+//   kernels/cuda/quantization/fp8_pack.cuh:26-75  (exact widening to fp32,
+//       round-to-nearest-even narrowing to fp16/bf16, FP8 -> 16-bit exact)
+//   kernels/cuda/quantization/int8_pack.cuh:51-56 (round half to even, clamp
+//       to [-127, 127])
+//   kernels/cuda/quantization/quantize_per_tensor_fp8.cu:117,129 (E4M3 cast
+//       with saturation to +-448, NaN kept)
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cbq {
+
+enum : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;          // 4 waves per workgroup
+constexpr float kQmaxInt8 = 127.0f;
+constexpr float kQmaxFp8 = 448.0f;
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// Raw 8-element chunks: one 16-byte load for 2-byte types, two for fp32.
+// ---------------------------------------------------------------------------
+template <int DT> struct Raw8 { uint4 a; };
+template <> struct Raw8<kF32> { uint4 a, b; };
+
+template <int DT> constexpr int elem_bytes() { return DT == kF32 ? 4 : 2; }
+
+template <int DT>
+__device__ __forceinline__ Raw8<DT> ld8(const void* base, int64_t elem) {
+  Raw8<DT> r;
+  const uint4* p = reinterpret_cast<const uint4*>(
+      static_cast<const char*>(base) + elem * elem_bytes<DT>());
+  r.a = p[0];
+  if constexpr (DT == kF32) r.b = p[1];
+  return r;
+}
+
+__device__ __forceinline__ f32x2 bf16x2_to_f32(uint32_t w) {
+  f32x2 f;
+  f.x = __uint_as_float(w << 16);
+  f.y = __uint_as_float(w & 0xffff0000u);
+  return f;
+}
+
+__device__ __forceinline__ f32x2 f16x2_to_f32(uint32_t w) {
+  return __builtin_convertvector(__builtin_bit_cast(f16x2, w), f32x2);
+}
+
+template <int DT>
+__device__ __forceinline__ f32x2 pair_to_f32(uint32_t w) {
+  if constexpr (DT == kBF16) return bf16x2_to_f32(w);
+  else return f16x2_to_f32(w);
+}
+
+template <int DT>
+__device__ __forceinline__ void cvt8(const Raw8<DT>& r, float (&f)[8]) {
+  if constexpr (DT == kF32) {
+    f[0] = __uint_as_float(r.a.x); f[1] = __uint_as_float(r.a.y);
+    f[2] = __uint_as_float(r.a.z); f[3] = __uint_as_float(r.a.w);
+    f[4] = __uint_as_float(r.b.x); f[5] = __uint_as_float(r.b.y);
+    f[6] = __uint_as_float(r.b.z); f[7] = __uint_as_float(r.b.w);
+  } else {
+    const uint32_t w[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      f32x2 p = pair_to_f32<DT>(w[k]);
+      f[2 * k] = p.x;
+      f[2 * k + 1] = p.y;
+    }
+  }
+}
+
+// One element at an arbitrary index (scalar paths and tails).
+template <int DT>
+__device__ __forceinline__ float ld1(const void* base, int64_t i) {
+  if constexpr (DT == kF32) {
+    return static_cast<const float*>(base)[i];
+  } else {
+    const uint32_t h = static_cast<const uint16_t*>(base)[i];
+    if constexpr (DT == kBF16) return __uint_as_float(h << 16);
+    else return static_cast<float>(__builtin_bit_cast(_Float16, (uint16_t)h));
+  }
+}
+
+// |x| max over a chunk. fmaxf returns the non-NaN operand, so NaN inputs are
+// ignored exactly as the reference's fmaxf fold does.
+__device__ __forceinline__ float absmax8(const float (&f)[8], float m) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) m = fmaxf(m, __builtin_fabsf(f[k]));
+  return m;
+}
+
+// ---------------------------------------------------------------------------
+// Output narrowing (round to nearest even).
+// ---------------------------------------------------------------------------
+template <int OUT>
+__device__ __forceinline__ uint32_t pack2_out(float a, float b) {
+  f32x2 v = {a, b};
+  if constexpr (OUT == kBF16) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+  }
+}
+
+template <int OUT>
+__device__ __forceinline__ uint16_t out1(float a) {
+  if constexpr (OUT == kBF16) return __builtin_bit_cast(uint16_t, (__bf16)a);
+  else return __builtin_bit_cast(uint16_t, (_Float16)a);
+}
+
+template <int OUT>
+__device__ __forceinline__ uint4 pack8_out(const float (&f)[8]) {
+  uint4 o;
+  o.x = pack2_out<OUT>(f[0], f[1]);
+  o.y = pack2_out<OUT>(f[2], f[3]);
+  o.z = pack2_out<OUT>(f[4], f[5]);
+  o.w = pack2_out<OUT>(f[6], f[7]);
+  return o;
+}
+
+// ---------------------------------------------------------------------------
+// INT8 encoder: round half to even, clamp to [-127, 127], NaN -> 0.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int q_int8(float v) {
+  float r = __builtin_rintf(v);              // v_rndne_f32: ties to even
+  r = r > 127.0f ? 127.0f : r;               // comparisons keep NaN as NaN
+  r = r < -127.0f ? -127.0f : r;
+  return (r == r) ? static_cast<int>(r) : 0;
+}
+
+__device__ __forceinline__ uint2 pack8_int8(const float (&f)[8], float inv) {
+  uint32_t w[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t b0 = static_cast<uint32_t>(q_int8(f[4 * h + 0] * inv)) & 0xffu;
+    const uint32_t b1 = static_cast<uint32_t>(q_int8(f[4 * h + 1] * inv)) & 0xffu;
+    const uint32_t b2 = static_cast<uint32_t>(q_int8(f[4 * h + 2] * inv)) & 0xffu;
+    const uint32_t b3 = static_cast<uint32_t>(q_int8(f[4 * h + 3] * inv)) & 0xffu;
+    w[h] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+  }
+  return make_uint2(w[0], w[1]);
+}
+
+// ---------------------------------------------------------------------------
+// FP8 E4M3 (OCP e4m3fn) encoder. gfx950's v_cvt_pk_fp8_f32 rounds to nearest
+// even; the explicit clamp gives the +-448 saturation and passes NaN through.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float sat448(float v) {
+  return __builtin_fabsf(v) > kQmaxFp8 ? __builtin_copysignf(kQmaxFp8, v) : v;
+}
+
+__device__ __forceinline__ uint32_t pack4_fp8(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(a), sat448(b), 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(c), sat448(d), w, true);
+  return static_cast<uint32_t>(w);
+}
+
+__device__ __forceinline__ uint2 pack8_fp8(const float (&f)[8], float inv) {
+  return make_uint2(pack4_fp8(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv),
+                    pack4_fp8(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv));
+}
+
+__device__ __forceinline__ uint8_t q_fp8_1(float v) {
+  return static_cast<uint8_t>(__builtin_amdgcn_cvt_pk_fp8_f32(sat448(v), 0.0f, 0, false) & 0xff);
+}
+
+// FP8 E4M3 -> fp32, exact (hardware conversion, OCP format on gfx950).
+__device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float* f) {
+  f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+  f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
+  f[0] = lo.x; f[1] = lo.y; f[2] = hi.x; f[3] = hi.y;
+}
+
+__device__ __forceinline__ void int8x4_to_f32(uint32_t w, float* f) {
+  f[0] = static_cast<float>(static_cast<int8_t>(w & 0xffu));
+  f[1] = static_cast<float>(static_cast<int8_t>((w >> 8) & 0xffu));
+  f[2] = static_cast<float>(static_cast<int8_t>((w >> 16) & 0xffu));
+  f[3] = static_cast<float>(static_cast<int8_t>(w >> 24));
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane max over aligned groups of LPR lanes (LPR a power of two <= 64).
+// Within a 16-lane DPP row: quad_perm xor-1, quad_perm xor-2, row_half_mirror,
+// row_mirror; across rows: ds_bpermute shuffles. Every lane of a group ends
+// with the group's maximum. All 64 lanes must be active.
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+template <int LPR>
+__device__ __forceinline__ float group_max(float m) {
+  static_assert(LPR >= 1 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "LPR");
+  if constexpr (LPR >= 2) m = fmaxf(m, dpp_f32<0xB1>(m));   // quad_perm [1,0,3,2]
+  if constexpr (LPR >= 4) m = fmaxf(m, dpp_f32<0x4E>(m));   // quad_perm [2,3,0,1]
+  if constexpr (LPR >= 8) m = fmaxf(m, dpp_f32<0x141>(m));  // row_half_mirror
+  if constexpr (LPR >= 16) m = fmaxf(m, dpp_f32<0x140>(m)); // row_mirror
+  if constexpr (LPR >= 32) m = fmaxf(m, __shfl_xor(m, 16, kWave));
+  if constexpr (LPR >= 64) m = fmaxf(m, __shfl_xor(m, 32, kWave));
+  return m;
+}
+
+// Workgroup-wide max; every thread gets the result. `red` holds one slot per
+// wave. Contains a barrier: call from uniform control flow only.
+__device__ __forceinline__ float block_max(float m, float* red) {
+  m = group_max<kWave>(m);
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x % kWave) == 0) red[wave] = m;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < static_cast<int>(blockDim.x) / kWave; ++w) r = fmaxf(r, red[w]);
+  __syncthreads();
+  return r;
+}
+
+// Reciprocal scale and stored scale, both correctly rounded fp32 divisions
+// (quantize_int8.cu:120-126 computes them in double and narrows once, which
+// is the same value; quantize_per_tensor_fp8.cu:99-102 intends the same).
+__device__ __forceinline__ float inv_scale(float amax, float eps, float qmax) {
+  return qmax / fmaxf(amax, eps);
+}
+
+}  // namespace cbq

@@ -1,0 +1,578 @@
+// cbq_quant.hip - symmetric FP8 E4M3 / INT8 quantization kernels for gfx950
+// and their C-ABI entry points.
+//
+// Kernels (reference kernels they replace, kernels/cuda/quantization/...):
+//   k_amax_tensor   per-tensor |x| max: 16-byte loads, wave64 DPP reduce, one
+//                   uint atomicMax per workgroup; the last workgroup turns the
+//                   maximum into inv / scale (quantize_per_tensor_fp8.cu:38-86,
+//                   quantize_int8.cu:47-101)
+//   k_cast_tensor   per-tensor cast, 16-byte loads and 8-byte packed stores
+//                   (quantize_per_tensor_fp8.cu:88-132, quantize_int8.cu:103-166)
+//   k_rows_sub      fused single-pass quant of rows of 8..2048 elements: each
+//                   row is owned by a power-of-two group of lanes, reduced
+//                   with DPP and cast from registers (per-group
+//                   quantize_int8.cu:307-371, short per-channel rows :173-297)
+//   k_rows_wg       fused single-pass quant of rows of 4096..16384 elements,
+//                   one workgroup per row held in registers (per-channel)
+//   k_rows_generic  any row length (two passes over the row; the second read
+//                   hits L2)
+//   k_colmax / k_col_finalize / k_cast_cols
+//                   per-column (axis 1) quant: partial column maxima per row
+//                   block, one finalize pass, then the cast with each
+//                   thread's eight column multipliers held in registers
+//
+// Numerics: see cbq_device.h. Every kernel guards its indices against the
+// sizes it is given; the entry points check shapes, dtypes and alignment.
+#include "cbq_device.h"
+#include "cbq_host.h"
+
+namespace cbq {
+namespace {
+
+// Control block words at the start of a workspace (zero between calls).
+enum : int { kCtlAmax = 0, kCtlCount = 1, kCtlInv = 2 };
+
+constexpr int kU = 4;                 // 8-element chunks in flight per thread
+constexpr int kTensorWgPerCu = 8;     // persistent grid size for per-tensor
+
+__device__ __forceinline__ uint32_t ld_acquire_agent(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// Per tensor
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_amax_tensor(
+    const void* __restrict__ x, int64_t n, int vec, uint32_t* __restrict__ ctl,
+    float eps, float qmax, float* __restrict__ scale_out) {
+  __shared__ float red[kBlock / kWave];
+  float m = 0.0f;
+  if (vec) {
+    const int64_t n8 = n >> 3;
+    const int64_t step = static_cast<int64_t>(gridDim.x) * kU * kBlock;
+    for (int64_t c0 = static_cast<int64_t>(blockIdx.x) * kU * kBlock + threadIdx.x; c0 < n8;
+         c0 += step) {
+      Raw8<DT> r[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
+        if (c < n8) r[u] = ld8<DT>(x, c * 8);
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
+        if (c < n8) {
+          float f[8];
+          cvt8<DT>(r[u], f);
+          m = absmax8(f, m);
+        }
+      }
+    }
+    if (blockIdx.x == 0) {
+      const int64_t i = n8 * 8 + threadIdx.x;   // the < 8 trailing elements
+      if (i < n) m = fmaxf(m, __builtin_fabsf(ld1<DT>(x, i)));
+    }
+  } else {
+    const int64_t step = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += step)
+      m = fmaxf(m, __builtin_fabsf(ld1<DT>(x, i)));
+  }
+  m = block_max(m, red);
+  if (threadIdx.x == 0) {
+    // m >= +0 and never NaN, so its bit pattern orders like the value.
+    atomicMax(&ctl[kCtlAmax], __float_as_uint(m));
+    __threadfence();
+    const uint32_t done = atomicAdd(&ctl[kCtlCount], 1u);
+    if (done == gridDim.x - 1) {
+      __threadfence();
+      const float amax = __uint_as_float(atomicOr(&ctl[kCtlAmax], 0u));
+      const float inv = inv_scale(amax, eps, qmax);
+      __hip_atomic_store(&ctl[kCtlInv], __float_as_uint(inv), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      *scale_out = 1.0f / inv;
+      atomicExch(&ctl[kCtlAmax], 0u);
+      atomicExch(&ctl[kCtlCount], 0u);
+    }
+  }
+}
+
+template <int DT, bool FP8>
+__global__ __launch_bounds__(kBlock) void k_cast_tensor(
+    const void* __restrict__ x, int64_t n, int vec, const uint32_t* __restrict__ ctl,
+    uint8_t* __restrict__ q) {
+  const float inv = __uint_as_float(ld_acquire_agent(&ctl[kCtlInv]));
+  if (vec) {
+    const int64_t n8 = n >> 3;
+    const int64_t step = static_cast<int64_t>(gridDim.x) * kU * kBlock;
+    for (int64_t c0 = static_cast<int64_t>(blockIdx.x) * kU * kBlock + threadIdx.x; c0 < n8;
+         c0 += step) {
+      Raw8<DT> r[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
+        if (c < n8) r[u] = ld8<DT>(x, c * 8);
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
+        if (c < n8) {
+          float f[8];
+          cvt8<DT>(r[u], f);
+          uint2 o = FP8 ? pack8_fp8(f, inv) : pack8_int8(f, inv);
+          *reinterpret_cast<uint2*>(q + c * 8) = o;
+        }
+      }
+    }
+    if (blockIdx.x == 0) {
+      const int64_t i = n8 * 8 + threadIdx.x;
+      if (i < n) {
+        const float v = ld1<DT>(x, i) * inv;
+        q[i] = FP8 ? q_fp8_1(v) : static_cast<uint8_t>(q_int8(v));
+      }
+    }
+  } else {
+    const int64_t step = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += step) {
+      const float v = ld1<DT>(x, i) * inv;
+      q[i] = FP8 ? q_fp8_1(v) : static_cast<uint8_t>(q_int8(v));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Rows (per-channel axis 0 and per-group): fused single pass
+// ---------------------------------------------------------------------------
+
+// Rows of L = LPR * VPL * 8 elements; LPR lanes own a row, each lane holding
+// VPL chunks. A wave covers 64 / LPR rows per iteration and RI iterations,
+// all loads issued before the first reduction.
+template <int DT, int LPR, int VPL, int RI>
+__global__ __launch_bounds__(kBlock) void k_rows_sub(
+    const void* __restrict__ x, int64_t rows, float eps, int8_t* __restrict__ q,
+    float* __restrict__ scale) {
+  constexpr int RPW = kWave / LPR;
+  constexpr int64_t L = static_cast<int64_t>(LPR) * VPL * 8;
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int sub = lane / LPR;
+  const int lr = lane % LPR;
+  const int64_t row0 =
+      (static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + wave) * (RI * RPW) + sub;
+
+  Raw8<DT> r[RI][VPL];
+#pragma unroll
+  for (int it = 0; it < RI; ++it) {
+    const int64_t row = row0 + static_cast<int64_t>(it) * RPW;
+    if (row < rows) {
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) r[it][v] = ld8<DT>(x, row * L + (v * LPR + lr) * 8);
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < RI; ++it) {
+    const int64_t row = row0 + static_cast<int64_t>(it) * RPW;
+    const bool ok = row < rows;
+    float f[VPL][8];
+    float m = 0.0f;
+    if (ok) {
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        cvt8<DT>(r[it][v], f[v]);
+        m = absmax8(f[v], m);
+      }
+    }
+    m = group_max<LPR>(m);   // every lane participates
+    const float inv = inv_scale(m, eps, kQmaxInt8);
+    if (ok) {
+#pragma unroll
+      for (int v = 0; v < VPL; ++v)
+        *reinterpret_cast<uint2*>(q + row * L + (v * LPR + lr) * 8) = pack8_int8(f[v], inv);
+      if (lr == 0) scale[row] = 1.0f / inv;
+    }
+  }
+}
+
+// One workgroup per row of L = 256 * VPL * 8 elements, held in registers.
+// Workgroups stride over rows (the row loop is uniform per workgroup).
+template <int DT, int VPL>
+__global__ __launch_bounds__(kBlock) void k_rows_wg(
+    const void* __restrict__ x, int64_t rows, float eps, int8_t* __restrict__ q,
+    float* __restrict__ scale) {
+  __shared__ float red[kBlock / kWave];
+  constexpr int64_t L = static_cast<int64_t>(kBlock) * VPL * 8;
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    Raw8<DT> r[VPL];
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) r[v] = ld8<DT>(x, row * L + (v * kBlock + threadIdx.x) * 8);
+    float f[VPL][8];
+    float m = 0.0f;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      cvt8<DT>(r[v], f[v]);
+      m = absmax8(f[v], m);
+    }
+    m = block_max(m, red);
+    const float inv = inv_scale(m, eps, kQmaxInt8);
+#pragma unroll
+    for (int v = 0; v < VPL; ++v)
+      *reinterpret_cast<uint2*>(q + row * L + (v * kBlock + threadIdx.x) * 8) = pack8_int8(f[v], inv);
+    if (threadIdx.x == 0) scale[row] = 1.0f / inv;
+  }
+}
+
+// Any row length: one workgroup per row (striding over rows), a reduce pass
+// then a cast pass. vec != 0 requires L % 8 == 0 and 16-byte / 8-byte
+// aligned x / q.
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_rows_generic(
+    const void* __restrict__ x, int64_t rows, int64_t L, int vec, float eps,
+    int8_t* __restrict__ q, float* __restrict__ scale) {
+  __shared__ float red[kBlock / kWave];
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const int64_t base = row * L;
+    float m = 0.0f;
+    if (vec) {
+      const int64_t nc = L >> 3;
+      for (int64_t c = threadIdx.x; c < nc; c += kBlock) {
+        float f[8];
+        cvt8<DT>(ld8<DT>(x, base + c * 8), f);
+        m = absmax8(f, m);
+      }
+    } else {
+      for (int64_t i = threadIdx.x; i < L; i += kBlock)
+        m = fmaxf(m, __builtin_fabsf(ld1<DT>(x, base + i)));
+    }
+    m = block_max(m, red);
+    const float inv = inv_scale(m, eps, kQmaxInt8);
+    if (vec) {
+      const int64_t nc = L >> 3;
+      for (int64_t c = threadIdx.x; c < nc; c += kBlock) {
+        float f[8];
+        cvt8<DT>(ld8<DT>(x, base + c * 8), f);
+        *reinterpret_cast<uint2*>(q + base + c * 8) = pack8_int8(f, inv);
+      }
+    } else {
+      for (int64_t i = threadIdx.x; i < L; i += kBlock)
+        q[base + i] = static_cast<int8_t>(q_int8(ld1<DT>(x, base + i) * inv));
+    }
+    if (threadIdx.x == 0) scale[row] = 1.0f / inv;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Columns (per-channel axis 1)
+// ---------------------------------------------------------------------------
+
+// Partial column maxima of row block blockIdx.y (rows [y*RB, y*RB+RB)).
+// vec: each thread owns 8 adjacent columns (cols % 8 == 0, aligned x);
+// otherwise one column. partial is [gridDim.y, cols] fp32.
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_colmax(
+    const void* __restrict__ x, int64_t rows, int64_t cols, int64_t RB, int vec,
+    float* __restrict__ partial) {
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * RB;
+  const int64_t r1 = r0 + RB < rows ? r0 + RB : rows;
+  float* out = partial + static_cast<int64_t>(blockIdx.y) * cols;
+  if (vec) {
+    const int64_t c = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * 8;
+    if (c >= cols) return;
+    float m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int64_t r = r0;
+    for (; r + 4 <= r1; r += 4) {
+      Raw8<DT> raw[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) raw[u] = ld8<DT>(x, (r + u) * cols + c);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        float f[8];
+        cvt8<DT>(raw[u], f);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) m[k] = fmaxf(m[k], __builtin_fabsf(f[k]));
+      }
+    }
+    for (; r < r1; ++r) {
+      float f[8];
+      cvt8<DT>(ld8<DT>(x, r * cols + c), f);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) m[k] = fmaxf(m[k], __builtin_fabsf(f[k]));
+    }
+    float4* o = reinterpret_cast<float4*>(out + c);
+    o[0] = make_float4(m[0], m[1], m[2], m[3]);
+    o[1] = make_float4(m[4], m[5], m[6], m[7]);
+  } else {
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (c >= cols) return;
+    float m = 0.0f;
+    for (int64_t r = r0; r < r1; ++r) m = fmaxf(m, __builtin_fabsf(ld1<DT>(x, r * cols + c)));
+    out[c] = m;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void k_col_finalize(
+    const float* __restrict__ partial, int64_t nrb, int64_t cols, float eps,
+    float* __restrict__ inv_out, float* __restrict__ scale) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (c >= cols) return;
+  float m = 0.0f;
+  for (int64_t b = 0; b < nrb; ++b) m = fmaxf(m, partial[b * cols + c]);
+  const float inv = inv_scale(m, eps, kQmaxInt8);
+  inv_out[c] = inv;
+  scale[c] = 1.0f / inv;
+}
+
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_cast_cols(
+    const void* __restrict__ x, int64_t rows, int64_t cols, int64_t RB, int vec,
+    const float* __restrict__ inv_c, int8_t* __restrict__ q) {
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * RB;
+  const int64_t r1 = r0 + RB < rows ? r0 + RB : rows;
+  if (vec) {
+    const int64_t c = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * 8;
+    if (c >= cols) return;
+    float inv[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) inv[k] = inv_c[c + k];
+    int64_t r = r0;
+    for (; r + 4 <= r1; r += 4) {
+      Raw8<DT> raw[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) raw[u] = ld8<DT>(x, (r + u) * cols + c);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        float f[8];
+        cvt8<DT>(raw[u], f);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) f[k] *= inv[k];
+        *reinterpret_cast<uint2*>(q + (r + u) * cols + c) = pack8_int8(f, 1.0f);
+      }
+    }
+    for (; r < r1; ++r) {
+      float f[8];
+      cvt8<DT>(ld8<DT>(x, r * cols + c), f);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) f[k] *= inv[k];
+      *reinterpret_cast<uint2*>(q + r * cols + c) = pack8_int8(f, 1.0f);
+    }
+  } else {
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (c >= cols) return;
+    const float inv = inv_c[c];
+    for (int64_t r = r0; r < r1; ++r)
+      q[r * cols + c] = static_cast<int8_t>(q_int8(ld1<DT>(x, r * cols + c) * inv));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch
+// ---------------------------------------------------------------------------
+bool valid_dtype(int dt, bool allow_f32) {
+  return dt == kF16 || dt == kBF16 || (allow_f32 && dt == kF32);
+}
+
+int64_t tensor_grid(int64_t n, bool vec) {
+  const int64_t work = vec ? cdiv(n >> 3, static_cast<int64_t>(kU) * kBlock) : cdiv(n, kBlock);
+  const int64_t cap = static_cast<int64_t>(device_cus()) * kTensorWgPerCu;
+  int64_t g = work < cap ? work : cap;
+  return g < 1 ? 1 : g;
+}
+
+template <int DT>
+int tensor_quant_t(const void* x, int64_t n, float eps, uint32_t* ctl, uint8_t* q, float* scale,
+                   bool fp8, hipStream_t s) {
+  const bool vec = aligned(x, 16) && aligned(q, 8);
+  const int64_t grid = tensor_grid(n, vec);
+  k_amax_tensor<DT><<<dim3(static_cast<unsigned>(grid)), dim3(kBlock), 0, s>>>(
+      x, n, vec ? 1 : 0, ctl, eps, fp8 ? kQmaxFp8 : kQmaxInt8, scale);
+  if (fp8) {
+    k_cast_tensor<DT, true><<<dim3(static_cast<unsigned>(grid)), dim3(kBlock), 0, s>>>(
+        x, n, vec ? 1 : 0, ctl, q);
+  } else {
+    k_cast_tensor<DT, false><<<dim3(static_cast<unsigned>(grid)), dim3(kBlock), 0, s>>>(
+        x, n, vec ? 1 : 0, ctl, q);
+  }
+  return launch_status(fp8 ? "cbq_quant_fp8_tensor" : "cbq_quant_int8_tensor");
+}
+
+int tensor_quant(const void* x, int dt, int64_t n, float eps, void* ws, size_t ws_bytes,
+                 uint8_t* q, float* scale, bool fp8, hipStream_t s) {
+  const char* what = fp8 ? "cbq_quant_fp8_tensor" : "cbq_quant_int8_tensor";
+  CBQ_REQUIRE(valid_dtype(dt, !fp8), "%s: unsupported input dtype code %d", what, dt);
+  CBQ_REQUIRE(n >= 0, "%s: negative element count", what);
+  if (n == 0) return CBQ_OK;
+  CBQ_REQUIRE(x && q && scale, "%s: null pointer", what);
+  CBQ_REQUIRE(ws && ws_bytes >= CBQ_WS_CTRL_BYTES && aligned(ws, 4),
+              "%s: workspace must be >= %d bytes, 4-byte aligned", what, CBQ_WS_CTRL_BYTES);
+  uint32_t* ctl = static_cast<uint32_t*>(ws);
+  switch (dt) {
+    case kF16: return tensor_quant_t<kF16>(x, n, eps, ctl, q, scale, fp8, s);
+    case kBF16: return tensor_quant_t<kBF16>(x, n, eps, ctl, q, scale, fp8, s);
+    default: return tensor_quant_t<kF32>(x, n, eps, ctl, q, scale, fp8, s);
+  }
+}
+
+// Workgroup count for one-workgroup-per-row kernels (they stride over rows).
+unsigned wg_rows_grid(int64_t rows) {
+  const int64_t cap = 1 << 20;
+  return static_cast<unsigned>(rows < cap ? rows : cap);
+}
+
+// Rows of length L (elements) -> fastest kernel shape that fits.
+template <int DT, int LPR, int VPL>
+void launch_rows_sub(const void* x, int64_t rows, float eps, int8_t* q, float* scale,
+                     hipStream_t s) {
+  constexpr int RI = (LPR * VPL >= 64) ? 2 : 4;
+  constexpr int64_t rows_per_wg = static_cast<int64_t>(kBlock / kWave) * RI * (kWave / LPR);
+  const int64_t grid = cdiv(rows, rows_per_wg);
+  k_rows_sub<DT, LPR, VPL, RI><<<dim3(static_cast<unsigned>(grid)), dim3(kBlock), 0, s>>>(
+      x, rows, eps, q, scale);
+}
+
+template <int DT>
+int rows_quant_t(const void* x, int64_t rows, int64_t L, float eps, int8_t* q, float* scale,
+                 hipStream_t s, const char* what) {
+  CBQ_REQUIRE(rows <= 0x7fffffffLL, "%s: too many rows (%lld)", what, (long long)rows);
+  const bool vec = (L % 8 == 0) && aligned(x, 16) && aligned(q, 8);
+  if (vec) {
+    switch (L) {
+      case 8: launch_rows_sub<DT, 1, 1>(x, rows, eps, q, scale, s); return launch_status(what);
+      case 16: launch_rows_sub<DT, 2, 1>(x, rows, eps, q, scale, s); return launch_status(what);
+      case 32: launch_rows_sub<DT, 4, 1>(x, rows, eps, q, scale, s); return launch_status(what);
+      case 64: launch_rows_sub<DT, 8, 1>(x, rows, eps, q, scale, s); return launch_status(what);
+      case 128: launch_rows_sub<DT, 16, 1>(x, rows, eps, q, scale, s); return launch_status(what);
+      case 256: launch_rows_sub<DT, 32, 1>(x, rows, eps, q, scale, s); return launch_status(what);
+      case 512: launch_rows_sub<DT, 64, 1>(x, rows, eps, q, scale, s); return launch_status(what);
+      case 1024: launch_rows_sub<DT, 64, 2>(x, rows, eps, q, scale, s); return launch_status(what);
+      case 2048: launch_rows_sub<DT, 64, 4>(x, rows, eps, q, scale, s); return launch_status(what);
+      case 4096:
+        k_rows_wg<DT, 2><<<dim3(wg_rows_grid(rows)), dim3(kBlock), 0, s>>>(x, rows, eps, q, scale);
+        return launch_status(what);
+      case 8192:
+        k_rows_wg<DT, 4><<<dim3(wg_rows_grid(rows)), dim3(kBlock), 0, s>>>(x, rows, eps, q, scale);
+        return launch_status(what);
+      case 16384:
+        k_rows_wg<DT, 8><<<dim3(wg_rows_grid(rows)), dim3(kBlock), 0, s>>>(x, rows, eps, q, scale);
+        return launch_status(what);
+      default: break;
+    }
+  }
+  k_rows_generic<DT><<<dim3(wg_rows_grid(rows)), dim3(kBlock), 0, s>>>(
+      x, rows, L, vec ? 1 : 0, eps, q, scale);
+  return launch_status(what);
+}
+
+int rows_quant(const void* x, int dt, int64_t rows, int64_t L, float eps, int8_t* q, float* scale,
+               hipStream_t s, const char* what) {
+  switch (dt) {
+    case kF16: return rows_quant_t<kF16>(x, rows, L, eps, q, scale, s, what);
+    case kBF16: return rows_quant_t<kBF16>(x, rows, L, eps, q, scale, s, what);
+    default: return rows_quant_t<kF32>(x, rows, L, eps, q, scale, s, what);
+  }
+}
+
+// Column quant geometry: the row-block count depends only on the shape so
+// that the workspace size can be computed without a device.
+struct ColGeom {
+  int64_t col_blocks, nrb, RB;
+  bool vec;
+};
+
+ColGeom col_geom(int64_t rows, int64_t cols, bool vec) {
+  ColGeom g;
+  g.vec = vec;
+  g.col_blocks = vec ? cdiv(cdiv(cols, 8), kBlock) : cdiv(cols, kBlock);
+  int64_t nrb = 1024 / (g.col_blocks > 0 ? g.col_blocks : 1);
+  const int64_t max_nrb = cdiv(rows, 16);
+  if (nrb > max_nrb) nrb = max_nrb;
+  if (nrb > 65535) nrb = 65535;
+  if (nrb < 1) nrb = 1;
+  g.RB = cdiv(rows, nrb);
+  g.nrb = cdiv(rows, g.RB);
+  return g;
+}
+
+size_t col_ws_bytes(int64_t rows, int64_t cols) {
+  // The byte count does not depend on the vector path: nrb is computed for
+  // the smaller (vector) column-block count, which never yields fewer row
+  // blocks than the scalar path does.
+  const ColGeom gv = col_geom(rows, cols, true);
+  const ColGeom gs = col_geom(rows, cols, false);
+  const int64_t nrb = gv.nrb > gs.nrb ? gv.nrb : gs.nrb;
+  return CBQ_WS_CTRL_BYTES + static_cast<size_t>(nrb) * cols * 4 + static_cast<size_t>(cols) * 4;
+}
+
+template <int DT>
+int cols_quant_t(const void* x, int64_t rows, int64_t cols, float eps, void* ws, int8_t* q,
+                 float* scale, hipStream_t s) {
+  const bool vec = (cols % 8 == 0) && aligned(x, 16) && aligned(q, 8);
+  const ColGeom g = col_geom(rows, cols, vec);
+  float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + CBQ_WS_CTRL_BYTES);
+  float* inv = partial + g.nrb * cols;
+  const dim3 grid2(static_cast<unsigned>(g.col_blocks), static_cast<unsigned>(g.nrb));
+  k_colmax<DT><<<grid2, dim3(kBlock), 0, s>>>(x, rows, cols, g.RB, vec ? 1 : 0, partial);
+  k_col_finalize<<<dim3(static_cast<unsigned>(cdiv(cols, kBlock))), dim3(kBlock), 0, s>>>(
+      partial, g.nrb, cols, eps, inv, scale);
+  k_cast_cols<DT><<<grid2, dim3(kBlock), 0, s>>>(x, rows, cols, g.RB, vec ? 1 : 0, inv, q);
+  return launch_status("cbq_quant_int8_channel");
+}
+
+}  // namespace
+}  // namespace cbq
+
+using namespace cbq;
+
+extern "C" int cbq_quant_fp8_tensor(const void* x, int dtype, int64_t n, float eps, void* ws,
+                                    size_t ws_bytes, uint8_t* q, float* scale,
+                                    cbq_stream_t stream) {
+  clear_error();
+  return tensor_quant(x, dtype, n, eps, ws, ws_bytes, q, scale, true, as_stream(stream));
+}
+
+extern "C" int cbq_quant_int8_tensor(const void* x, int dtype, int64_t n, float eps, void* ws,
+                                     size_t ws_bytes, int8_t* q, float* scale,
+                                     cbq_stream_t stream) {
+  clear_error();
+  return tensor_quant(x, dtype, n, eps, ws, ws_bytes, reinterpret_cast<uint8_t*>(q), scale, false,
+                      as_stream(stream));
+}
+
+extern "C" size_t cbq_quant_int8_channel_ws_bytes(int64_t rows, int64_t cols, int axis) {
+  if (axis != 1 || rows <= 0 || cols <= 0) return CBQ_WS_CTRL_BYTES;
+  return col_ws_bytes(rows, cols);
+}
+
+extern "C" int cbq_quant_int8_channel(const void* x, int dtype, int64_t rows, int64_t cols,
+                                      int axis, float eps, void* ws, size_t ws_bytes, int8_t* q,
+                                      float* scale, cbq_stream_t stream) {
+  clear_error();
+  const char* what = "cbq_quant_int8_channel";
+  CBQ_REQUIRE(valid_dtype(dtype, true), "%s: unsupported input dtype code %d", what, dtype);
+  CBQ_REQUIRE(axis == 0 || axis == 1, "%s: axis must be 0 or 1, got %d", what, axis);
+  CBQ_REQUIRE(rows >= 0 && cols >= 0, "%s: negative shape", what);
+  if (rows == 0 || cols == 0) return CBQ_OK;
+  CBQ_REQUIRE(x && q && scale, "%s: null pointer", what);
+  if (axis == 0) return rows_quant(x, dtype, rows, cols, eps, q, scale, as_stream(stream), what);
+  const size_t need = col_ws_bytes(rows, cols);
+  CBQ_REQUIRE(ws && ws_bytes >= need && aligned(ws, 16),
+              "%s: axis 1 needs a 16-byte aligned workspace of %zu bytes, got %zu", what, need,
+              ws_bytes);
+  switch (dtype) {
+    case kF16: return cols_quant_t<kF16>(x, rows, cols, eps, ws, q, scale, as_stream(stream));
+    case kBF16: return cols_quant_t<kBF16>(x, rows, cols, eps, ws, q, scale, as_stream(stream));
+    default: return cols_quant_t<kF32>(x, rows, cols, eps, ws, q, scale, as_stream(stream));
+  }
+}
+
+extern "C" int cbq_quant_int8_group(const void* x, int dtype, int64_t num_groups,
+                                    int64_t group_size, float eps, int8_t* q, float* scale,
+                                    cbq_stream_t stream) {
+  clear_error();
+  const char* what = "cbq_quant_int8_group";
+  CBQ_REQUIRE(valid_dtype(dtype, true), "%s: unsupported input dtype code %d", what, dtype);
+  CBQ_REQUIRE(group_size > 0 && group_size <= 4096, "%s: group_size must be in (0, 4096], got %lld",
+              what, (long long)group_size);
+  CBQ_REQUIRE(num_groups >= 0, "%s: negative group count", what);
+  if (num_groups == 0) return CBQ_OK;
+  CBQ_REQUIRE(x && q && scale, "%s: null pointer", what);
+  return rows_quant(x, dtype, num_groups, group_size, eps, q, scale, as_stream(stream), what);
+}

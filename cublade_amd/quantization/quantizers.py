@@ -1,0 +1,166 @@
+"""quantize_tensor / quantize_model (reference: quantization/quantizers.py:22-224).
+
+Same signatures, registry, defaults and exception types as the reference.
+Backed by the HIP C ABI through ``cublade_amd.bindings.hip``. One extension:
+``mode="channel"`` also accepts the LAST axis as ``ch_axis`` (per-column
+scales; the reference raises NotImplementedError for every ch_axis != 0).
+"""
+from __future__ import annotations
+
+from typing import List, Optional
+
+import torch
+import torch.nn as nn
+
+from .tensor import QuantizedTensor
+from .utils import replace_linear_layers
+from cublade_amd.bindings.hip.quantize_fp8 import (
+    quantize_per_tensor_fp8 as _hip_quant_fp8_tensor,
+)
+from cublade_amd.bindings.hip.quantize_int8 import (
+    quantize_per_tensor_int8 as _hip_quant_int8_tensor,
+    quantize_per_channel_int8 as _hip_quant_int8_channel,
+    quantize_per_group_int8 as _hip_quant_int8_group,
+)
+
+# (mode, storage dtype) -> kernel wrapper (quantizers.py:22-27).
+_HIP_QUANT_KERNELS = {
+    ("tensor", torch.float8_e4m3fn): _hip_quant_fp8_tensor,
+    ("tensor", torch.int8): _hip_quant_int8_tensor,
+    ("channel", torch.int8): _hip_quant_int8_channel,
+    ("group", torch.int8): _hip_quant_int8_group,
+}
+# Reference name of the same table.
+_CUDA_QUANT_KERNELS = _HIP_QUANT_KERNELS
+
+# Accepted input dtypes per (mode, dtype) (quantizers.py:32-37): FP8 takes
+# fp16/bf16; INT8 also takes fp32 (nn.Linear weights default to fp32).
+_ALLOWED_INPUT_DTYPES = {
+    ("tensor", torch.float8_e4m3fn): {torch.float16, torch.bfloat16},
+    ("tensor", torch.int8): {torch.float16, torch.bfloat16, torch.float32},
+    ("channel", torch.int8): {torch.float16, torch.bfloat16, torch.float32},
+    ("group", torch.int8): {torch.float16, torch.bfloat16, torch.float32},
+}
+
+
+def _require_cuda_input(x: torch.Tensor, key, *, what: str) -> None:
+    """Device / layout / dtype checks (quantizers.py:40-50). On ROCm a HIP
+    tensor reports ``is_cuda``."""
+    if not x.is_cuda:
+        raise ValueError(f"{what}: tensor must be on CUDA, got device={x.device}")
+    if not x.is_contiguous():
+        raise ValueError(f"{what}: tensor must be contiguous")
+    allowed = _ALLOWED_INPUT_DTYPES[key]
+    if x.dtype not in allowed:
+        names = sorted(str(d) for d in allowed)
+        raise ValueError(f"{what}: tensor dtype must be one of {names}, got {x.dtype}")
+
+
+def _zero_scalar(device: torch.device) -> torch.Tensor:
+    return torch.zeros((), dtype=torch.float32, device=device)
+
+
+def channel_kernel_axis(ndim: int, ch_axis: int) -> int:
+    """Map a user ``ch_axis`` to the channel kernel's axis: 0 -> one scale per
+    row of the (size(0), numel/size(0)) view; the last axis of an N-D tensor
+    (N >= 2) -> one scale per column of the (numel/F, F) view."""
+    ax = ch_axis + ndim if ch_axis < 0 else ch_axis
+    if ax == 0:
+        return 0
+    if ndim >= 2 and ax == ndim - 1:
+        return 1
+    raise NotImplementedError(
+        "INT8 channel quant requires ch_axis=0 or the last axis; got ch_axis=" + str(ch_axis)
+    )
+
+
+def quantize_tensor(
+    x: torch.Tensor,
+    scheme: str = "symmetric",
+    dtype: torch.dtype = torch.int8,
+    mode: str = "tensor",
+    group_size: int = 32,
+    ch_axis: int = 0,
+    eps: float = 1e-12,
+) -> QuantizedTensor:
+    """Quantize ``x`` per tensor, channel or group (symmetric only).
+
+    x must be a contiguous CUDA (HIP) tensor: fp16 / bf16 for FP8, fp16 /
+    bf16 / fp32 for INT8. FP8 supports mode "tensor" only. Returns a
+    QuantizedTensor with a 0-d fp32 zero point.
+    """
+    if scheme != "symmetric":
+        raise NotImplementedError(
+            f"quantize_tensor: only scheme='symmetric' is supported, got '{scheme}'"
+        )
+    key = (mode, dtype)
+    kernel = _HIP_QUANT_KERNELS.get(key)
+    if kernel is None:
+        raise ValueError(f"No quant kernel registered for mode='{mode}', dtype={dtype}")
+    _require_cuda_input(x, key, what="quantize_tensor")
+
+    if mode == "tensor":
+        q, scale = kernel(x, eps)
+    elif mode == "channel":
+        axis = channel_kernel_axis(x.dim(), ch_axis)
+        if axis == 0:
+            q, scale = kernel(x, eps)
+        else:
+            F = x.shape[-1]
+            q2, scale = kernel(x.view(-1, F), eps, axis=1)
+            q = q2.view(x.shape)
+    elif mode == "group":
+        moved = x.movedim(ch_axis, -1).contiguous()
+        lead, F = moved.shape[:-1], moved.shape[-1]
+        if F % group_size != 0:
+            raise ValueError(f"group_size {group_size} must evenly divide axis length {F}")
+        q_grouped, scale = kernel(moved.view(-1, group_size), group_size, eps)
+        q = q_grouped.view(*lead, F).movedim(-1, ch_axis).contiguous()
+    else:
+        raise ValueError(f"Unsupported mode '{mode}'; expected tensor / channel / group")
+
+    return QuantizedTensor(q, scale, _zero_scalar(x.device), mode, ch_axis, group_size, dtype,
+                           x.dtype)
+
+
+QUANT_LAYER_REGISTRY = {}
+
+
+def _init_registry():
+    """Filled lazily (the layer module imports this one)."""
+    if not QUANT_LAYER_REGISTRY:
+        from .linear import cuBladeW8A16LinearLayer
+        QUANT_LAYER_REGISTRY["w8a16"] = cuBladeW8A16LinearLayer
+
+
+def quantize_model(
+    model: nn.Module,
+    quant_type: str = "w8a16",
+    target_modules: Optional[List[str]] = None,
+    exclude_modules: Optional[List[str]] = None,
+    inplace: bool = True,
+    **quant_kwargs,
+):
+    """Replace the model's nn.Linear layers with quantized layers
+    (reference: quantizers.py:152-224).
+
+    quant_type: "w8a16" (INT8 per-output-channel weights, 16-bit activations).
+    target_modules / exclude_modules: substring filters on dotted names.
+    inplace=False quantizes a deep copy. quant_kwargs go to the layer
+    (handle_outliers, outlier_threshold). Returns the (possibly copied) model.
+    """
+    _init_registry()
+    if quant_type not in QUANT_LAYER_REGISTRY:
+        available = ", ".join(QUANT_LAYER_REGISTRY.keys())
+        raise ValueError(f"Unknown quant_type '{quant_type}'. Available: {available}")
+    if not inplace:
+        from copy import deepcopy
+        model = deepcopy(model)
+    replace_linear_layers(
+        model,
+        target_class=QUANT_LAYER_REGISTRY[quant_type],
+        target_modules=target_modules,
+        exclude_modules=exclude_modules,
+        quant_kwargs=quant_kwargs,
+    )
+    return model

@@ -1,0 +1,157 @@
+/*
+ * cublade_quant.h - C ABI of the MI355X (gfx950) quantization library
+ * libcublade_quant.so.
+ *
+ * Every entry point takes raw device pointers, element counts, dtype codes and
+ * a HIP stream, launches asynchronously on that stream, and returns a status
+ * code (CBQ_OK on success). No entry point allocates, frees or synchronises:
+ * the caller owns every buffer, including the workspace. On failure
+ * cbq_last_error() returns a thread-local message.
+ *
+ * Each function names the reference interface it replaces (paths relative to
+ * the cuBlade source tree, package `cublade`). The reference's pybind entry
+ * points allocate their outputs and launch on the legacy default stream; here
+ * the caller allocates and chooses the stream.
+ *
+ * Numerics (all bit-exact restatements of the reference kernels):
+ *   amax  = max |x| (NaN inputs ignored), per tensor / row / column / group
+ *   inv   = fp32(Q / max(amax, eps))     Q = 448 (FP8 E4M3) or 127 (INT8),
+ *                                        IEEE correctly rounded division
+ *   q     = FP8:  e4m3fn(x * inv), round-to-nearest-even, saturated to +-448
+ *           INT8: clamp(round_half_even(x * inv), -127, 127), NaN -> 0
+ *   scale = fp32(1 / inv)
+ *   dequant y = T(float(q) * scale), round-to-nearest-even to fp16 / bf16
+ */
+#ifndef CUBLADE_QUANT_H
+#define CUBLADE_QUANT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* A hipStream_t passed as an opaque pointer (NULL = the null stream). */
+typedef void* cbq_stream_t;
+
+/* Floating-point dtype codes for activations, inputs and outputs. */
+enum { CBQ_F32 = 0, CBQ_F16 = 1, CBQ_BF16 = 2 };
+
+/* Status codes. */
+enum { CBQ_OK = 0, CBQ_EINVAL = 1, CBQ_ELAUNCH = 2 };
+
+/* Workspace contract.  Entry points that take (ws, ws_bytes) use the first
+ * CBQ_WS_CTRL_BYTES bytes as a control block of counters that must be
+ * zero-filled before the first call and that every call leaves zero-filled
+ * again; the rest is per-call scratch. One workspace serves one stream at a
+ * time: calls that overlap in time must not share it. */
+#define CBQ_WS_CTRL_BYTES 256
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* cbq_last_error(void);
+
+/* ABI version (major * 100 + minor). */
+int cbq_abi_version(void);
+
+/* Workspace bytes needed by cbq_quant_int8_channel (axis 1 needs per-column
+ * partial maxima; axis 0 needs only the control block). */
+size_t cbq_quant_int8_channel_ws_bytes(int64_t rows, int64_t cols, int axis);
+
+/* ---- FP8 E4M3 per tensor ------------------------------------------------ */
+
+/* Replaces quantize_per_tensor_fp8_cuda (kernels/cuda/quantization/
+ * quantize_per_tensor_fp8.cu:162-182; kernels :38-132), bound as
+ * cublade.bindings.cuda.quantize_fp8.quantize_per_tensor_fp8
+ * (bindings/cuda/quantize_fp8.py:15-34).
+ * x: n elements of dtype CBQ_F16 or CBQ_BF16. q: n FP8 E4M3 codes.
+ * scale: one fp32, written when n > 0. ws: >= CBQ_WS_CTRL_BYTES. */
+int cbq_quant_fp8_tensor(const void* x, int dtype, int64_t n, float eps,
+                         void* ws, size_t ws_bytes, uint8_t* q, float* scale,
+                         cbq_stream_t stream);
+
+/* Replaces dequantize_per_tensor_fp8_cuda (dequantize_per_tensor_fp8.cu:84-109;
+ * kernel :23-66), bound as dequantize_fp8.dequantize_per_tensor_fp8
+ * (bindings/cuda/dequantize_fp8.py:15-35). out_dtype: CBQ_F16 or CBQ_BF16. */
+int cbq_dequant_fp8_tensor(const uint8_t* q, const float* scale, int64_t n,
+                           void* y, int out_dtype, cbq_stream_t stream);
+
+/* ---- INT8 --------------------------------------------------------------- */
+
+/* Replaces quantize_per_tensor_int8_cuda (quantize_int8.cu:470-484; kernels
+ * :47-166), bound as quantize_int8.quantize_per_tensor_int8
+ * (bindings/cuda/quantize_int8.py:18-38). dtype: CBQ_F32/F16/BF16. */
+int cbq_quant_int8_tensor(const void* x, int dtype, int64_t n, float eps,
+                          void* ws, size_t ws_bytes, int8_t* q, float* scale,
+                          cbq_stream_t stream);
+
+/* Replaces quantize_per_channel_int8_cuda (quantize_int8.cu:487-509; kernels
+ * :173-297), bound as quantize_int8.quantize_per_channel_int8
+ * (bindings/cuda/quantize_int8.py:41-62). x is viewed as rows x cols.
+ * axis 0: one scale per row (the reference's only axis); axis 1: one scale per
+ * column (an extension: same math with the maximum taken over rows).
+ * Unlike the reference, cols need not be a multiple of 16 / element size. */
+int cbq_quant_int8_channel(const void* x, int dtype, int64_t rows, int64_t cols,
+                           int axis, float eps, void* ws, size_t ws_bytes,
+                           int8_t* q, float* scale, cbq_stream_t stream);
+
+/* Replaces quantize_per_group_int8_cuda (quantize_int8.cu:514-536; kernels
+ * :307-371), bound as quantize_int8.quantize_per_group_int8
+ * (bindings/cuda/quantize_int8.py:65-87). x: num_groups x group_size,
+ * 0 < group_size <= 4096. scale: num_groups fp32. */
+int cbq_quant_int8_group(const void* x, int dtype, int64_t num_groups,
+                         int64_t group_size, float eps, int8_t* q, float* scale,
+                         cbq_stream_t stream);
+
+/* Replaces dequantize_per_tensor_int8_cuda (dequantize_int8.cu:210-225; kernel
+ * :29-64), bound as dequantize_int8.dequantize_per_tensor_int8
+ * (bindings/cuda/dequantize_int8.py:18-38). */
+int cbq_dequant_int8_tensor(const int8_t* q, const float* scale, int64_t n,
+                            void* y, int out_dtype, cbq_stream_t stream);
+
+/* Replaces dequantize_per_channel_int8_cuda (dequantize_int8.cu:227-247;
+ * kernel :70-109), bound as dequantize_int8.dequantize_per_channel_int8
+ * (bindings/cuda/dequantize_int8.py:41-58). axis 0: scale[rows];
+ * axis 1 (extension): scale[cols]. */
+int cbq_dequant_int8_channel(const int8_t* q, const float* scale, int64_t rows,
+                             int64_t cols, int axis, void* y, int out_dtype,
+                             cbq_stream_t stream);
+
+/* Replaces dequantize_per_group_int8_cuda (dequantize_int8.cu:249-273; kernel
+ * :118-134), bound as dequantize_int8.dequantize_per_group_int8
+ * (bindings/cuda/dequantize_int8.py:61-79). */
+int cbq_dequant_int8_group(const int8_t* q, const float* scale,
+                           int64_t num_groups, int64_t group_size, void* y,
+                           int out_dtype, cbq_stream_t stream);
+
+/* ---- W8A16 linear ------------------------------------------------------- */
+
+/* Workspace bytes needed by cbq_w8a16_linear for this shape. */
+size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_out);
+
+/* Replaces the forward chain of cuBladeW8A16LinearLayer
+ * (quantization/linear.py:83-137): int8 -> activation copy of the weight
+ * (:105, :123), the Triton GEMM bindings/triton/matmul.py:17-132 (kernel
+ * kernels/triton/matmul_kernel.py:9-99), the per-channel scale multiply
+ * (:113, :131), the outlier side-GEMM (:116-120) and the bias add (:134-135),
+ * in one launch:
+ *   y[m,n] = T( s[n] * sum_k x[m,k] * wq[n,k]
+ *               + sum_j x[m, outlier_cols[j]] * w_out[n,j] + bias[n] )
+ * with fp32 accumulation and one final round-to-nearest-even to T.
+ * x: [M,K] and y: [M,N] in act_dtype, row-major. CBQ_F16 / CBQ_BF16 run
+ * on MFMA; CBQ_F32 (the reference's fp32 Triton path) runs a general kernel.
+ * wq: int8 [N,K] row-major; its outlier columns hold 0.
+ * scales, bias (nullable): [N] act_dtype. outlier_cols: n_out int64 indices in
+ * [0, K) (nullable when n_out == 0); w_out: [N, n_out] act_dtype.
+ * ws: cbq_w8a16_ws_bytes(...) bytes, control block zeroed. */
+int cbq_w8a16_linear(const void* x, int act_dtype, const int8_t* wq,
+                     const void* scales, const void* bias,
+                     const int64_t* outlier_cols, int64_t n_out,
+                     const void* w_out, int64_t M, int64_t N, int64_t K,
+                     void* ws, size_t ws_bytes, void* y, cbq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CUBLADE_QUANT_H */

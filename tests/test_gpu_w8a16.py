@@ -1,0 +1,259 @@
+"""GPU parity of the W8A16 linear (HIP C ABI via the binding and the layer)
+against the oracle's exact-accumulation W8A16 (float64) and the golden
+vectors. Gate (north star): rtol 1e-2 / atol 1e-2.
+
+Covers the MFMA path (fp16 / bf16, M / N / K tails), the general path (fp32
+activations, K not a multiple of 16, unaligned activations), bias, the
+outlier side-GEMM, quantize_model on an MLP, state_dict round trips (own and
+reference compact layout) and the BASELINE config-5 shapes (row subsets
+against the oracle, full output against a GPU fp32 matmul of the same
+operands).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+import oracle
+from tests import _golden as G
+from tests._util import CODE_OF, DTYPE_OF, bits, from_bits
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = dict(rtol=1e-2, atol=1e-2)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _loaded():
+    from cublade_amd import _abi
+    _abi.lib()
+
+
+def w8a16(*args, **kw):
+    from cublade_amd.bindings.hip import w8a16_linear
+    return w8a16_linear(*args, **kw)
+
+
+def expand_compact(wq_c: np.ndarray, normal_cols, K: int) -> np.ndarray:
+    full = np.zeros((wq_c.shape[0], K), np.int8)
+    full[:, normal_cols] = wq_c
+    return full
+
+
+def oracle_y(x, code, wq_full, scales, bias=None, oc=None, w_out=None, rows=None):
+    """Oracle on the full-K weight (outlier columns are zero in wq_full)."""
+    return oracle.w8a16_linear(x, code, wq_full, scales, bias=bias,
+                               outlier_cols=None if oc is None else np.asarray(oc, np.int64),
+                               w_out=w_out, rows=rows)
+
+
+def make_case(M, K, N, dt, seed, bias=False, n_out=0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    oc = sorted(torch.randperm(K, generator=g)[:n_out].tolist()) if n_out else []
+    w = 0.02 * torch.randn(N, K, generator=g)
+    if oc:
+        x[:, oc] = 10.0 * torch.sign(torch.randn(M, len(oc), generator=g))
+        w[:, oc] *= 400.0
+    wn = w.clone()
+    if oc:
+        wn[:, oc] = 0
+    amax = wn.abs().amax(dim=1)
+    inv = torch.tensor(127.0) / torch.clamp(amax, min=1e-12)
+    wq = torch.round(wn * inv[:, None]).clamp(-127, 127).to(torch.int8)
+    s = (1.0 / inv).to(dt)
+    b = (0.1 * torch.randn(N, generator=g)).to(dt) if bias else None
+    w_out = w[:, oc].to(dt) if oc else None
+    return x.to(dt), wq, s, b, oc, w_out
+
+
+def run_and_check(M, K, N, dt, seed, bias=False, n_out=0, rows=None, x_offset=0):
+    x, wq, s, b, oc, w_out = make_case(M, K, N, dt, seed, bias, n_out)
+    code = CODE_OF[dt]
+    if x_offset:
+        xbuf = torch.zeros(M * K + x_offset, dtype=dt, device=DEV)
+        xbuf[x_offset:] = x.reshape(-1).to(DEV)
+        xd = xbuf[x_offset:].view(M, K)
+    else:
+        xd = x.to(DEV)
+    y = w8a16(xd, wq.to(DEV), s.to(DEV), None if b is None else b.to(DEV),
+              torch.tensor(oc, dtype=torch.int64, device=DEV) if oc else None,
+              None if w_out is None else w_out.to(DEV))
+    assert y.dtype == dt and tuple(y.shape) == (M, N)
+    r = None if rows is None else np.asarray(rows, np.int64)
+    ref = oracle_y(bits(x), code, wq.numpy(), bits(s), None if b is None else bits(b),
+                   oc or None, None if w_out is None else bits(w_out), rows=r)
+    got = y.float().cpu().numpy()
+    if r is not None:
+        got = got[r]
+    np.testing.assert_allclose(got, ref, **TOL)
+    return y
+
+
+@pytest.mark.parametrize("meta,arr", G.cases("w8a16"), ids=G.ids("w8a16"))
+def test_golden(meta, arr):
+    M, K, N = meta["shape"]
+    dt = DTYPE_OF[meta["dtype"]]
+    wq = arr["wq"]
+    oc = arr.get("outlier_cols")
+    if oc is not None:
+        wq = expand_compact(wq, arr["normal_cols"], K)
+    y = w8a16(from_bits(arr["x"].reshape(-1), meta["dtype"], DEV).view(M, K),
+              torch.from_numpy(wq).to(DEV),
+              from_bits(arr["scales"], meta["dtype"], DEV),
+              None if "bias" not in arr else from_bits(arr["bias"], meta["dtype"], DEV),
+              None if oc is None else torch.from_numpy(oc).to(DEV),
+              None if oc is None else from_bits(arr["w_out"].reshape(-1), meta["dtype"],
+                                                DEV).view(N, len(oc)))
+    np.testing.assert_allclose(y.float().cpu().numpy(), arr["y"], **TOL)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,K,N", [(1, 64, 48), (16, 128, 128), (100, 96, 200),
+                                   (128, 256, 128), (129, 80, 130), (256, 512, 384),
+                                   (7, 4096, 96), (300, 160, 257)])
+def test_mfma_shapes(dt, M, K, N):
+    run_and_check(M, K, N, dt, seed=M * 31 + K + N, bias=(M % 2 == 1))
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_outlier_side_gemm(dt):
+    run_and_check(64, 256, 96, dt, seed=5, bias=True, n_out=6)
+    run_and_check(130, 512, 200, dt, seed=6, bias=False, n_out=17)
+
+
+@pytest.mark.parametrize("M,K,N", [(5, 100, 40), (33, 24, 17)])
+def test_general_path_odd_k(M, K, N):
+    run_and_check(M, K, N, torch.float16, seed=K, bias=True)
+    run_and_check(M, K, N, torch.bfloat16, seed=K + 1, n_out=3)
+
+
+def test_general_path_fp32_and_unaligned():
+    run_and_check(20, 128, 64, torch.float32, seed=2, bias=True, n_out=2)
+    run_and_check(40, 256, 72, torch.float16, seed=3, bias=True, x_offset=3)
+
+
+def test_mfma_bit_stability_across_calls():
+    """Same inputs, same outputs, bit for bit (fixed accumulation order)."""
+    x, wq, s, b, _, _ = make_case(256, 1024, 512, torch.float16, 8, bias=True)
+    args = (x.to(DEV), wq.to(DEV), s.to(DEV), b.to(DEV))
+    y0 = w8a16(*args)
+    for _ in range(3):
+        assert torch.equal(w8a16(*args), y0)
+
+
+@pytest.mark.parametrize("M", [16, 256, 4096])
+def test_config5_shapes(M):
+    """x [M, 4096] N(0,1) with 6 feature columns at
+    magnitude U(8, 20); W [11008, 4096] ~ N(0, 0.02) quantized per channel
+    (fp16 scales)."""
+    from cublade_amd.quantization import cuBladeW8A16LinearLayer
+    g = torch.Generator().manual_seed(4)
+    K, N = 4096, 11008
+    x = torch.randn(M, K, generator=g)
+    oc = torch.sort(torch.randperm(K, generator=g)[:6]).values
+    mag = 8.0 + 12.0 * torch.rand(M, 6, generator=g)
+    x[:, oc] = torch.sign(torch.randn(M, 6, generator=g)) * mag
+    x = x.half()
+    w = (0.02 * torch.randn(N, K, generator=g)).half()
+    layer = cuBladeW8A16LinearLayer(K, N, bias=False, dtype=torch.float16).to(DEV)
+    layer.quantize(w.to(DEV))
+    assert layer.int8_weights.is_cuda and layer.scales.dtype == torch.float16
+    y = layer(x.to(DEV))
+    rows = np.arange(M) if M <= 16 else np.array([0, 1, M // 2, M - 1], np.int64)
+    ref = oracle_y(bits(x), oracle.F16, bits(layer.int8_weights), bits(layer.scales),
+                   rows=rows)
+    np.testing.assert_allclose(y.float().cpu().numpy()[rows], ref, **TOL)
+    # whole output against a GPU fp32 product of the same operands
+    wf = layer.int8_weights.float() * layer.scales.float()[:, None]
+    ref_full = x.to(DEV).float() @ wf.t().contiguous()
+    torch.testing.assert_close(y.float(), ref_full, **TOL)
+
+
+def test_layer_outlier_mode_and_state_dict():
+    from cublade_amd.quantization import cuBladeW8A16LinearLayer
+    g = torch.Generator().manual_seed(12)
+    K, N, M = 256, 128, 48
+    w = 0.02 * torch.randn(N, K, generator=g)
+    oc = [5, 77, 200]
+    w[3, oc] = torch.tensor([7.5, -9.0, 6.5])
+    w = w.half()
+    layer = cuBladeW8A16LinearLayer(K, N, bias=True, dtype=torch.float16, handle_outliers=True)
+    layer.quantize(w.to(DEV))
+    assert layer.outlier_cols.tolist() == oc
+    assert layer.int8_weights.shape == (N, K)
+    assert torch.count_nonzero(layer.int8_weights[:, oc]).item() == 0
+    layer.bias.data = (0.1 * torch.randn(N, generator=g)).half().to(DEV)
+    x = torch.randn(M, K, generator=g).half()
+    x[:, oc] = 12.0
+    y = layer(x.to(DEV))
+    ref = oracle_y(bits(x), oracle.F16, bits(layer.int8_weights), bits(layer.scales),
+                   bias=bits(layer.bias), oc=oc, w_out=bits(layer.outlier_weights))
+    np.testing.assert_allclose(y.float().cpu().numpy(), ref, **TOL)
+    # scales come from the normal columns only, as in the reference
+    normal = [c for c in range(K) if c not in oc]
+    amax = w.float()[:, normal].abs().amax(dim=1)
+    inv = torch.tensor(127.0) / amax
+    assert torch.equal(layer.scales.cpu(), (1.0 / inv).half())
+    # CPU forward (reference CPU branch) agrees
+    cpu = cuBladeW8A16LinearLayer(K, N, bias=True, dtype=torch.float16, handle_outliers=True)
+    cpu.load_state_dict({k: v.cpu() for k, v in layer.state_dict().items()})
+    y_cpu = cpu(x.float()).float().numpy()
+    np.testing.assert_allclose(y_cpu, ref, **TOL)
+    # reference compact layout [N, K - n_out] loads and gives the same output
+    sd = {k: v.cpu() for k, v in layer.state_dict().items()}
+    sd["int8_weights"] = sd["int8_weights"][:, normal].contiguous()
+    fresh = cuBladeW8A16LinearLayer(K, N, bias=True, dtype=torch.float16, handle_outliers=True)
+    fresh.load_state_dict(sd)
+    fresh = fresh.to(DEV)
+    assert torch.equal(fresh.int8_weights, layer.int8_weights)
+    assert torch.equal(fresh(x.to(DEV)), y)
+
+
+def test_quantize_model_mlp():
+    from cublade_amd.quantization import cuBladeW8A16LinearLayer, quantize_model
+    torch.manual_seed(42)
+    model = nn.Sequential(nn.Linear(128, 256), nn.ReLU(), nn.Linear(256, 128), nn.ReLU(),
+                          nn.Linear(128, 10)).half().to(DEV)
+    x = torch.randn(32, 128).half().to(DEV)
+    with torch.no_grad():
+        y_fp = model(x).float()
+    qm = quantize_model(model, "w8a16", exclude_modules=["4"], inplace=False)
+    assert isinstance(qm[0], cuBladeW8A16LinearLayer) and isinstance(qm[2], cuBladeW8A16LinearLayer)
+    assert isinstance(qm[4], nn.Linear)
+    assert isinstance(model[0], nn.Linear)   # inplace=False left the original
+    with torch.no_grad():
+        y_q = qm(x).float()
+    err = (y_q - y_fp).abs()
+    assert err.max().item() < 0.05 and (err ** 2).mean().item() < 1e-4
+    # layer 0 alone against the oracle
+    with torch.no_grad():
+        y0 = qm[0](x)
+    ref = oracle_y(bits(x), oracle.F16, bits(qm[0].int8_weights), bits(qm[0].scales),
+                   bias=bits(qm[0].bias))
+    np.testing.assert_allclose(y0.float().cpu().numpy(), ref, **TOL)
+
+
+def test_toy_flow_cpu_model():
+    """The reference toy demo flow (examples/quantization/w8a16_toy_model.py):
+    an fp32 MLP on the CPU is quantized (kernels on the GPU), buffers stay on
+    the CPU, and the CPU forward follows the reference CPU branch."""
+    from cublade_amd.quantization import quantize_model
+    torch.manual_seed(42)
+    model = nn.Sequential(nn.Linear(128, 256), nn.ReLU(), nn.Linear(256, 128), nn.ReLU(),
+                          nn.Linear(128, 10))
+    x = torch.randn(4, 128)
+    with torch.no_grad():
+        y_fp = model(x)
+    qm = quantize_model(model, "w8a16", inplace=False)
+    assert not qm[0].int8_weights.is_cuda and qm[0].scales.dtype == torch.float32
+    with torch.no_grad():
+        y_q = qm(x)
+    assert ((y_q - y_fp) ** 2).mean().item() < 0.01 and (y_q - y_fp).abs().max().item() < 0.5
+    # the same model on the GPU (fp32 activations: general path) agrees
+    qg = qm.to(DEV)
+    with torch.no_grad():
+        y_g = qg(x.to(DEV)).cpu()
+    torch.testing.assert_close(y_g, y_q, rtol=1e-4, atol=1e-4)

@@ -1,0 +1,224 @@
+"""Host-side tests (no GPU): the C-ABI library loads and exports every
+declared symbol, its argument validation fails before any device work, the
+loader memoises failures, and the Python layer's host logic (checks, outlier
+utilities, layer replacement, CPU branch, state_dict layouts) behaves like
+the reference's."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+import oracle
+from tests._util import bits
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _lib():
+    from cublade_amd import _abi
+    return _abi.lib()
+
+
+def declared_symbols():
+    text = (ROOT / "include" / "cublade_quant.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(cbq_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib()
+    names = declared_symbols()
+    assert len(names) == 13
+    for n in names:
+        assert hasattr(L, n), n
+    from cublade_amd import _abi
+    assert set(names) == set(_abi.SIGNATURES)
+
+
+def test_abi_version_and_error_slot():
+    L = _lib()
+    assert L.cbq_abi_version() == 100
+    assert L.cbq_last_error() in (b"",) or isinstance(L.cbq_last_error(), bytes)
+
+
+def _einval(rc, needle):
+    L = _lib()
+    assert rc == 1
+    assert needle in L.cbq_last_error().decode()
+
+
+def test_abi_rejects_bad_arguments_without_device_work():
+    L = _lib()
+    P = ctypes.c_void_p
+    fake = P(0x1000)
+    _einval(L.cbq_quant_fp8_tensor(fake, 0, 16, 1e-12, fake, 256, fake, fake, None), "dtype")
+    _einval(L.cbq_quant_int8_tensor(fake, 1, 16, 1e-12, fake, 8, fake, fake, None), "workspace")
+    _einval(L.cbq_quant_int8_group(fake, 2, 4, 0, 1e-12, fake, fake, None), "group_size")
+    _einval(L.cbq_quant_int8_group(fake, 2, 4, 4097, 1e-12, fake, fake, None), "group_size")
+    _einval(L.cbq_quant_int8_channel(fake, 2, 4, 4, 2, 1e-12, fake, 256, fake, fake, None), "axis")
+    _einval(L.cbq_quant_int8_channel(fake, 2, 64, 64, 1, 1e-12, fake, 256, fake, fake, None),
+            "workspace")
+    _einval(L.cbq_dequant_fp8_tensor(fake, fake, 16, fake, 0, None), "out_dtype")
+    _einval(L.cbq_dequant_int8_group(fake, fake, 4, 8, fake, 3, None), "out_dtype")
+    _einval(L.cbq_dequant_int8_channel(fake, fake, 4, 8, 5, fake, 1, None), "axis")
+    _einval(L.cbq_w8a16_linear(fake, 7, fake, fake, None, None, 0, None, 4, 4, 4, fake, 256,
+                               fake, None), "activation dtype")
+    _einval(L.cbq_w8a16_linear(fake, 1, fake, fake, None, None, 2, None, 4, 4, 4, fake, 256,
+                               fake, None), "outlier")
+    _einval(L.cbq_quant_int8_tensor(None, 1, 16, 1e-12, fake, 256, fake, fake, None), "null")
+    # empty inputs are a successful no-op (nothing is dereferenced)
+    assert L.cbq_quant_fp8_tensor(None, 1, 0, 1e-12, None, 0, None, None, None) == 0
+    assert L.cbq_quant_int8_group(None, 1, 0, 32, 1e-12, None, None, None) == 0
+    assert L.cbq_w8a16_linear(None, 1, None, None, None, None, 0, None, 0, 8, 8, None, 0,
+                              None, None) == 0
+
+
+def test_workspace_sizes():
+    L = _lib()
+    assert L.cbq_quant_int8_channel_ws_bytes(100, 100, 0) == 256
+    big = L.cbq_quant_int8_channel_ws_bytes(28672, 8192, 1)
+    assert big >= 256 + 8192 * 4 * 2 and big < 64 << 20
+    assert L.cbq_w8a16_ws_bytes(16, 11008, 4096, 0) >= 256
+
+
+def test_loader_memoises_failures(tmp_path):
+    from cublade_amd import _loader
+    bad = tmp_path / "bad.hip"
+    bad.write_text("this is not C++\n")
+    name = "cbq_test_bad_module"
+    with pytest.raises(RuntimeError, match="hipcc failed"):
+        _loader.load_hip_module(name, [bad])
+    assert _loader.load_error(name) is not None and not _loader.is_loaded(name)
+    with pytest.raises(RuntimeError, match="failed to compile earlier"):
+        _loader.load_hip_module(name, [bad])
+    assert _loader.load_cuda_module is _loader.load_hip_module
+    assert _loader.is_loaded("cublade_quant") or _lib() is not None
+
+
+def test_quantize_tensor_host_checks():
+    from cublade_amd.quantization import quantize_tensor, dequantize_tensor, QuantizedTensor
+    x = torch.randn(8, 16)
+    with pytest.raises(NotImplementedError):
+        quantize_tensor(x, scheme="asymmetric")
+    with pytest.raises(ValueError, match="No quant kernel"):
+        quantize_tensor(x, dtype=torch.float8_e4m3fn, mode="group")
+    with pytest.raises(ValueError, match="must be on CUDA"):
+        quantize_tensor(x)
+    qt = QuantizedTensor(torch.zeros(4, dtype=torch.int8), torch.ones(()), torch.zeros(()),
+                         "tensor", 0, 32, torch.int8, torch.bfloat16)
+    with pytest.raises(ValueError, match="must be on CUDA"):
+        dequantize_tensor(qt)
+
+
+def test_channel_axis_mapping():
+    from cublade_amd.quantization.quantizers import channel_kernel_axis
+    assert channel_kernel_axis(2, 0) == 0 and channel_kernel_axis(2, 1) == 1
+    assert channel_kernel_axis(2, -1) == 1 and channel_kernel_axis(3, -1) == 1
+    assert channel_kernel_axis(1, 0) == 0 and channel_kernel_axis(1, -1) == 0
+    with pytest.raises(NotImplementedError):
+        channel_kernel_axis(3, 1)
+
+
+def test_outlier_utils_match_definition():
+    from cublade_amd.quantization import (detect_outlier_columns, separate_outliers,
+                                          split_weights_by_outliers)
+    w = torch.zeros(4, 10)
+    w[1, 3] = 6.5
+    w[2, 7] = -7.0
+    w[0, 5] = 6.0            # not > threshold
+    w[3, 9] = float("nan")   # NaN never counts
+    assert detect_outlier_columns(w, 6.0) == [3, 7]
+    wn, wo, nc, oc = split_weights_by_outliers(w, [7, 3])
+    assert nc == [0, 1, 2, 4, 5, 6, 8, 9] and oc == [7, 3]
+    assert torch.equal(wo, w[:, [7, 3]], ) and wn.shape == (4, 8)
+    wn, wo, nc, oc = separate_outliers(w, 6.0)
+    assert oc == [3, 7] and wo.shape == (4, 2)
+
+
+def test_replace_linear_layers_filters():
+    from cublade_amd.quantization import replace_linear_layers
+
+    class Fake(nn.Module):
+        def __init__(self, in_f, out_f, bias=True, dtype=torch.float32, **kw):
+            super().__init__()
+            self.shape, self.kw, self.dtype_ = (in_f, out_f), kw, dtype
+            self.bias = None
+            self.got = None
+
+        def quantize(self, w):
+            self.got = w
+
+    model = nn.Sequential()
+    model.add_module("q_proj", nn.Linear(4, 8))
+    model.add_module("k_proj", nn.Linear(4, 8, bias=False))
+    inner = nn.Sequential()
+    inner.add_module("lm_head", nn.Linear(8, 3))
+    inner.add_module("v_proj", nn.Linear(8, 3).half())
+    model.add_module("inner", inner)
+    replace_linear_layers(model, Fake, target_modules=["proj"], exclude_modules=["k_"],
+                          quant_kwargs={"handle_outliers": True})
+    assert isinstance(model.q_proj, Fake) and model.q_proj.kw == {"handle_outliers": True}
+    assert isinstance(model.k_proj, nn.Linear)
+    assert isinstance(model.inner.lm_head, nn.Linear)
+    assert isinstance(model.inner.v_proj, Fake) and model.inner.v_proj.dtype_ == torch.float16
+    assert model.q_proj.got is not None and model.q_proj.bias is not None
+
+
+def _cpu_layer(K, N, dt, bias, seed, outliers=()):
+    from cublade_amd.quantization import cuBladeW8A16LinearLayer
+    g = torch.Generator().manual_seed(seed)
+    layer = cuBladeW8A16LinearLayer(K, N, bias=bias, dtype=dt, handle_outliers=bool(outliers))
+    wq = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    oc = list(outliers)
+    if oc:
+        wq[:, oc] = 0
+        layer.outlier_cols = torch.tensor(oc, dtype=torch.long)
+        layer.normal_cols = torch.tensor([c for c in range(K) if c not in oc], dtype=torch.long)
+        layer.outlier_weights = (0.5 * torch.randn(N, len(oc), generator=g)).to(dt)
+    layer.int8_weights = wq
+    layer.scales = (torch.rand(N, generator=g) * 0.01).to(dt)
+    if bias:
+        layer.bias.data = (0.1 * torch.randn(N, generator=g)).to(dt)
+    return layer
+
+
+@pytest.mark.parametrize("outliers", [(), (1, 9, 30)])
+def test_layer_cpu_branch_matches_oracle(outliers):
+    layer = _cpu_layer(40, 24, torch.float32, True, 3, outliers)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(2, 3, 40, generator=g)
+    y = layer(x)
+    assert y.shape == (2, 3, 24)
+    ref = oracle.w8a16_linear(x.reshape(-1, 40).numpy(), oracle.F32, layer.int8_weights.numpy(),
+                              layer.scales.numpy(), bias=layer.bias.detach().numpy(),
+                              outlier_cols=np.array(outliers, np.int64) if outliers else None,
+                              w_out=layer.outlier_weights.numpy() if outliers else None)
+    np.testing.assert_allclose(y.reshape(-1, 24).detach().numpy(), ref, rtol=1e-5, atol=1e-5)
+
+
+def test_state_dict_compact_layout_expands():
+    from cublade_amd.quantization import cuBladeW8A16LinearLayer
+    src = _cpu_layer(16, 6, torch.float16, True, 7, outliers=(2, 11))
+    sd = src.state_dict()
+    normal = src.normal_cols
+    sd = dict(sd)
+    sd["int8_weights"] = sd["int8_weights"][:, normal].contiguous()   # reference layout
+    dst = cuBladeW8A16LinearLayer(16, 6, bias=True, dtype=torch.float16, handle_outliers=True)
+    dst.load_state_dict(sd)
+    assert torch.equal(dst.int8_weights, src.int8_weights)
+    assert torch.equal(dst.outlier_cols, src.outlier_cols)
+    x = torch.randn(3, 16)
+    torch.testing.assert_close(dst(x), src(x))
+
+
+def test_oracle_not_imported_by_product():
+    """The product package never imports the oracle (test infrastructure)."""
+    for p in (ROOT / "cublade_amd").rglob("*.py"):
+        text = p.read_text()
+        assert "import oracle" not in text and "from oracle" not in text, p
