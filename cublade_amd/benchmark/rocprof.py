@@ -1,0 +1,78 @@
+"""Summaries of rocprofv3 results (the SQLite database rocprofv3 writes).
+
+    # kernel durations (run: rocprofv3 --kernel-trace --stats -d DIR -o NAME -- python ...)
+    python -m cublade_amd.benchmark.rocprof kernels DIR/NAME_results.db
+
+    # HBM bytes per dispatch from counters (run once with --pmc FETCH_SIZE and once
+    # with --pmc WRITE_SIZE; both counters are KiB per dispatch)
+    python -m cublade_amd.benchmark.rocprof counters DIR/NAME_results.db
+
+Kernel names are shortened to their template signature. Output is plain
+text for profiles/.
+"""
+from __future__ import annotations
+
+import re
+import sqlite3
+import sys
+from collections import defaultdict
+
+
+def _short(name: str) -> str:
+    name = re.sub(r"\(anonymous namespace\)::", "", name)
+    name = re.sub(r"\(.*\)$", "", name)            # drop the parameter list
+    name = name.replace("void ", "")
+    return name[:110]
+
+
+def kernel_stats(db: str):
+    """[(kernel, calls, avg_us, min_us, max_us, total_us)] sorted by total."""
+    con = sqlite3.connect(db)
+    rows = con.execute("select name, duration from kernels").fetchall()
+    agg = defaultdict(list)
+    for name, dur in rows:
+        agg[_short(name)].append(dur / 1e3)   # ns -> us
+    out = [(k, len(v), sum(v) / len(v), min(v), max(v), sum(v)) for k, v in agg.items()]
+    return sorted(out, key=lambda r: -r[5])
+
+
+def counter_stats(db: str):
+    """{(kernel, counter): [values per dispatch]} from a --pmc run."""
+    con = sqlite3.connect(db)
+    tabs = {r[0] for r in con.execute("select name from sqlite_master")}
+    res = defaultdict(list)
+    if "counters_collection" in tabs:
+        q = ("select kernel_name, counter_name, sum(value) from counters_collection "
+             "group by dispatch_id, counter_name")
+        for k, c, v in con.execute(q):
+            res[(_short(k), c)].append(v)
+        return res
+    # rocpd schema: pmc events joined with dispatches
+    q = ("select k.name, i.name, sum(p.value) from rocpd_pmc_event p "
+         "join rocpd_info_pmc i on p.pmc_id = i.id "
+         "join rocpd_kernel_dispatch d on p.event_id = d.event_id "
+         "join rocpd_info_kernel_symbol k on d.kernel_id = k.id "
+         "group by d.id, i.name")
+    for k, c, v in con.execute(q):
+        res[(_short(k), c)].append(v)
+    return res
+
+
+def main(argv=None):
+    argv = argv if argv is not None else sys.argv[1:]
+    if len(argv) != 2 or argv[0] not in ("kernels", "counters"):
+        print(__doc__)
+        return 2
+    if argv[0] == "kernels":
+        print(f"{'kernel':110s} {'calls':>6s} {'avg_us':>10s} {'min_us':>10s} {'max_us':>10s}")
+        for k, n, avg, mn, mx, _ in kernel_stats(argv[1]):
+            print(f"{k:110s} {n:6d} {avg:10.2f} {mn:10.2f} {mx:10.2f}")
+    else:
+        for (k, c), vals in sorted(counter_stats(argv[1]).items()):
+            avg = sum(vals) / len(vals)
+            print(f"{k:110s} {c:12s} n={len(vals):4d} avg={avg:14.1f}")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

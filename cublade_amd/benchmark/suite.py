@@ -1,0 +1,114 @@
+"""Benchmark suite over the BASELINE configurations (one GPU).
+
+Each op is timed through the public API with HIP events, the Infinity Cache
+flushed before every call, and reported as algorithmic bytes (or FLOPs) per
+second and as a fraction of the MI355X roofline (8 TB/s HBM, 2.5 PFLOP/s
+dense fp16 MFMA). Algorithmic bytes per op (N elements, C channels, G
+groups): per-tensor quant 2N read (amax) + 2N read + N written + 4 (cast);
+row / group quant 2N + N + 4C (one pass); column quant 2N + 2N + N + 4F (two
+passes); dequant N + 2N + 4 * scales. W8A16: 2 * M * N * K FLOPs.
+
+    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5 [--json out.json]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import statistics
+import sys
+
+import torch
+
+from . import configs
+from .core import FP16_MFMA_PEAK_FLOP_S, HBM_PEAK_BYTES_S, MallFlush, time_op
+
+
+def _rec(cfg, op, us, bytes_=None, flops=None):
+    med = statistics.median(us)
+    r = {"config": cfg, "op": op, "us_median": round(med, 2), "us_min": round(min(us), 2)}
+    if bytes_ is not None:
+        r["bytes"] = int(bytes_)
+        r["gbs"] = round(bytes_ / med / 1e3, 1)
+        r["hbm_frac"] = round(bytes_ / (med * 1e-6) / HBM_PEAK_BYTES_S, 4)
+    if flops is not None:
+        r["flops"] = int(flops)
+        r["tflops"] = round(flops / med / 1e6, 2)
+        r["mfma_frac"] = round(flops / (med * 1e-6) / FP16_MFMA_PEAK_FLOP_S, 4)
+    return r
+
+
+def run(selected, reps=20, warmup=3):
+    from cublade_amd.quantization import (cuBladeW8A16LinearLayer, dequantize_tensor,
+                                          quantize_tensor)
+    dev = torch.device("cuda")
+    flush = MallFlush(dev)
+    out = []
+
+    def q_and_dq(cfg, x, qkw, q_bytes, dq_bytes, tag=""):
+        qt = quantize_tensor(x, **qkw)
+        out.append(_rec(cfg, "quant" + tag, time_op(lambda: quantize_tensor(x, **qkw), reps,
+                                                     warmup, flush), q_bytes))
+        out.append(_rec(cfg, "dequant" + tag, time_op(lambda: dequantize_tensor(qt), reps,
+                                                      warmup, flush), dq_bytes))
+        print(json.dumps(out[-2]), json.dumps(out[-1]), sep="\n", flush=True)
+
+    if "c1" in selected:
+        x = configs.c1_fp8_tensor().to(dev)
+        n = x.numel()
+        q_and_dq("c1", x, dict(dtype=torch.float8_e4m3fn, mode="tensor"),
+                 2 * n + 2 * n + n + 4, n + 2 * n + 4)
+        del x
+    if "c2" in selected:
+        x = configs.c2_int8_tensor().to(dev)
+        n = x.numel()
+        q_and_dq("c2", x, dict(dtype=torch.int8, mode="tensor"), 2 * n + 2 * n + n + 4,
+                 n + 2 * n + 4)
+        del x
+    if "c3" in selected:
+        x = configs.c3_int8_channel().to(dev)
+        n, C, F = x.numel(), x.shape[0], x.shape[1]
+        q_and_dq("c3", x, dict(dtype=torch.int8, mode="channel", ch_axis=0),
+                 2 * n + n + 4 * C, n + 2 * n + 4 * C, "_axis0")
+        q_and_dq("c3", x, dict(dtype=torch.int8, mode="channel", ch_axis=1),
+                 2 * n + 2 * n + n + 4 * F, n + 2 * n + 4 * F, "_axis1")
+        del x
+    if "c4" in selected:
+        x = configs.c4_int8_group().to(dev)
+        n = x.numel()
+        G = n // 128
+        q_and_dq("c4", x, dict(dtype=torch.int8, mode="group", group_size=128, ch_axis=-1),
+                 2 * n + n + 4 * G, n + 2 * n + 4 * G)
+        del x
+    if "c5" in selected:
+        for M in (16, 256, 4096):
+            x, w = configs.c5_w8a16(M)
+            N, K = w.shape
+            layer = cuBladeW8A16LinearLayer(K, N, bias=False, dtype=torch.float16)
+            layer.quantize(w.to(dev))
+            xd = x.to(dev)
+            us = time_op(lambda: layer(xd), reps, warmup, flush)
+            bytes_ = N * K + 2 * N + 2 * M * K + 2 * M * N
+            r = _rec("c5", f"w8a16_m{M}", us, bytes_, 2.0 * M * N * K)
+            out.append(r)
+            print(json.dumps(r), flush=True)
+            del layer, xd
+    torch.cuda.synchronize()
+    return out
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5")
+    ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--json", default=None)
+    a = ap.parse_args(argv)
+    res = run(set(a.configs.split(",")), a.reps, a.warmup)
+    if a.json:
+        with open(a.json, "w") as f:
+            json.dump(res, f, indent=1)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

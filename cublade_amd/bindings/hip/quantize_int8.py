@@ -34,7 +34,7 @@ def quantize_per_tensor_int8(
     scale = torch.empty((), dtype=torch.float32, device=dev)
     L = _abi.lib()
     with torch.cuda.device(dev):
-        ws = _abi.workspace(dev, _abi.WS_CTRL_BYTES)
+        ws = _abi.workspace(dev, L.cbq_quant_tensor_ws_bytes())
         rc = L.cbq_quant_int8_tensor(_abi.ptr(x), code, n, float(eps), _abi.ptr(ws), ws.numel(),
                                      _abi.ptr(q), _abi.ptr(scale), _abi.stream_handle(dev))
     _abi.check(rc, "quantize_per_tensor_int8")

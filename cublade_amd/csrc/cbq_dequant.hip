@@ -19,7 +19,7 @@
 namespace cbq {
 namespace {
 
-constexpr int kDU = 2;   // 16-code chunks in flight per thread (per tensor)
+constexpr int kDU = 4;   // 16-code chunks in flight per thread (per tensor)
 
 template <bool FP8>
 __device__ __forceinline__ void dec4(uint32_t w, float* f) {

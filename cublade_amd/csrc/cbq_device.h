@@ -113,10 +113,14 @@ __device__ __forceinline__ uint32_t pack2_out(float a, float b) {
   }
 }
 
+// Scalar narrowing. The empty asm pins `a` as a finished fp32 value: without
+// it the compiler folds a preceding multiply into v_fma_mixlo_f16 (a*b + 0,
+// rounded once to fp16), which turns -0 into +0 and skips the fp32 rounding
+// of the product that the reference performs.
 template <int OUT>
 __device__ __forceinline__ uint16_t out1(float a) {
-  if constexpr (OUT == kBF16) return __builtin_bit_cast(uint16_t, (__bf16)a);
-  else return __builtin_bit_cast(uint16_t, (_Float16)a);
+  asm volatile("" : "+v"(a));
+  return static_cast<uint16_t>(pack2_out<OUT>(a, 0.0f) & 0xffffu);
 }
 
 template <int OUT>

@@ -2,11 +2,14 @@
 // and their C-ABI entry points.
 //
 // Kernels (reference kernels they replace, kernels/cuda/quantization/...):
-//   k_amax_tensor   per-tensor |x| max: 16-byte loads, wave64 DPP reduce, one
-//                   uint atomicMax per workgroup; the last workgroup turns the
-//                   maximum into inv / scale (quantize_per_tensor_fp8.cu:38-86,
-//                   quantize_int8.cu:47-101)
-//   k_cast_tensor   per-tensor cast, 16-byte loads and 8-byte packed stores
+//   k_amax_tensor   per-tensor |x| max over a persistent grid: 16-byte loads,
+//                   wave64 DPP reduce, one partial maximum per workgroup
+//                   written to the workspace (no atomics: measured on MI355X,
+//                   ~4k same-address device atomics cost ~100 us)
+//                   (quantize_per_tensor_fp8.cu:38-86, quantize_int8.cu:47-101)
+//   k_cast_tensor   per-tensor cast: every workgroup reduces the partial
+//                   maxima (<= 8 KiB, L2-resident) to inv, then 16-byte loads
+//                   and 8-byte packed stores; workgroup 0 writes the scale
 //                   (quantize_per_tensor_fp8.cu:88-132, quantize_int8.cu:103-166)
 //   k_rows_sub      fused single-pass quant of rows of 8..2048 elements: each
 //                   row is owned by a power-of-two group of lanes, reduced
@@ -29,23 +32,16 @@
 namespace cbq {
 namespace {
 
-// Control block words at the start of a workspace (zero between calls).
-enum : int { kCtlAmax = 0, kCtlCount = 1, kCtlInv = 2 };
-
 constexpr int kU = 4;                 // 8-element chunks in flight per thread
 constexpr int kTensorWgPerCu = 8;     // persistent grid size for per-tensor
-
-__device__ __forceinline__ uint32_t ld_acquire_agent(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+constexpr int kMaxTensorWg = 2048;    // cap on that grid (= partial maxima)
 
 // ---------------------------------------------------------------------------
 // Per tensor
 // ---------------------------------------------------------------------------
 template <int DT>
 __global__ __launch_bounds__(kBlock) void k_amax_tensor(
-    const void* __restrict__ x, int64_t n, int vec, uint32_t* __restrict__ ctl,
-    float eps, float qmax, float* __restrict__ scale_out) {
+    const void* __restrict__ x, int64_t n, int vec, float* __restrict__ partial) {
   __shared__ float red[kBlock / kWave];
   float m = 0.0f;
   if (vec) {
@@ -79,29 +75,25 @@ __global__ __launch_bounds__(kBlock) void k_amax_tensor(
       m = fmaxf(m, __builtin_fabsf(ld1<DT>(x, i)));
   }
   m = block_max(m, red);
-  if (threadIdx.x == 0) {
-    // m >= +0 and never NaN, so its bit pattern orders like the value.
-    atomicMax(&ctl[kCtlAmax], __float_as_uint(m));
-    __threadfence();
-    const uint32_t done = atomicAdd(&ctl[kCtlCount], 1u);
-    if (done == gridDim.x - 1) {
-      __threadfence();
-      const float amax = __uint_as_float(atomicOr(&ctl[kCtlAmax], 0u));
-      const float inv = inv_scale(amax, eps, qmax);
-      __hip_atomic_store(&ctl[kCtlInv], __float_as_uint(inv), __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-      *scale_out = 1.0f / inv;
-      atomicExch(&ctl[kCtlAmax], 0u);
-      atomicExch(&ctl[kCtlCount], 0u);
-    }
-  }
+  if (threadIdx.x == 0) partial[blockIdx.x] = m;
+}
+
+// Maximum of the nparts partial maxima -> inv; every thread gets it.
+__device__ __forceinline__ float reduce_partials(const float* __restrict__ partial, int nparts,
+                                                 float* red) {
+  float m = 0.0f;
+  for (int i = threadIdx.x; i < nparts; i += kBlock) m = fmaxf(m, partial[i]);
+  return block_max(m, red);
 }
 
 template <int DT, bool FP8>
 __global__ __launch_bounds__(kBlock) void k_cast_tensor(
-    const void* __restrict__ x, int64_t n, int vec, const uint32_t* __restrict__ ctl,
-    uint8_t* __restrict__ q) {
-  const float inv = __uint_as_float(ld_acquire_agent(&ctl[kCtlInv]));
+    const void* __restrict__ x, int64_t n, int vec, const float* __restrict__ partial,
+    int nparts, float eps, uint8_t* __restrict__ q, float* __restrict__ scale_out) {
+  __shared__ float red[kBlock / kWave];
+  const float inv = inv_scale(reduce_partials(partial, nparts, red), eps,
+                              FP8 ? kQmaxFp8 : kQmaxInt8);
+  if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = 1.0f / inv;
   if (vec) {
     const int64_t n8 = n >> 3;
     const int64_t step = static_cast<int64_t>(gridDim.x) * kU * kBlock;
@@ -372,27 +364,30 @@ bool valid_dtype(int dt, bool allow_f32) {
 
 int64_t tensor_grid(int64_t n, bool vec) {
   const int64_t work = vec ? cdiv(n >> 3, static_cast<int64_t>(kU) * kBlock) : cdiv(n, kBlock);
-  const int64_t cap = static_cast<int64_t>(device_cus()) * kTensorWgPerCu;
+  int64_t cap = static_cast<int64_t>(device_cus()) * kTensorWgPerCu;
+  if (cap > kMaxTensorWg) cap = kMaxTensorWg;
   int64_t g = work < cap ? work : cap;
   return g < 1 ? 1 : g;
 }
 
 template <int DT>
-int tensor_quant_t(const void* x, int64_t n, float eps, uint32_t* ctl, uint8_t* q, float* scale,
+int tensor_quant_t(const void* x, int64_t n, float eps, float* partial, uint8_t* q, float* scale,
                    bool fp8, hipStream_t s) {
   const bool vec = aligned(x, 16) && aligned(q, 8);
   const int64_t grid = tensor_grid(n, vec);
-  k_amax_tensor<DT><<<dim3(static_cast<unsigned>(grid)), dim3(kBlock), 0, s>>>(
-      x, n, vec ? 1 : 0, ctl, eps, fp8 ? kQmaxFp8 : kQmaxInt8, scale);
+  const dim3 g(static_cast<unsigned>(grid)), b(kBlock);
+  k_amax_tensor<DT><<<g, b, 0, s>>>(x, n, vec ? 1 : 0, partial);
   if (fp8) {
-    k_cast_tensor<DT, true><<<dim3(static_cast<unsigned>(grid)), dim3(kBlock), 0, s>>>(
-        x, n, vec ? 1 : 0, ctl, q);
+    k_cast_tensor<DT, true><<<g, b, 0, s>>>(x, n, vec ? 1 : 0, partial, static_cast<int>(grid),
+                                            eps, q, scale);
   } else {
-    k_cast_tensor<DT, false><<<dim3(static_cast<unsigned>(grid)), dim3(kBlock), 0, s>>>(
-        x, n, vec ? 1 : 0, ctl, q);
+    k_cast_tensor<DT, false><<<g, b, 0, s>>>(x, n, vec ? 1 : 0, partial, static_cast<int>(grid),
+                                             eps, q, scale);
   }
   return launch_status(fp8 ? "cbq_quant_fp8_tensor" : "cbq_quant_int8_tensor");
 }
+
+size_t tensor_ws_bytes() { return CBQ_WS_CTRL_BYTES + sizeof(float) * kMaxTensorWg; }
 
 int tensor_quant(const void* x, int dt, int64_t n, float eps, void* ws, size_t ws_bytes,
                  uint8_t* q, float* scale, bool fp8, hipStream_t s) {
@@ -401,13 +396,13 @@ int tensor_quant(const void* x, int dt, int64_t n, float eps, void* ws, size_t w
   CBQ_REQUIRE(n >= 0, "%s: negative element count", what);
   if (n == 0) return CBQ_OK;
   CBQ_REQUIRE(x && q && scale, "%s: null pointer", what);
-  CBQ_REQUIRE(ws && ws_bytes >= CBQ_WS_CTRL_BYTES && aligned(ws, 4),
-              "%s: workspace must be >= %d bytes, 4-byte aligned", what, CBQ_WS_CTRL_BYTES);
-  uint32_t* ctl = static_cast<uint32_t*>(ws);
+  CBQ_REQUIRE(ws && ws_bytes >= tensor_ws_bytes() && aligned(ws, 16),
+              "%s: workspace must be >= %zu bytes, 16-byte aligned", what, tensor_ws_bytes());
+  float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + CBQ_WS_CTRL_BYTES);
   switch (dt) {
-    case kF16: return tensor_quant_t<kF16>(x, n, eps, ctl, q, scale, fp8, s);
-    case kBF16: return tensor_quant_t<kBF16>(x, n, eps, ctl, q, scale, fp8, s);
-    default: return tensor_quant_t<kF32>(x, n, eps, ctl, q, scale, fp8, s);
+    case kF16: return tensor_quant_t<kF16>(x, n, eps, partial, q, scale, fp8, s);
+    case kBF16: return tensor_quant_t<kBF16>(x, n, eps, partial, q, scale, fp8, s);
+    default: return tensor_quant_t<kF32>(x, n, eps, partial, q, scale, fp8, s);
   }
 }
 
@@ -535,6 +530,8 @@ extern "C" int cbq_quant_int8_tensor(const void* x, int dtype, int64_t n, float 
   return tensor_quant(x, dtype, n, eps, ws, ws_bytes, reinterpret_cast<uint8_t*>(q), scale, false,
                       as_stream(stream));
 }
+
+extern "C" size_t cbq_quant_tensor_ws_bytes(void) { return tensor_ws_bytes(); }
 
 extern "C" size_t cbq_quant_int8_channel_ws_bytes(int64_t rows, int64_t cols, int axis) {
   if (axis != 1 || rows <= 0 || cols <= 0) return CBQ_WS_CTRL_BYTES;

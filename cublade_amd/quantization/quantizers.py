@@ -56,8 +56,20 @@ def _require_cuda_input(x: torch.Tensor, key, *, what: str) -> None:
         raise ValueError(f"{what}: tensor dtype must be one of {names}, got {x.dtype}")
 
 
+_ZERO_POINTS: dict = {}
+
+
 def _zero_scalar(device: torch.device) -> torch.Tensor:
-    return torch.zeros((), dtype=torch.float32, device=device)
+    """The 0-d fp32 zero point of the symmetric scheme. One tensor per device
+    is shared by every QuantizedTensor (read-only by contract), so a quantize
+    call launches no fill kernel for it (the reference allocates a fresh
+    torch.zeros(()) per call, quantizers.py:53-54)."""
+    key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
+    z = _ZERO_POINTS.get(key)
+    if z is None:
+        z = torch.zeros((), dtype=torch.float32, device=device)
+        _ZERO_POINTS[key] = z
+    return z
 
 
 def channel_kernel_axis(ndim: int, ch_axis: int) -> int:

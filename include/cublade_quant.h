@@ -41,10 +41,11 @@ enum { CBQ_F32 = 0, CBQ_F16 = 1, CBQ_BF16 = 2 };
 /* Status codes. */
 enum { CBQ_OK = 0, CBQ_EINVAL = 1, CBQ_ELAUNCH = 2 };
 
-/* Workspace contract.  Entry points that take (ws, ws_bytes) use the first
- * CBQ_WS_CTRL_BYTES bytes as a control block of counters that must be
- * zero-filled before the first call and that every call leaves zero-filled
- * again; the rest is per-call scratch. One workspace serves one stream at a
+/* Workspace contract.  Entry points that take (ws, ws_bytes) need a
+ * 16-byte aligned device buffer of at least the size their *_ws_bytes query
+ * returns. The first CBQ_WS_CTRL_BYTES bytes are a control block reserved for
+ * counters: zero-filled before the first call, and left zero-filled by every
+ * call; the rest is per-call scratch. One workspace serves one stream at a
  * time: calls that overlap in time must not share it. */
 #define CBQ_WS_CTRL_BYTES 256
 
@@ -53,6 +54,10 @@ const char* cbq_last_error(void);
 
 /* ABI version (major * 100 + minor). */
 int cbq_abi_version(void);
+
+/* Workspace bytes needed by cbq_quant_fp8_tensor / cbq_quant_int8_tensor
+ * (one partial maximum per workgroup of the persistent grid). */
+size_t cbq_quant_tensor_ws_bytes(void);
 
 /* Workspace bytes needed by cbq_quant_int8_channel (axis 1 needs per-column
  * partial maxima; axis 0 needs only the control block). */
@@ -65,7 +70,7 @@ size_t cbq_quant_int8_channel_ws_bytes(int64_t rows, int64_t cols, int axis);
  * cublade.bindings.cuda.quantize_fp8.quantize_per_tensor_fp8
  * (bindings/cuda/quantize_fp8.py:15-34).
  * x: n elements of dtype CBQ_F16 or CBQ_BF16. q: n FP8 E4M3 codes.
- * scale: one fp32, written when n > 0. ws: >= CBQ_WS_CTRL_BYTES. */
+ * scale: one fp32, written when n > 0. ws: cbq_quant_tensor_ws_bytes(). */
 int cbq_quant_fp8_tensor(const void* x, int dtype, int64_t n, float eps,
                          void* ws, size_t ws_bytes, uint8_t* q, float* scale,
                          cbq_stream_t stream);

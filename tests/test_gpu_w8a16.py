@@ -186,6 +186,7 @@ def test_layer_outlier_mode_and_state_dict():
     assert layer.int8_weights.shape == (N, K)
     assert torch.count_nonzero(layer.int8_weights[:, oc]).item() == 0
     layer.bias.data = (0.1 * torch.randn(N, generator=g)).half().to(DEV)
+    layer.bias.requires_grad_(False)
     x = torch.randn(M, K, generator=g).half()
     x[:, oc] = 12.0
     y = layer(x.to(DEV))
@@ -200,7 +201,7 @@ def test_layer_outlier_mode_and_state_dict():
     # CPU forward (reference CPU branch) agrees
     cpu = cuBladeW8A16LinearLayer(K, N, bias=True, dtype=torch.float16, handle_outliers=True)
     cpu.load_state_dict({k: v.cpu() for k, v in layer.state_dict().items()})
-    y_cpu = cpu(x.float()).float().numpy()
+    y_cpu = cpu(x.float()).detach().float().numpy()
     np.testing.assert_allclose(y_cpu, ref, **TOL)
     # reference compact layout [N, K - n_out] loads and gives the same output
     sd = {k: v.cpu() for k, v in layer.state_dict().items()}
@@ -232,7 +233,7 @@ def test_quantize_model_mlp():
     with torch.no_grad():
         y0 = qm[0](x)
     ref = oracle_y(bits(x), oracle.F16, bits(qm[0].int8_weights), bits(qm[0].scales),
-                   bias=bits(qm[0].bias))
+                   bias=bits(qm[0].bias.detach()))
     np.testing.assert_allclose(y0.float().cpu().numpy(), ref, **TOL)
 
 
