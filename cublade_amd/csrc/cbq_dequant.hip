@@ -36,7 +36,7 @@ __device__ __forceinline__ float dec1(uint8_t b) {
 
 template <int OUT>
 __device__ __forceinline__ void st8(void* y, int64_t elem, const float (&f)[8]) {
-  *reinterpret_cast<uint4*>(static_cast<uint16_t*>(y) + elem) = pack8_out<OUT>(f);
+  stg16(static_cast<uint16_t*>(y) + elem, pack8_out<OUT>(f));
 }
 
 template <int OUT>
@@ -61,7 +61,7 @@ __global__ __launch_bounds__(kBlock) void k_deq_tensor(
 #pragma unroll
       for (int u = 0; u < kDU; ++u) {
         const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
-        if (c < n16) r[u] = reinterpret_cast<const uint4*>(q)[c];
+        if (c < n16) r[u] = ldg16(q + c * 16);
       }
 #pragma unroll
       for (int u = 0; u < kDU; ++u) {
@@ -116,7 +116,7 @@ __global__ __launch_bounds__(kBlock) void k_deq_rows_sub(
       s[it] = scale[row];
 #pragma unroll
       for (int v = 0; v < VPL; ++v)
-        r[it][v] = *reinterpret_cast<const uint2*>(q + row * L + (v * LPR + lr) * 8);
+        r[it][v] = ldg8(q + row * L + (v * LPR + lr) * 8);
     }
   }
 #pragma unroll
@@ -150,7 +150,7 @@ __global__ __launch_bounds__(kBlock) void k_deq_rows_wg(
       uint2 r[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u)
-        r[u] = *reinterpret_cast<const uint2*>(q + base + (c + u * kBlock) * 8);
+        r[u] = ldg8(q + base + (c + u * kBlock) * 8);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         float f[8];
@@ -162,7 +162,7 @@ __global__ __launch_bounds__(kBlock) void k_deq_rows_wg(
       }
     }
     for (; c < nc; c += kBlock) {
-      const uint2 r = *reinterpret_cast<const uint2*>(q + base + c * 8);
+      const uint2 r = ldg8(q + base + c * 8);
       float f[8];
       int8x4_to_f32(r.x, f);
       int8x4_to_f32(r.y, f + 4);
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(kBlock) void k_deq_cols(
     for (; r + 4 <= r1; r += 4) {
       uint2 raw[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) raw[u] = *reinterpret_cast<const uint2*>(q + (r + u) * cols + c);
+      for (int u = 0; u < 4; ++u) raw[u] = ldg8(q + (r + u) * cols + c);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         float f[8];
@@ -216,7 +216,7 @@ __global__ __launch_bounds__(kBlock) void k_deq_cols(
       }
     }
     for (; r < r1; ++r) {
-      const uint2 raw = *reinterpret_cast<const uint2*>(q + r * cols + c);
+      const uint2 raw = ldg8(q + r * cols + c);
       float f[8];
       int8x4_to_f32(raw.x, f);
       int8x4_to_f32(raw.y, f + 4);

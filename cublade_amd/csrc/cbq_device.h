@@ -28,6 +28,62 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
+// Streaming loads and stores. Data read once (quantization inputs, codes to
+// dequantize) is loaded non-temporally so it does not allocate in the
+// Infinity Cache: measured on MI355X, 16-byte streaming reads reach ~6.8 TB/s
+// that way against ~3.8 TB/s with ordinary loads once the cache holds dirty
+// lines. Narrow outputs (8-byte code stores) are stored non-temporally too;
+// wide outputs (16-byte dequantized stores) are faster as ordinary stores.
+// The three switches are compile-time tuning knobs.
+// ---------------------------------------------------------------------------
+#ifndef CBQ_NT_LOADS
+#define CBQ_NT_LOADS 1
+#endif
+#ifndef CBQ_NT_STORES_NARROW
+#define CBQ_NT_STORES_NARROW 1
+#endif
+#ifndef CBQ_NT_STORES_WIDE
+#define CBQ_NT_STORES_WIDE 0
+#endif
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint4 ldg16(const void* p) {
+#if CBQ_NT_LOADS
+  const u32x4 v = __builtin_nontemporal_load(static_cast<const u32x4*>(p));
+#else
+  const u32x4 v = *static_cast<const u32x4*>(p);
+#endif
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint2 ldg8(const void* p) {
+#if CBQ_NT_LOADS
+  const u32x2 v = __builtin_nontemporal_load(static_cast<const u32x2*>(p));
+#else
+  const u32x2 v = *static_cast<const u32x2*>(p);
+#endif
+  return make_uint2(v.x, v.y);
+}
+
+__device__ __forceinline__ void stg8(void* p, uint2 v) {
+#if CBQ_NT_STORES_NARROW
+  __builtin_nontemporal_store(u32x2{v.x, v.y}, static_cast<u32x2*>(p));
+#else
+  *static_cast<u32x2*>(p) = u32x2{v.x, v.y};
+#endif
+}
+
+__device__ __forceinline__ void stg16(void* p, uint4 v) {
+#if CBQ_NT_STORES_WIDE
+  __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, static_cast<u32x4*>(p));
+#else
+  *static_cast<u32x4*>(p) = u32x4{v.x, v.y, v.z, v.w};
+#endif
+}
+
+// ---------------------------------------------------------------------------
 // Raw 8-element chunks: one 16-byte load for 2-byte types, two for fp32.
 // ---------------------------------------------------------------------------
 template <int DT> struct Raw8 { uint4 a; };
@@ -38,10 +94,9 @@ template <int DT> constexpr int elem_bytes() { return DT == kF32 ? 4 : 2; }
 template <int DT>
 __device__ __forceinline__ Raw8<DT> ld8(const void* base, int64_t elem) {
   Raw8<DT> r;
-  const uint4* p = reinterpret_cast<const uint4*>(
-      static_cast<const char*>(base) + elem * elem_bytes<DT>());
-  r.a = p[0];
-  if constexpr (DT == kF32) r.b = p[1];
+  const char* p = static_cast<const char*>(base) + elem * elem_bytes<DT>();
+  r.a = ldg16(p);
+  if constexpr (DT == kF32) r.b = ldg16(p + 16);
   return r;
 }
 

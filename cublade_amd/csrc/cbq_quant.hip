@@ -112,7 +112,7 @@ __global__ __launch_bounds__(kBlock) void k_cast_tensor(
           float f[8];
           cvt8<DT>(r[u], f);
           uint2 o = FP8 ? pack8_fp8(f, inv) : pack8_int8(f, inv);
-          *reinterpret_cast<uint2*>(q + c * 8) = o;
+          stg8(q + c * 8, o);
         }
       }
     }
@@ -179,7 +179,7 @@ __global__ __launch_bounds__(kBlock) void k_rows_sub(
     if (ok) {
 #pragma unroll
       for (int v = 0; v < VPL; ++v)
-        *reinterpret_cast<uint2*>(q + row * L + (v * LPR + lr) * 8) = pack8_int8(f[v], inv);
+        stg8(q + row * L + (v * LPR + lr) * 8, pack8_int8(f[v], inv));
       if (lr == 0) scale[row] = 1.0f / inv;
     }
   }
@@ -208,7 +208,7 @@ __global__ __launch_bounds__(kBlock) void k_rows_wg(
     const float inv = inv_scale(m, eps, kQmaxInt8);
 #pragma unroll
     for (int v = 0; v < VPL; ++v)
-      *reinterpret_cast<uint2*>(q + row * L + (v * kBlock + threadIdx.x) * 8) = pack8_int8(f[v], inv);
+      stg8(q + row * L + (v * kBlock + threadIdx.x) * 8, pack8_int8(f[v], inv));
     if (threadIdx.x == 0) scale[row] = 1.0f / inv;
   }
 }
@@ -242,7 +242,7 @@ __global__ __launch_bounds__(kBlock) void k_rows_generic(
       for (int64_t c = threadIdx.x; c < nc; c += kBlock) {
         float f[8];
         cvt8<DT>(ld8<DT>(x, base + c * 8), f);
-        *reinterpret_cast<uint2*>(q + base + c * 8) = pack8_int8(f, inv);
+        stg8(q + base + c * 8, pack8_int8(f, inv));
       }
     } else {
       for (int64_t i = threadIdx.x; i < L; i += kBlock)
@@ -301,16 +301,29 @@ __global__ __launch_bounds__(kBlock) void k_colmax(
   }
 }
 
+// Column maxima from the partials: a workgroup covers kFinCols columns; its
+// kBlock / kFinCols thread slices stride over the row blocks, then combine
+// through LDS.
+constexpr int kFinCols = 32;
 __global__ __launch_bounds__(kBlock) void k_col_finalize(
     const float* __restrict__ partial, int64_t nrb, int64_t cols, float eps,
     float* __restrict__ inv_out, float* __restrict__ scale) {
-  const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-  if (c >= cols) return;
+  constexpr int kSlices = kBlock / kFinCols;
+  __shared__ float red[kSlices][kFinCols];
+  const int cl = threadIdx.x % kFinCols, sl = threadIdx.x / kFinCols;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * kFinCols + cl;
   float m = 0.0f;
-  for (int64_t b = 0; b < nrb; ++b) m = fmaxf(m, partial[b * cols + c]);
-  const float inv = inv_scale(m, eps, kQmaxInt8);
-  inv_out[c] = inv;
-  scale[c] = 1.0f / inv;
+  if (c < cols)
+    for (int64_t b = sl; b < nrb; b += kSlices) m = fmaxf(m, partial[b * cols + c]);
+  red[sl][cl] = m;
+  __syncthreads();
+  if (sl == 0 && c < cols) {
+#pragma unroll
+    for (int k = 1; k < kSlices; ++k) m = fmaxf(m, red[k][cl]);
+    const float inv = inv_scale(m, eps, kQmaxInt8);
+    inv_out[c] = inv;
+    scale[c] = 1.0f / inv;
+  }
 }
 
 template <int DT>
@@ -336,7 +349,7 @@ __global__ __launch_bounds__(kBlock) void k_cast_cols(
         cvt8<DT>(raw[u], f);
 #pragma unroll
         for (int k = 0; k < 8; ++k) f[k] *= inv[k];
-        *reinterpret_cast<uint2*>(q + (r + u) * cols + c) = pack8_int8(f, 1.0f);
+        stg8(q + (r + u) * cols + c, pack8_int8(f, 1.0f));
       }
     }
     for (; r < r1; ++r) {
@@ -344,7 +357,7 @@ __global__ __launch_bounds__(kBlock) void k_cast_cols(
       cvt8<DT>(ld8<DT>(x, r * cols + c), f);
 #pragma unroll
       for (int k = 0; k < 8; ++k) f[k] *= inv[k];
-      *reinterpret_cast<uint2*>(q + r * cols + c) = pack8_int8(f, 1.0f);
+      stg8(q + r * cols + c, pack8_int8(f, 1.0f));
     }
   } else {
     const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
@@ -505,7 +518,7 @@ int cols_quant_t(const void* x, int64_t rows, int64_t cols, float eps, void* ws,
   float* inv = partial + g.nrb * cols;
   const dim3 grid2(static_cast<unsigned>(g.col_blocks), static_cast<unsigned>(g.nrb));
   k_colmax<DT><<<grid2, dim3(kBlock), 0, s>>>(x, rows, cols, g.RB, vec ? 1 : 0, partial);
-  k_col_finalize<<<dim3(static_cast<unsigned>(cdiv(cols, kBlock))), dim3(kBlock), 0, s>>>(
+  k_col_finalize<<<dim3(static_cast<unsigned>(cdiv(cols, kFinCols))), dim3(kBlock), 0, s>>>(
       partial, g.nrb, cols, eps, inv, scale);
   k_cast_cols<DT><<<grid2, dim3(kBlock), 0, s>>>(x, rows, cols, g.RB, vec ? 1 : 0, inv, q);
   return launch_status("cbq_quant_int8_channel");
