@@ -2,28 +2,31 @@
 
 Workload: per-tensor symmetric INT8 of an fp16
 [8192, 8192] tensor of 0.5 * Student-t(df=3) values, seed 1. One step is the
-whole hot path over that tensor: quantize_tensor (amax kernel + cast kernel)
-then dequantize_tensor (dequant kernel), through the public API.
+whole hot path over that tensor through the public API: quantize_tensor
+(amax kernel + cast kernel) then dequantize_tensor (dequant kernel).
 
-Timing: inputs resident in HBM; before each timed phase a 512 MiB
-read-modify-write of a scratch buffer evicts the 256 MB Infinity Cache (and
-keeps the GPU busy while the host enqueues the phase); each phase is timed
-with HIP events on the launch stream and the flush is outside the events.
-value = algorithmic bytes of the K steps / summed phase time.
+Timing: inputs resident in HBM. Before each timed phase a read-only sweep of
+a 512 MiB buffer evicts the 256 MB Infinity Cache and the L2s (leaving clean
+lines) and keeps the GPU busy while the host enqueues the phase; each phase
+is timed with HIP events on its launch stream, the sweep outside the events.
+value = algorithmic bytes of the K steps / summed phase time (GB/s).
+Algorithmic bytes per step (N = 67,108,864): amax 2N + cast 2N + N + 4 +
+dequant N + 2N + 4 = 536,870,920.
 
-Roofline: the dequant kernel (one launch per dequantize_tensor call),
-algorithmic bytes per launch = 67,108,864 codes read + 134,217,728 output
-bytes written + 4 scale bytes = 201,326,596 B, over its event-timed
-duration; peak 8 TB/s. traffic: HBM bytes per launch measured separately
-with rocprofv3 FETCH_SIZE / WRITE_SIZE (see profiles/), passed in via
---traffic-bytes or null.
+Roofline: the dequant kernel k_deq_tensor<int8, fp16>, the longest of the
+three. Algorithmic bytes per launch: N codes read + 2N output bytes written +
+4 scale bytes = 201,326,596 B. Its duration is measured live as the mean of
+ROOF_LAUNCHES back-to-back launches between two HIP events on the launch
+stream (after a cache sweep; the codes are read with non-temporal loads, so
+later launches re-read them from HBM); peak 8 TB/s. traffic: HBM bytes per
+launch from rocprofv3 FETCH_SIZE + WRITE_SIZE runs, read from
+profiles/dequant_int8_c2_traffic.json when present (null otherwise).
 
-Also reported (extra keys): each phase's GB/s, and the W8A16 linear at
-M = 4096 in TFLOP/s against the 2.5 PFLOP/s dense
-fp16 MFMA peak.
+Extra keys: per-phase GB/s, the W8A16 linear at M = 4096 (BASELINE
+configs[4]) in TFLOP/s against the 2.5 PFLOP/s dense fp16 MFMA peak.
 
-cpu_baseline: the C oracle (test infrastructure, single thread) on the
-first 8,388,608 elements of the same tensor, repeated for about 10 s.
+cpu_baseline: the C oracle (test infrastructure, single thread) on the first
+8,388,608 elements of the same tensor, repeated for about 10 s.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -47,6 +50,8 @@ BYTES_AMAX = 2 * N_ELEM
 BYTES_CAST = 2 * N_ELEM + N_ELEM + 4
 BYTES_DEQ = N_ELEM + 2 * N_ELEM + 4
 BYTES_STEP = BYTES_AMAX + BYTES_CAST + BYTES_DEQ
+ROOF_LAUNCHES = 10
+TRAFFIC_FILE = ROOT / "profiles" / "dequant_int8_c2_traffic.json"
 
 
 def parse():
@@ -56,28 +61,18 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-w8a16", action="store_true", help="skip the W8A16 extra")
-    ap.add_argument("--traffic-bytes", type=float, default=None,
-                    help="rocprofv3-measured HBM bytes per dequant launch")
+    ap.add_argument("--flush", default="clean", choices=["clean", "dirty"])
     return ap.parse_args()
-
-
-def make_input(torch):
-    g = torch.Generator().manual_seed(1)
-    shape = (8192, 8192)
-    z = torch.randn(*shape, generator=g)
-    c = [torch.randn(*shape, generator=g) for _ in range(3)]
-    t = z / torch.sqrt((c[0] ** 2 + c[1] ** 2 + c[2] ** 2) / 3)
-    x = (0.5 * t).half()
-    assert torch.isfinite(x).all()
-    return x
 
 
 def cpu_baseline(x_cpu):
     import numpy as np
+    import torch
+
     import oracle
 
     sample = x_cpu.reshape(-1)[: 8 * 1024 * 1024].contiguous()
-    xb = sample.view(__import__("torch").int16).numpy().view(np.uint16)
+    xb = sample.view(torch.int16).numpy().view(np.uint16)
     n = xb.size
     t_total, reps = 0.0, 0
     while t_total < 10.0 and reps < 50:
@@ -98,33 +93,31 @@ def cpu_baseline(x_cpu):
     }
 
 
-def w8a16_extra(torch, steps):
-    from cublade_amd.bindings.hip import w8a16_linear
+def w8a16_extra(torch, reps):
+    from cublade_amd.benchmark import configs
+    from cublade_amd.benchmark.core import MallFlush, time_op
+    from cublade_amd.quantization import cuBladeW8A16LinearLayer
 
-    g = torch.Generator().manual_seed(4)
-    M, K, N = 4096, 4096, 11008
-    x = torch.randn(M, K, generator=g)
-    oc = torch.sort(torch.randperm(K, generator=g)[:6]).values
-    x[:, oc] = torch.sign(torch.randn(M, 6, generator=g)) * (8 + 12 * torch.rand(M, 6, generator=g))
     dev = torch.device("cuda")
-    x = x.half().to(dev)
-    wq = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
-    s = (torch.rand(N, generator=g) * 1e-3).half().to(dev)
-    y = w8a16_linear(x, wq, s)
-    for _ in range(3):
-        y = w8a16_linear(x, wq, s)
-    torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-    ev[0].record()
-    for _ in range(steps):
-        y = w8a16_linear(x, wq, s)
-    ev[1].record()
-    torch.cuda.synchronize()
-    ms = ev[0].elapsed_time(ev[1]) / steps
-    flops = 2.0 * M * N * K
-    del y
-    return {"w8a16_m4096_ms": round(ms, 4), "w8a16_m4096_tflops": round(flops / ms / 1e9, 2),
-            "w8a16_m4096_mfma_frac": round(flops / (ms * 1e-3) / FP16_PEAK, 4)}
+    x, w = configs.c5_w8a16(4096)
+    N, K = w.shape
+    layer = cuBladeW8A16LinearLayer(K, N, bias=False, dtype=torch.float16)
+    layer.quantize(w.to(dev))
+    xd = x.to(dev)
+    us = time_op(lambda: layer(xd), reps, 2, MallFlush(dev))
+    us_med = sorted(us)[len(us) // 2]
+    flops = 2.0 * 4096 * N * K
+    return {"w8a16_m4096_us": round(us_med, 2),
+            "w8a16_m4096_tflops": round(flops / us_med / 1e6, 2),
+            "w8a16_m4096_mfma_frac": round(flops / (us_med * 1e-6) / FP16_PEAK, 4)}
+
+
+def load_traffic():
+    try:
+        d = json.loads(TRAFFIC_FILE.read_text())
+        return float(d["hbm_bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def main():
@@ -136,25 +129,27 @@ def main():
     import torch
 
     from cublade_amd import _abi
+    from cublade_amd.benchmark import configs
+    from cublade_amd.benchmark.core import MallFlush
     from cublade_amd.quantization import dequantize_tensor, quantize_tensor
 
     _abi.lib()
     dev = torch.device("cuda:0")
-    x_cpu = make_input(torch)
+    x_cpu = configs.c2_int8_tensor()
     x = x_cpu.to(dev)
-    flush = torch.zeros(512 * 1024 * 1024 // 4, dtype=torch.int32, device=dev)
+    flush = MallFlush(dev, mode=args.flush)
     stream = torch.cuda.current_stream(dev)
 
+    def ev():
+        return torch.cuda.Event(enable_timing=True)
+
     def step(t_q, t_d):
-        flush.add_(1)
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e2 = torch.cuda.Event(enable_timing=True)
-        e3 = torch.cuda.Event(enable_timing=True)
+        flush()
+        e0, e1, e2, e3 = ev(), ev(), ev(), ev()
         e0.record(stream)
         qt = quantize_tensor(x, dtype=torch.int8, mode="tensor")
         e1.record(stream)
-        flush.add_(1)
+        flush()
         e2.record(stream)
         y = dequantize_tensor(qt)
         e3.record(stream)
@@ -177,9 +172,22 @@ def main():
     d_ms = [a.elapsed_time(b) for a, b in td]
     sum_s = (sum(q_ms) + sum(d_ms)) / 1e3
     value = BYTES_STEP * args.steps / sum_s / 1e9
-    deq_avg_s = sum(d_ms) / len(d_ms) / 1e3
-    deq_gbs = BYTES_DEQ / deq_avg_s / 1e9
-    quant_gbs = (BYTES_AMAX + BYTES_CAST) / (sum(q_ms) / len(q_ms) / 1e3) / 1e9
+    quant_us = sum(q_ms) / len(q_ms) * 1e3
+    deq_us = sum(d_ms) / len(d_ms) * 1e3
+
+    # roofline kernel: back-to-back dequant launches after one sweep
+    roof = []
+    for _ in range(3):
+        flush()
+        a, b = ev(), ev()
+        a.record(stream)
+        for _ in range(ROOF_LAUNCHES):
+            dequantize_tensor(qt)
+        b.record(stream)
+        roof.append((a, b))
+    torch.cuda.synchronize()
+    roof_us = min(a.elapsed_time(b) for a, b in roof) * 1e3 / ROOF_LAUNCHES
+    achieved = BYTES_DEQ / (roof_us * 1e-6) / 1e9
 
     out = {
         "metric": "quant/dequant HBM GB/s (% of peak) at 1 MI355X; W8A16 TFLOPS at M=4096",
@@ -197,18 +205,19 @@ def main():
         "config": {"workload": "INT8 per-tensor quantize_tensor + dequantize_tensor, fp16 "
                                "[8192, 8192] 0.5*t(df=3), seed 1 (BASELINE configs[1])",
                    "hbm_frac": round(value * 1e9 / HBM_PEAK, 4),
-                   "mall_flushed": True},
-        "roofline": {"bound": "hbm", "achieved": round(deq_gbs, 2), "peak": HBM_PEAK / 1e9,
-                     "unit": "GB/s", "frac": round(deq_gbs * 1e9 / HBM_PEAK, 4),
-                     "traffic": args.traffic_bytes, "kernel": "k_deq_tensor<int8, fp16>",
-                     "bytes_per_launch": BYTES_DEQ,
-                     "avg_launch_us": round(deq_avg_s * 1e6, 2)},
-        "phases": {"quant_gbs": round(quant_gbs, 2), "quant_us": round(sum(q_ms) / len(q_ms) * 1e3, 2),
-                   "dequant_gbs": round(deq_gbs, 2), "dequant_us": round(deq_avg_s * 1e6, 2)},
-        "wall_s_incl_flush": round(wall, 3),
+                   "cache_sweep": args.flush},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": round(achieved * 1e9 / HBM_PEAK, 4),
+                     "traffic": load_traffic(), "kernel": "k_deq_tensor<int8, fp16>",
+                     "bytes_per_launch": BYTES_DEQ, "avg_launch_us": round(roof_us, 2)},
+        "phases": {"quant_us": round(quant_us, 2),
+                   "quant_gbs": round((BYTES_AMAX + BYTES_CAST) / quant_us / 1e3, 2),
+                   "dequant_us": round(deq_us, 2),
+                   "dequant_gbs": round(BYTES_DEQ / deq_us / 1e3, 2)},
+        "wall_s_incl_sweeps": round(wall, 3),
     }
     if not args.no_w8a16:
-        out.update(w8a16_extra(torch, max(3, args.steps // 4)))
+        out.update(w8a16_extra(torch, max(3, args.steps // 2)))
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(x_cpu)
     print(json.dumps(out), flush=True)

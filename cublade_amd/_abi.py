@@ -24,7 +24,7 @@ SOURCES = [
     CSRC / "cbq_w8a16.hip",
 ]
 
-WS_CTRL_BYTES = 256
+WS_CTRL_BYTES = 16384
 
 F32, F16, BF16 = 0, 1, 2
 DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}

@@ -1,0 +1,63 @@
+#!/bin/bash
+# Profiles the benchmark workloads with rocprofv3 and writes text summaries.
+#
+#   bash cublade_amd/benchmark/profile.sh OUTDIR
+#
+# 1. kernel trace of bench.py (BASELINE configs[1] step + W8A16 M=4096)
+# 2. FETCH_SIZE and WRITE_SIZE of bench.py (one counter per run), and of a
+#    256 MiB device copy (copy_calib.py) to calibrate both counters
+# 3. kernel trace of the per-config suite (configs 1-5)
+# Summaries: OUTDIR/bench_c2_kernels.txt, OUTDIR/dequant_int8_c2_traffic.json,
+# OUTDIR/suite_kernels.txt, OUTDIR/suite.json. Raw databases stay in OUTDIR/raw.
+# Run from the repository root on a GPU machine. Every GPU step has its own
+# time limit; the script stops at the first failing step.
+set -u
+OUT=${1:?usage: profile.sh OUTDIR}
+RAW="$OUT/raw"
+mkdir -p "$RAW"
+export TMPDIR=/tmp
+PY="python -u"
+R="python -m cublade_amd.benchmark.rocprof"
+
+step() { echo "[profile] $*"; }
+
+step "kernel trace: bench.py"
+timeout -k 10 300 rocprofv3 --kernel-trace --stats -d "$RAW/trace" -o bench -- \
+  $PY bench.py --no-cpu > "$RAW/trace.log" 2>&1 || exit $?
+step "counter FETCH_SIZE: bench.py"
+timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE --kernel-trace -d "$RAW/fetch" -o bench -- \
+  $PY bench.py --no-cpu --no-w8a16 --steps 3 --warmup 1 > "$RAW/fetch.log" 2>&1 || exit $?
+step "counter WRITE_SIZE: bench.py"
+timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE --kernel-trace -d "$RAW/write" -o bench -- \
+  $PY bench.py --no-cpu --no-w8a16 --steps 3 --warmup 1 > "$RAW/write.log" 2>&1 || exit $?
+step "counter FETCH_SIZE: 256 MiB copy"
+timeout -s KILL 60 rocprofv3 --pmc FETCH_SIZE --kernel-trace -d "$RAW/cal_fetch" -o calib -- \
+  $PY -m cublade_amd.benchmark.copy_calib > "$RAW/cal_fetch.log" 2>&1 || exit $?
+step "counter WRITE_SIZE: 256 MiB copy"
+timeout -s KILL 60 rocprofv3 --pmc WRITE_SIZE --kernel-trace -d "$RAW/cal_write" -o calib -- \
+  $PY -m cublade_amd.benchmark.copy_calib > "$RAW/cal_write.log" 2>&1 || exit $?
+step "kernel trace: suite"
+timeout -k 10 500 rocprofv3 --kernel-trace --stats -d "$RAW/suite" -o suite -- \
+  $PY -m cublade_amd.benchmark.suite --reps 10 --json "$OUT/suite.json" > "$RAW/suite.log" 2>&1 || exit $?
+
+step "summaries"
+{
+  echo "# rocprofv3 kernel trace of bench.py (BASELINE configs[1] step, W8A16 M=4096 extra)"
+  echo "# command: rocprofv3 --kernel-trace --stats -d RAW/trace -o bench -- python -u bench.py --no-cpu"
+  echo "# durations in microseconds"
+  $R kernels "$RAW/trace/bench_results.db"
+  echo
+  echo "# bench.py output line under the profiler:"
+  grep '"metric"' "$RAW/trace.log"
+} > "$OUT/bench_c2_kernels.txt" || exit $?
+$R traffic "k_deq_tensor<false, 1>" "$RAW/fetch/bench_results.db" "$RAW/write/bench_results.db" \
+  "$RAW/cal_fetch/calib_results.db" "$RAW/cal_write/calib_results.db" 262144 \
+  | python -c 'import json,sys; d=json.load(sys.stdin); d["command"]="bash cublade_amd/benchmark/profile.sh OUTDIR: rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --kernel-trace -- python -u bench.py --no-cpu --no-w8a16 --steps 3 --warmup 1; calibration: the same counters over python -m cublade_amd.benchmark.copy_calib (256 MiB copy = 262144 KiB)"; d["algorithmic_bytes_per_launch"]=201326596; d["traffic_over_algorithmic"]=round(d["hbm_bytes_per_launch"]/201326596,4); print(json.dumps(d, indent=1))' \
+  > "$OUT/dequant_int8_c2_traffic.json" || exit $?
+{
+  echo "# rocprofv3 kernel trace of the per-config suite (configs 1-5, 10 timed calls each)"
+  echo "# command: rocprofv3 --kernel-trace --stats -d RAW/suite -o suite -- python -u -m cublade_amd.benchmark.suite --reps 10"
+  echo "# durations in microseconds"
+  $R kernels "$RAW/suite/suite_results.db"
+} > "$OUT/suite_kernels.txt" || exit $?
+step "done"

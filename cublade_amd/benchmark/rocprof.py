@@ -7,8 +7,14 @@
     # with --pmc WRITE_SIZE; both counters are KiB per dispatch)
     python -m cublade_amd.benchmark.rocprof counters DIR/NAME_results.db
 
+    # HBM bytes per launch of one kernel, calibrated against a known copy
+    python -m cublade_amd.benchmark.rocprof traffic KERNEL FETCH.db WRITE.db \
+        CAL_FETCH.db CAL_WRITE.db CAL_KIB
+
+The calibration runs profile a copy of CAL_KIB KiB (copy_calib.py); the
+factor for each counter is CAL_KIB / (its mean over the copy dispatches).
 Kernel names are shortened to their template signature. Output is plain
-text for profiles/.
+text (JSON for traffic) for profiles/.
 """
 from __future__ import annotations
 
@@ -58,8 +64,34 @@ def counter_stats(db: str):
     return res
 
 
+def _mean_for(stats, kernel_sub, counter):
+    vals = [v for (k, c), vs in stats.items() if kernel_sub in k and c == counter for v in vs]
+    if not vals:
+        raise SystemExit(f"no {counter} samples for a kernel matching {kernel_sub!r}")
+    return sum(vals) / len(vals), len(vals)
+
+
+def traffic(kernel, fetch_db, write_db, cal_fetch_db, cal_write_db, cal_kib):
+    """Calibrated HBM bytes per launch of `kernel` (substring match)."""
+    cal_kib = float(cal_kib)
+    cf, _ = _mean_for(counter_stats(cal_fetch_db), "copyBuffer", "FETCH_SIZE")
+    cw, _ = _mean_for(counter_stats(cal_write_db), "copyBuffer", "WRITE_SIZE")
+    f, nf = _mean_for(counter_stats(fetch_db), kernel, "FETCH_SIZE")
+    w, nw = _mean_for(counter_stats(write_db), kernel, "WRITE_SIZE")
+    ff, fw = cal_kib / cf, cal_kib / cw
+    read_b, write_b = f * ff * 1024, w * fw * 1024
+    return {"kernel": kernel, "fetch_kib_raw": round(f, 1), "write_kib_raw": round(w, 1),
+            "dispatches": [nf, nw], "fetch_factor": round(ff, 4), "write_factor": round(fw, 4),
+            "hbm_read_bytes": int(read_b), "hbm_write_bytes": int(write_b),
+            "hbm_bytes_per_launch": int(read_b + write_b)}
+
+
 def main(argv=None):
     argv = argv if argv is not None else sys.argv[1:]
+    if argv and argv[0] == "traffic" and len(argv) == 7:
+        import json
+        print(json.dumps(traffic(*argv[1:]), indent=1))
+        return 0
     if len(argv) != 2 or argv[0] not in ("kernels", "counters"):
         print(__doc__)
         return 2

@@ -37,11 +37,11 @@ def _rec(cfg, op, us, bytes_=None, flops=None):
     return r
 
 
-def run(selected, reps=20, warmup=3):
+def run(selected, reps=20, warmup=3, flush_mode="clean"):
     from cublade_amd.quantization import (cuBladeW8A16LinearLayer, dequantize_tensor,
                                           quantize_tensor)
     dev = torch.device("cuda")
-    flush = MallFlush(dev)
+    flush = MallFlush(dev, mode=flush_mode)
     out = []
 
     def q_and_dq(cfg, x, qkw, q_bytes, dq_bytes, tag=""):
@@ -102,8 +102,9 @@ def main(argv=None):
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--json", default=None)
+    ap.add_argument("--flush", default="clean", choices=["clean", "dirty"])
     a = ap.parse_args(argv)
-    res = run(set(a.configs.split(",")), a.reps, a.warmup)
+    res = run(set(a.configs.split(",")), a.reps, a.warmup, a.flush)
     if a.json:
         with open(a.json, "w") as f:
             json.dump(res, f, indent=1)

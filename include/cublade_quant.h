@@ -47,7 +47,7 @@ enum { CBQ_OK = 0, CBQ_EINVAL = 1, CBQ_ELAUNCH = 2 };
  * counters: zero-filled before the first call, and left zero-filled by every
  * call; the rest is per-call scratch. One workspace serves one stream at a
  * time: calls that overlap in time must not share it. */
-#define CBQ_WS_CTRL_BYTES 256
+#define CBQ_WS_CTRL_BYTES 16384
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* cbq_last_error(void);

@@ -111,9 +111,11 @@ def test_golden(meta, arr):
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("M,K,N", [(1, 64, 48), (16, 128, 128), (100, 96, 200),
-                                   (128, 256, 128), (129, 80, 130), (256, 512, 384),
-                                   (7, 4096, 96), (300, 160, 257)])
+@pytest.mark.parametrize("M,K,N", [(1, 64, 48), (16, 128, 128), (7, 4096, 96),     # skinny, TM 1
+                                   (24, 128, 96), (40, 256, 200), (64, 64, 64),    # skinny, TM 2 / 4
+                                   (100, 96, 200), (128, 256, 128), (129, 80, 130),
+                                   (256, 512, 384), (300, 160, 257),               # 128 x 64 tiles
+                                   (1030, 128, 300), (1024, 320, 512)])            # 256 x 256 tiles
 def test_mfma_shapes(dt, M, K, N):
     run_and_check(M, K, N, dt, seed=M * 31 + K + N, bias=(M % 2 == 1))
 

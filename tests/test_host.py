@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_slot():
     L = _lib()
-    assert L.cbq_abi_version() == 100
+    assert L.cbq_abi_version() == 101
     assert L.cbq_last_error() in (b"",) or isinstance(L.cbq_last_error(), bytes)
 
 
@@ -58,7 +58,7 @@ def test_abi_rejects_bad_arguments_without_device_work():
     P = ctypes.c_void_p
     fake = P(0x1000)
     _einval(L.cbq_quant_fp8_tensor(fake, 0, 16, 1e-12, fake, 256, fake, fake, None), "dtype")
-    _einval(L.cbq_quant_int8_tensor(fake, 1, 16, 1e-12, fake, 256, fake, fake, None), "workspace")
+    _einval(L.cbq_quant_int8_tensor(fake, 1, 16, 1e-12, fake, 1024, fake, fake, None), "workspace")
     _einval(L.cbq_quant_int8_group(fake, 2, 4, 0, 1e-12, fake, fake, None), "group_size")
     _einval(L.cbq_quant_int8_group(fake, 2, 4, 4097, 1e-12, fake, fake, None), "group_size")
     _einval(L.cbq_quant_int8_channel(fake, 2, 4, 4, 2, 1e-12, fake, 256, fake, fake, None), "axis")
@@ -81,11 +81,13 @@ def test_abi_rejects_bad_arguments_without_device_work():
 
 def test_workspace_sizes():
     L = _lib()
-    assert L.cbq_quant_int8_channel_ws_bytes(100, 100, 0) == 256
-    assert L.cbq_quant_tensor_ws_bytes() == 256 + 4 * 2048
+    from cublade_amd import _abi
+    C = _abi.WS_CTRL_BYTES
+    assert L.cbq_quant_int8_channel_ws_bytes(100, 100, 0) == C
+    assert L.cbq_quant_tensor_ws_bytes() == C + 4 * 2048
     big = L.cbq_quant_int8_channel_ws_bytes(28672, 8192, 1)
-    assert big >= 256 + 8192 * 4 * 2 and big < 64 << 20
-    assert L.cbq_w8a16_ws_bytes(16, 11008, 4096, 0) >= 256
+    assert big >= C + 8192 * 4 * 2 and big < 64 << 20
+    assert L.cbq_w8a16_ws_bytes(16, 11008, 4096, 0) >= C
 
 
 def test_loader_memoises_failures(tmp_path):
