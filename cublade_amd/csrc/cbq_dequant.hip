@@ -2,8 +2,8 @@
 // their C-ABI entry points: y = T(float(q) * scale), rounded to nearest even.
 //
 // Kernels (reference kernels they replace, kernels/cuda/quantization/...):
-//   k_deq_tensor     one scale: 16 codes per thread step, one 16-byte load
-//                    and two 16-byte stores (dequantize_per_tensor_fp8.cu:23-66,
+//   k_deq_tensor     one scale: a full grid, 4 x 8 codes per thread, 8-byte
+//                    loads and 16-byte stores (dequantize_per_tensor_fp8.cu:23-66,
 //                    dequantize_int8.cu:29-64)
 //   k_deq_rows_sub   rows of 8..2048 codes (per-group, short per-channel rows)
 //                    owned by power-of-two lane groups; 8-byte loads, 16-byte
@@ -19,7 +19,7 @@
 namespace cbq {
 namespace {
 
-constexpr int kDU = 4;   // 16-code chunks in flight per thread (per tensor)
+constexpr int kDU = 4;   // 8-code chunks in flight per thread (per tensor)
 
 template <bool FP8>
 __device__ __forceinline__ void dec4(uint32_t w, float* f) {
@@ -47,42 +47,40 @@ __device__ __forceinline__ void st1(void* y, int64_t i, float v) {
 // ---------------------------------------------------------------------------
 // Per tensor
 // ---------------------------------------------------------------------------
+// Workgroup b covers codes [b * kDeqSpan, (b + 1) * kDeqSpan): each thread
+// loads kDU chunks of 8 codes (8-byte non-temporal loads, all in flight) and
+// writes each as one 16-byte store. A full (non-persistent) grid: measured
+// faster than a grid-stride loop for this write-heavy shape.
+constexpr int kDeqSpan = kBlock * kDU * 8;
+
 template <bool FP8, int OUT>
 __global__ __launch_bounds__(kBlock) void k_deq_tensor(
     const uint8_t* __restrict__ q, const float* __restrict__ scale, int64_t n, int vec,
     void* __restrict__ y) {
   const float s = scale[0];
   if (vec) {
-    const int64_t n16 = n >> 4;
-    const int64_t step = static_cast<int64_t>(gridDim.x) * kDU * kBlock;
-    for (int64_t c0 = static_cast<int64_t>(blockIdx.x) * kDU * kBlock + threadIdx.x; c0 < n16;
-         c0 += step) {
-      uint4 r[kDU];
+    const int64_t n8 = n >> 3;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * (kBlock * kDU) + threadIdx.x;
+    uint2 r[kDU];
 #pragma unroll
-      for (int u = 0; u < kDU; ++u) {
-        const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
-        if (c < n16) r[u] = ldg16(q + c * 16);
-      }
+    for (int u = 0; u < kDU; ++u) {
+      const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
+      if (c < n8) r[u] = ldg8(q + c * 8);
+    }
 #pragma unroll
-      for (int u = 0; u < kDU; ++u) {
-        const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
-        if (c < n16) {
-          float f[8];
-          dec4<FP8>(r[u].x, f);
-          dec4<FP8>(r[u].y, f + 4);
+    for (int u = 0; u < kDU; ++u) {
+      const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
+      if (c < n8) {
+        float f[8];
+        dec4<FP8>(r[u].x, f);
+        dec4<FP8>(r[u].y, f + 4);
 #pragma unroll
-          for (int k = 0; k < 8; ++k) f[k] *= s;
-          st8<OUT>(y, c * 16, f);
-          dec4<FP8>(r[u].z, f);
-          dec4<FP8>(r[u].w, f + 4);
-#pragma unroll
-          for (int k = 0; k < 8; ++k) f[k] *= s;
-          st8<OUT>(y, c * 16 + 8, f);
-        }
+        for (int k = 0; k < 8; ++k) f[k] *= s;
+        st8<OUT>(y, c * 8, f);
       }
     }
     if (blockIdx.x == 0) {
-      const int64_t i = n16 * 16 + threadIdx.x;   // the < 16 trailing codes
+      const int64_t i = n8 * 8 + threadIdx.x;   // the < 8 trailing codes
       if (i < n) st1<OUT>(y, i, dec1<FP8>(q[i]) * s);
     }
   } else {
@@ -246,10 +244,18 @@ unsigned rows_grid(int64_t rows) {
 template <bool FP8, int OUT>
 int deq_tensor_t(const uint8_t* q, const float* scale, int64_t n, void* y, hipStream_t s,
                  const char* what) {
-  const bool vec = aligned(q, 16) && aligned(y, 16);
-  const int64_t work = vec ? cdiv(n >> 4, static_cast<int64_t>(kDU) * kBlock) : cdiv(n, kBlock);
-  const int64_t cap = static_cast<int64_t>(device_cus()) * 8;
-  int64_t grid = work < cap ? work : cap;
+  const bool vec = aligned(q, 8) && aligned(y, 16);
+  int64_t grid;
+  if (vec) {
+    grid = cdiv(n, kDeqSpan);
+    if (grid > 0x7fffffffLL / kBlock) {
+      set_error("%s: tensor too large (%lld elements)", what, (long long)n);
+      return CBQ_EINVAL;
+    }
+  } else {
+    const int64_t cap = static_cast<int64_t>(device_cus()) * 8;
+    grid = cdiv(n, kBlock) < cap ? cdiv(n, kBlock) : cap;
+  }
   if (grid < 1) grid = 1;
   k_deq_tensor<FP8, OUT><<<dim3(static_cast<unsigned>(grid)), dim3(kBlock), 0, s>>>(
       q, scale, n, vec ? 1 : 0, y);

@@ -45,16 +45,20 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 #ifndef CBQ_NT_STORES_WIDE
 #define CBQ_NT_STORES_WIDE 0
 #endif
+// The per-tensor amax pass: its input is read again by the cast pass, so an
+// ordinary (allocating) load can leave it in the Infinity Cache for the cast.
+#ifndef CBQ_NT_LOADS_AMAX
+#define CBQ_NT_LOADS_AMAX 1
+#endif
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+template <bool NT = (CBQ_NT_LOADS != 0)>
 __device__ __forceinline__ uint4 ldg16(const void* p) {
-#if CBQ_NT_LOADS
-  const u32x4 v = __builtin_nontemporal_load(static_cast<const u32x4*>(p));
-#else
-  const u32x4 v = *static_cast<const u32x4*>(p);
-#endif
+  u32x4 v;
+  if constexpr (NT) v = __builtin_nontemporal_load(static_cast<const u32x4*>(p));
+  else v = *static_cast<const u32x4*>(p);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
@@ -91,12 +95,12 @@ template <> struct Raw8<kF32> { uint4 a, b; };
 
 template <int DT> constexpr int elem_bytes() { return DT == kF32 ? 4 : 2; }
 
-template <int DT>
+template <int DT, bool NT = (CBQ_NT_LOADS != 0)>
 __device__ __forceinline__ Raw8<DT> ld8(const void* base, int64_t elem) {
   Raw8<DT> r;
   const char* p = static_cast<const char*>(base) + elem * elem_bytes<DT>();
-  r.a = ldg16(p);
-  if constexpr (DT == kF32) r.b = ldg16(p + 16);
+  r.a = ldg16<NT>(p);
+  if constexpr (DT == kF32) r.b = ldg16<NT>(p + 16);
   return r;
 }
 

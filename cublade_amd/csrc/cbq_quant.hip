@@ -7,9 +7,10 @@
 //                   written to the workspace (no atomics: measured on MI355X,
 //                   ~4k same-address device atomics cost ~100 us)
 //                   (quantize_per_tensor_fp8.cu:38-86, quantize_int8.cu:47-101)
-//   k_cast_tensor   per-tensor cast: every workgroup reduces the partial
-//                   maxima (<= 8 KiB, L2-resident) to inv, then 16-byte loads
-//                   and 8-byte packed stores; workgroup 0 writes the scale
+//   k_cast_tensor   per-tensor cast on the same persistent grid: each workgroup
+//                   issues its first 16-byte loads, reduces the partial maxima
+//                   (L2-resident) to inv meanwhile, then 8-byte packed stores;
+//                   workgroup 0 writes the scale
 //                   (quantize_per_tensor_fp8.cu:88-132, quantize_int8.cu:103-166)
 //   k_rows_sub      fused single-pass quant of rows of 8..2048 elements: each
 //                   row is owned by a power-of-two group of lanes, reduced
@@ -32,8 +33,11 @@
 namespace cbq {
 namespace {
 
+#ifndef CBQ_TENSOR_WG_PER_CU
+#define CBQ_TENSOR_WG_PER_CU 8
+#endif
 constexpr int kU = 4;                 // 8-element chunks in flight per thread
-constexpr int kTensorWgPerCu = 8;     // persistent grid size for per-tensor
+constexpr int kTensorWgPerCu = CBQ_TENSOR_WG_PER_CU;   // persistent grid per CU
 constexpr int kMaxTensorWg = 2048;    // cap on that grid (= partial maxima)
 
 // ---------------------------------------------------------------------------
@@ -53,7 +57,7 @@ __global__ __launch_bounds__(kBlock) void k_amax_tensor(
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
         const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
-        if (c < n8) r[u] = ld8<DT>(x, c * 8);
+        if (c < n8) r[u] = ld8<DT, (CBQ_NT_LOADS_AMAX != 0)>(x, c * 8);
       }
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
@@ -86,24 +90,36 @@ __device__ __forceinline__ float reduce_partials(const float* __restrict__ parti
   return block_max(m, red);
 }
 
+// Persistent grid (the amax pass's): each workgroup issues its first chunk
+// loads, reduces the partial maxima (<= kMaxTensorWg floats, L2-resident) to
+// inv while they are in flight, then strides over the tensor. Measured on
+// MI355X, a full grid is slower here: every one of its workgroups pays the
+// partial reduction.
 template <int DT, bool FP8>
 __global__ __launch_bounds__(kBlock) void k_cast_tensor(
     const void* __restrict__ x, int64_t n, int vec, const float* __restrict__ partial,
     int nparts, float eps, uint8_t* __restrict__ q, float* __restrict__ scale_out) {
   __shared__ float red[kBlock / kWave];
-  const float inv = inv_scale(reduce_partials(partial, nparts, red), eps,
-                              FP8 ? kQmaxFp8 : kQmaxInt8);
-  if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = 1.0f / inv;
+  constexpr float kQ = FP8 ? kQmaxFp8 : kQmaxInt8;
   if (vec) {
     const int64_t n8 = n >> 3;
     const int64_t step = static_cast<int64_t>(gridDim.x) * kU * kBlock;
-    for (int64_t c0 = static_cast<int64_t>(blockIdx.x) * kU * kBlock + threadIdx.x; c0 < n8;
-         c0 += step) {
-      Raw8<DT> r[kU];
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * kU * kBlock + threadIdx.x;
+    Raw8<DT> r[kU];
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
-        if (c < n8) r[u] = ld8<DT>(x, c * 8);
+    for (int u = 0; u < kU; ++u) {
+      const int64_t c = first + static_cast<int64_t>(u) * kBlock;
+      if (c < n8) r[u] = ld8<DT>(x, c * 8);
+    }
+    const float inv = inv_scale(reduce_partials(partial, nparts, red), eps, kQ);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = 1.0f / inv;
+    for (int64_t c0 = first; c0 < n8; c0 += step) {
+      if (c0 != first) {
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+          const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
+          if (c < n8) r[u] = ld8<DT>(x, c * 8);
+        }
       }
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
@@ -111,19 +127,20 @@ __global__ __launch_bounds__(kBlock) void k_cast_tensor(
         if (c < n8) {
           float f[8];
           cvt8<DT>(r[u], f);
-          uint2 o = FP8 ? pack8_fp8(f, inv) : pack8_int8(f, inv);
-          stg8(q + c * 8, o);
+          stg8(q + c * 8, FP8 ? pack8_fp8(f, inv) : pack8_int8(f, inv));
         }
       }
     }
     if (blockIdx.x == 0) {
-      const int64_t i = n8 * 8 + threadIdx.x;
+      const int64_t i = n8 * 8 + threadIdx.x;   // the < 8 trailing elements
       if (i < n) {
         const float v = ld1<DT>(x, i) * inv;
         q[i] = FP8 ? q_fp8_1(v) : static_cast<uint8_t>(q_int8(v));
       }
     }
   } else {
+    const float inv = inv_scale(reduce_partials(partial, nparts, red), eps, kQ);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = 1.0f / inv;
     const int64_t step = static_cast<int64_t>(gridDim.x) * kBlock;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += step) {
       const float v = ld1<DT>(x, i) * inv;
@@ -375,6 +392,8 @@ bool valid_dtype(int dt, bool allow_f32) {
   return dt == kF16 || dt == kBF16 || (allow_f32 && dt == kF32);
 }
 
+// Persistent grid shared by the amax and cast passes (one partial maximum per
+// workgroup).
 int64_t tensor_grid(int64_t n, bool vec) {
   const int64_t work = vec ? cdiv(n >> 3, static_cast<int64_t>(kU) * kBlock) : cdiv(n, kBlock);
   int64_t cap = static_cast<int64_t>(device_cus()) * kTensorWgPerCu;

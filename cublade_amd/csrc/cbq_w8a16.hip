@@ -410,7 +410,7 @@ __global__ __launch_bounds__(256) void k_skinny(GemmArgs a) {
 }
 
 template <int ACT, int TM, int TN, int U>
-void launch_skinny(const GemmArgs& a, hipStream_t s) {
+void launch_skinny(GemmArgs a, hipStream_t s) {
   k_skinny<ACT, TM, TN, U><<<dim3(static_cast<unsigned>(cdiv(a.N, 16 * TN))), dim3(256), 0, s>>>(a);
 }
 
