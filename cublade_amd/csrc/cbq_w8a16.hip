@@ -29,6 +29,10 @@
 // contiguous run of tiles, and tiles run in groups of 8 m-tiles, so the
 // workgroups resident on one XCD share activation and weight k-slices in L2.
 //
+// k_gemm_dma<ACT> (M >= 1024, K % 64 == 0): 256 x 256 tiles of
+// v_mfma_f32_32x32x16 fed by LDS DMA, int8 weights widened after the
+// fragment read, explicitly scheduled k-steps (see the kernel's comment).
+//
 // k_skinny<ACT, TM, TN, U> (M <= 64): weight streaming with the K split across
 // the waves of a workgroup and reduced through LDS (see below). A split of K
 // across workgroups was measured slower on MI355X: publishing partial tiles
@@ -44,6 +48,7 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef __bf16 b8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16x __attribute__((ext_vector_type(16)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 // Operands and staging registers use native vector types: HIP's uint4 is a
@@ -64,9 +69,10 @@ template <int ACT>
 __device__ __forceinline__ void i8x4_to_act(uint32_t w, uint32_t& lo, uint32_t& hi) {
   if constexpr (ACT == kF16) {
     // fp16 0x6400 | b is 1024 + b for a byte b; b = q + 128, minus 1152 -> q.
+    // v_perm_b32 selector bytes 0-3 pick bytes of u, 4 picks 0x64.
     const uint32_t u = w ^ 0x80808080u;
-    const uint32_t l = (u & 0xffu) | ((u & 0xff00u) << 8) | 0x64006400u;
-    const uint32_t h = ((u >> 16) & 0xffu) | ((u >> 8) & 0x00ff0000u) | 0x64006400u;
+    const uint32_t l = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t h = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
     const h2 bias = {static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
     lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, l) - bias);
     hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, h) - bias);
@@ -109,6 +115,51 @@ __device__ __forceinline__ void decode_tile(int b, const GemmArgs& a, int& tm, i
   const int r = t % (G * a.tiles_n);
   tm = first_m + r % gsize;
   tn = r / gsize;
+}
+
+// Outlier side-GEMM for 4 consecutive outputs y[m, nb .. nb+3]:
+// v[r] += sum_j x[m, oc[j]] * w_out[nb + r, j], in j order. The loop is kept
+// rolled so that the unrolled tile epilogues stay small enough to keep their
+// accumulators in registers.
+template <int ACT>
+__device__ __forceinline__ f4 outlier_quad(const GemmArgs& a, int m, int nb, f4 v) {
+#pragma nounroll
+  for (int jj = 0; jj < a.n_out; ++jj) {
+    const int64_t k = a.oc[jj];
+    if (k < 0 || k >= a.K) continue;
+    const float xv = act_to_f32<ACT>(a.x[static_cast<int64_t>(m) * a.K + k]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (nb + r < a.N)
+        v[r] += xv * act_to_f32<ACT>(a.w_out[static_cast<int64_t>(nb + r) * a.n_out + jj]);
+  }
+  return v;
+}
+
+// Tile epilogue for one MFMA accumulator quad: y[m, nb + r] =
+// T(acc[r] * s[n] (+ outlier sum) (+ bias[n])), fp32 until the one rounding.
+template <int ACT>
+__device__ __forceinline__ void store_quad(const GemmArgs& a, const f4& acc, int m, int nb,
+                                           bool vec_store) {
+  f4 v;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    v[r] = nb + r < a.N ? acc[r] * act_to_f32<ACT>(a.scales[nb + r]) : 0.0f;
+  if (a.n_out > 0) v = outlier_quad<ACT>(a, m, nb, v);
+  if (a.bias) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (nb + r < a.N) v[r] += act_to_f32<ACT>(a.bias[nb + r]);
+  }
+  uint16_t* dst = a.y + static_cast<int64_t>(m) * a.N + nb;
+  if (vec_store && nb + 3 < a.N) {
+    *reinterpret_cast<uint2*>(dst) = make_uint2(pack2_out<ACT>(v[0], v[1]),
+                                                pack2_out<ACT>(v[2], v[3]));
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (nb + r < a.N) dst[r] = out1<ACT>(v[r]);
+  }
 }
 
 template <int ACT, int BM, int BN, int BK, int WGM, int WGN, int PD>
@@ -254,38 +305,338 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm(GemmArgs a) {
 #pragma unroll
   for (int j = 0; j < TM; ++j) {
     const int m = m0 + wm * (BM / WGM) + j * 16 + (lane & 15);
-    if (m >= a.M) continue;
+    if (m < a.M) {
+#pragma unroll
+      for (int i = 0; i < TN; ++i)
+        store_quad<ACT>(a, acc[i][j], m, n0 + wn * (BN / WGN) + i * 16 + (lane >> 4) * 4, vec_store);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// k_gemm_dma<ACT>: large-M tile kernel fed by LDS DMA.
+//
+// Tile 256 (m) x 256 (n) x 64 (k), 4 waves in 2 x 2, each wave 128 x 128 as
+// 4 x 4 tiles of v_mfma_f32_32x32x16_{f16,bf16} (256 accumulator registers).
+// On MI355X this MFMA runs at the full dense rate (2.47 PFLOP/s measured),
+// the 16x16x32 form at about half of it. Operand tiles go from global memory
+// straight into LDS with global_load_lds_dwordx4 (no VGPR staging, no LDS
+// store instructions): x as 256 rows of 128 bytes, the weight tile as 256
+// rows of 64 int8 codes. The codes are widened to the activation dtype after
+// the fragment read, so LDS holds half the bytes of a widened tile. Three
+// LDS stages (3 x 48 KiB): while the MFMAs of tile t run, tiles t + 1 and
+// t + 2 are in flight; each k-half's fragments are read while the previous
+// half is multiplied; one barrier per k-step.
+//
+// LDS rows are XOR-swizzled at 16-byte granularity so that the 16 lanes of a
+// fragment read phase (16 rows, one 16-byte chunk each) hit 16 distinct
+// 4-bank groups: x chunk c of row r sits at position c ^ ((r >> 1) & 7),
+// weight chunk c at c ^ ((r >> 2) & 3). The DMA writes 64 consecutive
+// 16-byte slots per wave instruction, so each lane loads the source chunk its
+// slot holds.
+//
+// k order: in a 64-k step, lane half h = lane / 32 owns k in [32 h, 32 h + 32)
+// of its weight row (two 16-byte reads) and of its x row (four reads). MFMA s
+// (0..3) takes k [32 h + 8 s, 32 h + 8 s + 8) from both operands, so A and B
+// see the same k permutation and the products are unchanged.
+//
+// Requirements (checked on the host): K % 64 == 0, x and wq 16-byte aligned,
+// M * K * 2 and N * K below 2^32 (32-bit per-lane offsets from a scalar base).
+// Rows past M or N are clamped to the last row; their products land in
+// outputs that are never stored.
+
+// LDS DMA of 16 bytes per lane: global sbase + voff -> LDS byte address lds +
+// 16 * lane (lds is wave-uniform). M0 carries the LDS address; it is saved
+// and restored inside the statement.
+__device__ __forceinline__ void lds_dma16(uint32_t voff, const void* sbase, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(sbase), "s"(lds)
+      : "memory");
+}
+
+// Wait until at most N vector-memory operations (the LDS DMAs of later tiles)
+// are outstanding and all LDS reads have returned, then barrier. Written as
+// one asm statement so that no LDS access is moved across it.
+template <int N>
+__device__ __forceinline__ void dma_wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// A wave-uniform pointer in SGPRs (the DMA's scalar base operand).
+template <typename T>
+__device__ __forceinline__ const T* uniform_ptr(const T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const T*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+}
+
+template <int ACT>
+__device__ __forceinline__ f16x mfma32x32x16(const u32x4& a, const u32x4& b, f16x c) {
+  if constexpr (ACT == kF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8, a),
+                                                  __builtin_bit_cast(h8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(b8, a),
+                                                   __builtin_bit_cast(b8, b), c, 0, 0, 0);
+}
+
+template <int ACT>
+__global__ __launch_bounds__(256) void k_gemm_dma(GemmArgs a) {
+  constexpr int BM = 256, BN = 256, BK = 64, NS = 3;
+  constexpr int XB = BM * BK * 2;          // x stage bytes (32 KiB)
+  constexpr int WB = BN * BK;              // weight stage bytes (16 KiB)
+  constexpr int SB = XB + WB;
+  constexpr int XL = XB / (256 * 16);      // DMA instructions per thread: 8
+  constexpr int WL = WB / (256 * 16);      // 4
+  constexpr int TM = 4, TN = 4;            // 32 x 32 tiles per wave
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * SB];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  int tm, tn;
+  decode_tile(blockIdx.x, a, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int nk = a.K / BK;
+  const uint32_t sbase = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+
+  // Per-lane DMA source offsets (bytes from the k0 column of the tile).
+  uint32_t xo[XL], wo[WL];
+#pragma unroll
+  for (int u = 0; u < XL; ++u) {
+    const int row = (u * 4 + wave) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((row >> 1) & 7);
+    const int m = min(m0 + row, a.M - 1);
+    xo[u] = static_cast<uint32_t>(m) * static_cast<uint32_t>(a.K) * 2u + c * 16u;
+  }
+#pragma unroll
+  for (int u = 0; u < WL; ++u) {
+    const int row = (u * 4 + wave) * 16 + (lane >> 2);
+    const int c = (lane & 3) ^ ((row >> 2) & 3);
+    const int n = min(n0 + row, a.N - 1);
+    wo[u] = static_cast<uint32_t>(n) * static_cast<uint32_t>(a.K) + c * 16u;
+  }
+  // DMA instruction u (0..XL+WL-1) of tile t into `stage`.
+  auto issue_one = [&](int t, int stage, int u) {
+    if (u < XL)
+      lds_dma16(xo[u], uniform_ptr(a.x + t * BK), sbase + stage * SB + wave * 1024 + u * 4096);
+    else
+      lds_dma16(wo[u - XL], uniform_ptr(a.wq + t * BK),
+                sbase + stage * SB + XB + wave * 1024 + (u - XL) * 4096);
+  };
+  auto issue = [&](int t, int stage) {
+#pragma unroll
+    for (int u = 0; u < XL + WL; ++u) issue_one(t, stage, u);
+  };
+
+  // Fragment read offsets within a stage: row r32 of each 32-row tile,
+  // lane half h.
+  const int r32 = lane & 31, h = lane >> 5;
+  uint32_t xr[4], wr[2];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    xr[q] = (wm * 128 + r32) * 128 + (((4 * h + q) ^ ((r32 >> 1) & 7)) << 4);
+#pragma unroll
+  for (int e = 0; e < 2; ++e)
+    wr[e] = XB + (wn * 128 + r32) * 64 + (((2 * h + e) ^ ((r32 >> 2) & 3)) << 4);
+
+  f16x acc[TN][TM];
+#pragma unroll
+  for (int i = 0; i < TN; ++i)
+#pragma unroll
+    for (int j = 0; j < TM; ++j) acc[i][j] = f16x{};
+
+  // A k-step is two halves: half e takes weight chunk e (k [32 h + 16 e,
+  // +16) of the lane's row) and x chunks 2 e and 2 e + 1, i.e. MFMA k-slices
+  // q = 2 e and 2 e + 1. Two fragment register sets, one per half; the reads
+  // for the next half land in one set while the MFMAs consume the other.
+  struct Frags {
+    u32x4 x[TM][2];
+    u32x4 w[TN];
+  };
+  Frags fr[2];
+  // Fragment read r (0..11) of half e: 8 x reads (j = r / 2, q = r % 2),
+  // then 4 weight reads (i = r - 8).
+  auto read_one = [&](int stage, int e, Frags& f, int r) {
+    const uint8_t* st = smem + stage * SB;
+    if (r < 2 * TM)
+      f.x[r >> 1][r & 1] = *reinterpret_cast<const u32x4*>(st + xr[2 * e + (r & 1)] + (r >> 1) * 4096);
+    else
+      f.w[r - 2 * TM] = *reinterpret_cast<const u32x4*>(st + wr[e] + (r - 2 * TM) * 2048);
+  };
+  auto read_half = [&](int stage, int e, Frags& f) {
+#pragma unroll
+    for (int r = 0; r < 2 * TM + TN; ++r) read_one(stage, e, f, r);
+  };
+  // Widen word c (0..3: 4 codes) of row tile i's weight fragment into w.
+  auto cvt_word = [&](const Frags& f, int i, int c, u32x4 (&w)[2]) {
+    const uint32_t src = c == 0 ? f.w[i].x : c == 1 ? f.w[i].y : c == 2 ? f.w[i].z : f.w[i].w;
+    uint32_t lo, hi;
+    i8x4_to_act<ACT>(src, lo, hi);
+    const int q = c >> 1, k = (c & 1) * 2;
+    w[q][k] = lo;
+    w[q][k + 1] = hi;
+  };
+  auto cvt_row = [&](const Frags& f, int i, u32x4 (&w)[2]) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) cvt_word(f, i, c, w);
+  };
+  // MFMA pair p (0..3) of row tile i: k-slice q = p / 2, columns j = 2 (p % 2)
+  // and 2 (p % 2) + 1. Within a row tile, an accumulator is reused every
+  // fourth MFMA; a dependent back-to-back MFMA would wait for the whole
+  // latency of the previous one.
+  auto mma_pair = [&](const Frags& f, int i, const u32x4 (&w)[2], int p) {
+    const int q = p >> 1, j0 = (p & 1) * 2;
+    acc[i][j0] = mfma32x32x16<ACT>(w[q], f.x[j0][q], acc[i][j0]);
+    acc[i][j0 + 1] = mfma32x32x16<ACT>(w[q], f.x[j0 + 1][q], acc[i][j0 + 1]);
+  };
+  // Explicit schedule. Row tile i's 8 MFMAs run as 4 pairs; after pair p
+  // the wave issues other work for the next pair's 64 MFMA cycles: word p
+  // of the next row tile's widening, and in the second half the DMA of tile
+  // t + 3 (3 instructions per pair, row tile 0) and the reads of tile t + 1's
+  // first half (3 per pair, row tile 1). sched_barrier pins the order.
+  u32x4 wa[2], wb[2];   // widened weights: current and next row tile
+  auto half = [&](Frags& f, Frags* fnext, auto&& extra) {
 #pragma unroll
     for (int i = 0; i < TN; ++i) {
-      const int nb = n0 + wn * (BN / WGN) + i * 16 + (lane >> 4) * 4;
-      float v[4];
+      u32x4 (&cur)[2] = (i & 1) ? wb : wa;
+      u32x4 (&nxt)[2] = (i & 1) ? wa : wb;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        mma_pair(f, i, cur, p);
+        if (i + 1 < TN) cvt_word(f, i + 1, p, nxt);
+        else if (fnext) cvt_word(*fnext, 0, p, nxt);
+        extra(i, p);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  // Step t: set 0 holds half 0 of tile t, set 1 half 1, wa row tile 0 of
+  // set 0 widened; tiles t + 1 and t + 2 are in flight. Half 0 (its last
+  // pairs widen row tile 0 of set 1); wait for tile t + 1 and barrier (every
+  // wave is past its reads of tile t's stage); half 1 with the DMA of tile
+  // t + 3 into that stage and the reads of tile t + 1's half 0 into set 0;
+  // then the reads of half 1 into set 1.
+  int stage_next = 1;   // stage of tile t + 1
+  auto step = [&](int t) {
+    const bool more = t + 1 < nk;
+    half(fr[0], &fr[1], [&](int, int) {});
+    if (more) {
+      if (t + 2 < nk) dma_wait_barrier<XL + WL>();
+      else dma_wait_barrier<0>();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int stage_cur = stage_next == 0 ? NS - 1 : stage_next - 1;
+    const bool dma = t + 3 < nk;
+    half(fr[1], more ? &fr[0] : nullptr, [&](int i, int p) {
+      if (i == 0 && dma) {
+#pragma unroll
+        for (int u = 0; u < 3; ++u) issue_one(t + 3, stage_cur, p * 3 + u);
+      }
+      if (more && i == 1) {
+#pragma unroll
+        for (int u = 0; u < 3; ++u) read_one(stage_next, 0, fr[0], p * 3 + u);
+      }
+    });
+    if (more) {
+      read_half(stage_next, 1, fr[1]);
+      stage_next = stage_next == NS - 1 ? 0 : stage_next + 1;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  if (nk > 0) {
+    issue(0, 0);
+    if (nk > 1) {
+      issue(1, 1);
+      dma_wait_barrier<XL + WL>();
+    } else {
+      dma_wait_barrier<0>();
+    }
+    if (nk > 2) issue(2, 2);
+    read_half(0, 0, fr[0]);
+    read_half(0, 1, fr[1]);
+    cvt_row(fr[0], 0, wa);
+  }
+  for (int t = 0; t < nk; ++t) step(t);
+
+  // Epilogue. Accumulator values 4q .. 4q+3 of tile (i, j) are the wave's
+  // outputs (m, n .. n+3) with m = 32 j + r32, n = 32 i + 8 q + 4 h. Each is
+  // finished in fp32 (scale, outlier sum, bias, in that order), rounded once,
+  // and written to an LDS copy of the wave's 128 x 128 output tile; the tile
+  // is then stored with 16-byte row-contiguous stores. The per-lane scales
+  // are loaded once, before any output store.
+  constexpr int EPS = 136;   // LDS row stride of the output tile (halfs)
+  static_assert(4 * 128 * EPS * 2 <= NS * SB, "epilogue tile fits in LDS");
+  dma_wait_barrier<0>();     // every wave is done with the operand stages
+  uint16_t* ep = reinterpret_cast<uint16_t*>(smem) + wave * (128 * EPS);
+  const int mw = m0 + wm * 128, nw = n0 + wn * 128;
+#pragma unroll
+  for (int i = 0; i < TN; ++i) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int nl = i * 32 + 8 * q + 4 * h;
+      float sc[4], bs[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int n = nb + r;
-        float val = 0.0f;
-        if (n < a.N) {
-          val = acc[i][j][r] * act_to_f32<ACT>(a.scales[n]);
-          for (int jj = 0; jj < a.n_out; ++jj) {
-            const int64_t k = a.oc[jj];
-            if (k >= 0 && k < a.K)
-              val += act_to_f32<ACT>(a.x[static_cast<int64_t>(m) * a.K + k]) *
-                     act_to_f32<ACT>(a.w_out[static_cast<int64_t>(n) * a.n_out + jj]);
-          }
-          if (a.bias) val += act_to_f32<ACT>(a.bias[n]);
-        }
-        v[r] = val;
+        const int n = nw + nl + r;
+        sc[r] = n < a.N ? act_to_f32<ACT>(a.scales[n]) : 0.0f;
+        bs[r] = (a.bias && n < a.N) ? act_to_f32<ACT>(a.bias[n]) : 0.0f;
       }
-      uint16_t* dst = a.y + static_cast<int64_t>(m) * a.N + nb;
-      if (vec_store && nb + 3 < a.N) {
-        *reinterpret_cast<uint2*>(dst) = make_uint2(pack2_out<ACT>(v[0], v[1]),
-                                                    pack2_out<ACT>(v[2], v[3]));
-      } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (nb + r < a.N) dst[r] = out1<ACT>(v[r]);
+      for (int j = 0; j < TM; ++j) {
+        f4 v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = acc[i][j][4 * q + r] * sc[r];
+        const int m = mw + j * 32 + r32;
+        if (a.n_out > 0 && m < a.M) v = outlier_quad<ACT>(a, m, nw + nl, v);
+        if (a.bias) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] += bs[r];
+        }
+        *reinterpret_cast<uint2*>(&ep[(j * 32 + r32) * EPS + nl]) =
+            make_uint2(pack2_out<ACT>(v[0], v[1]), pack2_out<ACT>(v[2], v[3]));
       }
     }
   }
+  // Row-contiguous stores: 16 lanes cover one 128-wide row (8 outputs each).
+  const bool vec16 = (a.N % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
+#pragma unroll 4
+  for (int u = 0; u < 32; ++u) {
+    const int row = u * 4 + (lane >> 4), c8 = (lane & 15) * 8;
+    const int m = mw + row, n = nw + c8;
+    if (m >= a.M || n >= a.N) continue;
+    const u32x4 val = *reinterpret_cast<const u32x4*>(&ep[row * EPS + c8]);
+    uint16_t* dst = a.y + static_cast<int64_t>(m) * a.N + n;
+    if (vec16 && n + 8 <= a.N) {
+      *reinterpret_cast<u32x4*>(dst) = val;
+    } else {
+      const uint32_t w[4] = {val.x, val.y, val.z, val.w};
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+        if (n + r < a.N) dst[r] = static_cast<uint16_t>(w[r >> 1] >> (16 * (r & 1)));
+    }
+  }
+}
+
+template <int ACT>
+void launch_gemm_dma(GemmArgs a, hipStream_t s) {
+  a.tiles_m = static_cast<int>(cdiv(a.M, 256));
+  a.tiles_n = static_cast<int>(cdiv(a.N, 256));
+  const unsigned grid = static_cast<unsigned>(a.tiles_m) * a.tiles_n;
+  k_gemm_dma<ACT><<<dim3(grid), dim3(256), 0, s>>>(a);
 }
 
 // Small M (M <= 16 * TM): weight streaming. A workgroup owns 16 * TN weight
@@ -375,36 +726,9 @@ __global__ __launch_bounds__(256) void k_skinny(GemmArgs a) {
 #pragma unroll
   for (int j = 0; j < TM; ++j) {
     const int m = j * 16 + row;
-    if (m >= a.M) continue;
+    if (m < a.M) {
 #pragma unroll
-    for (int i = 0; i < TN; ++i) {
-      const int nb = n0 + i * 16 + g * 4;
-      float v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int n = nb + r;
-        float val = 0.0f;
-        if (n < a.N) {
-          val = acc[i][j][r] * act_to_f32<ACT>(a.scales[n]);
-          for (int jj = 0; jj < a.n_out; ++jj) {
-            const int64_t k = a.oc[jj];
-            if (k >= 0 && k < a.K)
-              val += act_to_f32<ACT>(a.x[static_cast<int64_t>(m) * a.K + k]) *
-                     act_to_f32<ACT>(a.w_out[static_cast<int64_t>(n) * a.n_out + jj]);
-          }
-          if (a.bias) val += act_to_f32<ACT>(a.bias[n]);
-        }
-        v[r] = val;
-      }
-      uint16_t* dst = a.y + static_cast<int64_t>(m) * a.N + nb;
-      if (vec_store && nb + 3 < a.N) {
-        *reinterpret_cast<uint2*>(dst) = make_uint2(pack2_out<ACT>(v[0], v[1]),
-                                                    pack2_out<ACT>(v[2], v[3]));
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (nb + r < a.N) dst[r] = out1<ACT>(v[r]);
-      }
+      for (int i = 0; i < TN; ++i) store_quad<ACT>(a, acc[i][j], m, n0 + i * 16 + g * 4, vec_store);
     }
   }
 }
@@ -442,14 +766,23 @@ __global__ __launch_bounds__(kBlock) void k_w8a16_simple(
 // Kernel choice by M (measured on MI355X at N = 11008, K = 4096):
 //   M <= 64       k_skinny (weight streaming), TM = ceil(M / 16)
 //   64 < M < 1024 k_gemm 128 x 64 x 64, 2 x 2 waves
-//   M >= 1024     k_gemm 256 x 256 x 64, 4 x 2 waves
-enum Kind { kSkinny1, kSkinny2, kSkinny4, kTileMid, kTileLarge };
+//   M >= 1024     k_gemm_dma (K % 64 == 0 and 32-bit operand offsets),
+//                 else k_gemm 256 x 256 x 64, 4 x 2 waves
+enum Kind { kSkinny1, kSkinny2, kSkinny4, kTileMid, kTileLarge, kTileDma };
 
-Kind choose(int64_t M) {
+// k_gemm_dma addresses x and wq with 32-bit byte offsets from a scalar base
+// and needs whole 64-k steps.
+bool dma_ok(int64_t M, int64_t N, int64_t K) {
+  constexpr int64_t kLim = (1LL << 32) - 4096;
+  return K % 64 == 0 && M * K * 2 < kLim && N * K < kLim;
+}
+
+Kind choose(int64_t M, int64_t N, int64_t K) {
   if (M <= 16) return kSkinny1;
   if (M <= 32) return kSkinny2;
   if (M <= 64) return kSkinny4;
-  return M >= 1024 ? kTileLarge : kTileMid;
+  if (M < 1024) return kTileMid;
+  return dma_ok(M, N, K) ? kTileDma : kTileLarge;
 }
 
 template <int ACT, int BM, int BN, int BK, int WGM, int WGN, int PD>
@@ -467,6 +800,7 @@ void launch_kind(Kind k, const GemmArgs& a, hipStream_t s) {
     case kSkinny2: launch_skinny<ACT, 2, 1, 4>(a, s); break;
     case kSkinny4: launch_skinny<ACT, 4, 1, 2>(a, s); break;
     case kTileMid: launch_gemm<ACT, 128, 64, 64, 2, 2, 1>(a, s); break;
+    case kTileDma: launch_gemm_dma<ACT>(a, s); break;
     default: launch_gemm<ACT, 256, 256, 64, 4, 2, 1>(a, s); break;
   }
 }
@@ -510,7 +844,7 @@ int w8a16_t(const void* x, const int8_t* wq, const void* scales, const void* bia
   a.N = static_cast<int>(N);
   a.K = static_cast<int>(K);
   a.n_out = static_cast<int>(n_out);
-  launch_kind<ACT>(choose(M), a, s);
+  launch_kind<ACT>(choose(M, N, K), a, s);
   return launch_status("cbq_w8a16_linear");
 }
 

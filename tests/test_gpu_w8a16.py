@@ -115,7 +115,9 @@ def test_golden(meta, arr):
                                    (24, 128, 96), (40, 256, 200), (64, 64, 64),    # skinny, TM 2 / 4
                                    (100, 96, 200), (128, 256, 128), (129, 80, 130),
                                    (256, 512, 384), (300, 160, 257),               # 128 x 64 tiles
-                                   (1030, 128, 300), (1024, 320, 512)])            # 256 x 256 tiles
+                                   (1030, 128, 300), (1024, 320, 512),             # DMA 256 x 256
+                                   (1031, 192, 1000), (1024, 64, 256), (1290, 448, 520),
+                                   (1024, 80, 300), (1100, 208, 264)])             # K % 64 != 0
 def test_mfma_shapes(dt, M, K, N):
     run_and_check(M, K, N, dt, seed=M * 31 + K + N, bias=(M % 2 == 1))
 
@@ -124,6 +126,7 @@ def test_mfma_shapes(dt, M, K, N):
 def test_outlier_side_gemm(dt):
     run_and_check(64, 256, 96, dt, seed=5, bias=True, n_out=6)
     run_and_check(130, 512, 200, dt, seed=6, bias=False, n_out=17)
+    run_and_check(1100, 256, 300, dt, seed=7, bias=True, n_out=5)      # DMA tile kernel
 
 
 @pytest.mark.parametrize("M,K,N", [(5, 100, 40), (33, 24, 17)])
