@@ -33,6 +33,9 @@
 // v_mfma_f32_32x32x16 fed by LDS DMA, int8 weights widened after the
 // fragment read, explicitly scheduled k-steps (see the kernel's comment).
 //
+// k_stream1<ACT> (M <= 16) and k_stream<ACT, TM> (M <= 64): persistent
+// weight streaming for large weights (see the kernels' comments).
+//
 // k_skinny<ACT, TM, TN, U> (M <= 64): weight streaming with the K split across
 // the waves of a workgroup and reduced through LDS (see below). A split of K
 // across workgroups was measured slower on MI355X: publishing partial tiles
@@ -738,6 +741,328 @@ void launch_skinny(GemmArgs a, hipStream_t s) {
   k_skinny<ACT, TM, TN, U><<<dim3(static_cast<unsigned>(cdiv(a.N, 16 * TN))), dim3(256), 0, s>>>(a);
 }
 
+// ---------------------------------------------------------------------------
+// k_stream<ACT, TM> (M <= 16 * TM, TM <= 4): persistent weight streaming.
+//
+// One 16-wave workgroup per CU owns up to kStreamMaxTiles (3) row tiles of
+// 16 weight rows (tile b, b + G, b + 2G for grid size G). The activations
+// are staged in LDS by DMA once per K-chunk (the M rows, kc columns; at most
+// 128 KiB) and shared by every tile of the workgroup, so x crosses L2 once
+// per CU and chunk instead of once per row tile. Within a chunk the 16 waves
+// split the 64-k blocks. Each wave issues the x DMA, then the weight loads of
+// all its (tile, block) pairs straight from HBM into registers
+// (non-temporal, 16 bytes per lane, a fixed count so that the wait for the
+// DMA, vmcnt(#weight loads), leaves them in flight), then multiplies: per
+// block two x fragment reads from LDS serve every tile. Per block a lane
+// holds W[n][k0 + 16 g .. +16] and x[m][k0 + 16 g .. +16] (g = lane / 16):
+// the low and high 8 values feed two v_mfma_f32_16x16x32 with the same k
+// permutation on both operands. After the last chunk all partial tiles go
+// through LDS at once; wave (tile r, m-tile j) sums its 16 partials in wave
+// order (deterministic) and runs the epilogue with scales loaded at start.
+//
+// x LDS rows are padded by 16 bytes so that the 16 rows of a fragment read
+// fall in distinct bank groups; rows past M are not staged (their outputs
+// are never stored). Requirements (host): K % 1024 == 0, 16-byte aligned x
+// and wq, M <= 16 * TM, M * K * 2 < 2^32.
+constexpr int kStreamWaves = 16;
+constexpr int kStreamMaxTiles = 3;
+constexpr int kStreamLdsBytes = 132096;   // x chunk, then the partial tiles
+
+template <int TM>
+constexpr int stream_kc() { return TM == 1 ? 4096 : TM == 2 ? 2048 : 1024; }
+
+template <int ACT, int TM>
+__global__ __launch_bounds__(64 * kStreamWaves) void k_stream(GemmArgs a) {
+  constexpr int MP = 16 * TM;                 // padded rows
+  constexpr int KC = stream_kc<TM>();         // chunk columns
+  constexpr int RS = KC * 2 + 16;             // LDS row stride, bytes
+  constexpr int NB = KC / 64 / kStreamWaves;  // 64-k blocks per wave per chunk
+  constexpr int RT = kStreamMaxTiles;
+  constexpr int NLOAD = NB * RT;              // weight loads per wave per chunk
+  static_assert(MP * RS <= kStreamLdsBytes, "x chunk fits in LDS");
+  static_assert(RT * TM <= kStreamWaves, "one reduction pair per wave");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStreamLdsBytes];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int row = lane & 15, g = lane >> 4;
+  const int tiles = (a.N + 15) / 16;
+  const int G = gridDim.x;
+  const uint32_t sbase = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+  int ntile = 0;
+#pragma unroll
+  for (int r = 0; r < RT; ++r) ntile += (static_cast<int>(blockIdx.x) + r * G < tiles) ? 1 : 0;
+
+  // Reduction pair of this wave: tile rr, m-tile jr. Its scales and bias are
+  // loaded now, long before they are needed.
+  const int rr = wave / TM, jr = wave % TM;
+  const bool has_pair = rr < ntile && jr * 16 < a.M;
+  const int nq = (static_cast<int>(blockIdx.x) + rr * G) * 16 + g * 4;
+  // Raw values, loaded unconditionally (clamped index) so that they do not
+  // serialize the kernel's start; converted in the epilogue.
+  uint16_t sraw[4], braw[4];
+  const uint16_t* bsrc = a.bias ? a.bias : a.scales;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int n = min(nq + q, a.N - 1);
+    sraw[q] = a.scales[n];
+    braw[q] = bsrc[n];
+  }
+
+  f4 acc[RT][TM];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int j = 0; j < TM; ++j) acc[r][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // Weight row of this lane in each tile (clamped: loads of missing tiles
+  // and blocks read valid memory and their products are skipped).
+  const int8_t* wrow[RT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+    const int tile = min(static_cast<int>(blockIdx.x) + r * G, tiles - 1);
+    wrow[r] = a.wq + static_cast<int64_t>(min(tile * 16 + row, a.N - 1)) * a.K + 16 * g;
+  }
+
+  for (int c0 = 0; c0 < a.K; c0 += KC) {
+    const int clen = min(KC, a.K - c0);       // a multiple of 1024
+    const int nb = clen / 64;
+    __syncthreads();                          // previous chunk's x reads done
+    // Stage x[0 .. M, c0 .. c0 + clen) in LDS: one wave instruction moves
+    // 1 KiB (512 values) of one row.
+    const int segs = clen / 512;
+    for (int q = wave; q < a.M * segs && q < MP * segs; q += kStreamWaves) {
+      const int m = q / segs, sg = q % segs;
+      lds_dma16(static_cast<uint32_t>((m * a.K + c0 + sg * 512) * 2) + lane * 16u,
+                uniform_ptr(a.x), sbase + m * RS + sg * 1024);
+    }
+    // Weight loads of all (block, tile) pairs of this wave, always NLOAD.
+    // Wave blocks are contiguous (b = wave * nbw + i) so that one wave reads
+    // both 64-byte halves of each 128-byte line of its rows.
+    const int nbw = nb / kStreamWaves;        // nb is a multiple of 16
+    u32x4 w[NB][RT];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int b = min(wave * nbw + i, nb - 1);
+#pragma unroll
+      for (int r = 0; r < RT; ++r)
+        w[i][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[r] + c0 + b * 64));
+    }
+    // The DMA was issued before the NLOAD weight loads; loads complete in
+    // order, so at most NLOAD outstanding means the DMA has landed.
+    dma_wait_barrier<NLOAD>();
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int b = wave * nbw + i;
+      if (i >= nbw) continue;
+      u32x4 xl[TM], xh[TM];
+#pragma unroll
+      for (int j = 0; j < TM; ++j) {
+        const uint8_t* p = smem + (j * 16 + row) * RS + (b * 64 + 16 * g) * 2;
+        xl[j] = *reinterpret_cast<const u32x4*>(p);
+        xh[j] = *reinterpret_cast<const u32x4*>(p + 16);
+      }
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        if (r >= ntile) continue;
+        uint32_t o[8];
+        i8x4_to_act<ACT>(w[i][r].x, o[0], o[1]);
+        i8x4_to_act<ACT>(w[i][r].y, o[2], o[3]);
+        i8x4_to_act<ACT>(w[i][r].z, o[4], o[5]);
+        i8x4_to_act<ACT>(w[i][r].w, o[6], o[7]);
+        const u32x4 lo = {o[0], o[1], o[2], o[3]}, hi = {o[4], o[5], o[6], o[7]};
+#pragma unroll
+        for (int j = 0; j < TM; ++j) {
+          acc[r][j] = mfma16x16x32<ACT>(lo, xl[j], acc[r][j]);
+          acc[r][j] = mfma16x16x32<ACT>(hi, xh[j], acc[r][j]);
+        }
+      }
+    }
+  }
+
+  // All partial tiles through LDS (rounds of RPR tiles if they do not fit);
+  // wave (rr, jr) sums its 16 partials in wave order and stores.
+  constexpr int RPR = kStreamLdsBytes / (kStreamWaves * TM * 1024) < RT
+                          ? kStreamLdsBytes / (kStreamWaves * TM * 1024) : RT;
+  f4* red = reinterpret_cast<f4*>(smem);
+  const bool vec_store = (a.N % 4) == 0;
+#pragma unroll
+  for (int r0 = 0; r0 < RT; r0 += RPR) {
+    __syncthreads();
+#pragma unroll
+    for (int r = r0; r < r0 + RPR && r < RT; ++r)
+#pragma unroll
+      for (int j = 0; j < TM; ++j)
+        red[(((r - r0) * TM + j) * kStreamWaves + wave) * 64 + lane] = acc[r][j];
+    __syncthreads();
+    if (has_pair && rr >= r0 && rr < r0 + RPR) {
+      const f4* src = red + ((rr - r0) * TM + jr) * kStreamWaves * 64 + lane;
+      f4 sum = src[0];
+      for (int w2 = 1; w2 < kStreamWaves; ++w2) sum += src[w2 * 64];
+      const int m = jr * 16 + row;
+      if (m < a.M) {
+        f4 v;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = sum[q] * act_to_f32<ACT>(sraw[q]);
+        if (a.n_out > 0) v = outlier_quad<ACT>(a, m, nq, v);
+        if (a.bias) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] += act_to_f32<ACT>(braw[q]);
+        }
+        uint16_t* dst = a.y + static_cast<int64_t>(m) * a.N + nq;
+        if (vec_store && nq + 3 < a.N) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack2_out<ACT>(v[0], v[1]),
+                                                      pack2_out<ACT>(v[2], v[3]));
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (nq + q < a.N) dst[q] = out1<ACT>(v[q]);
+        }
+      }
+    }
+  }
+}
+
+// k_stream1<ACT> (M <= 16): weight streaming with row-contiguous loads.
+//
+// One 16-wave workgroup owns 3 consecutive row tiles (48 weight rows).
+// Every wave issues all of its weight loads at once, as 1 KiB row-contiguous
+// requests (wave w: rows 3 w .. 3 w + 2, each row's 4 KiB in sequence; 64
+// lanes x 16 bytes per request), which stream from HBM far faster than MFMA-shaped
+// requests (16 rows x 64 bytes). Per 1024-k step the rows are written to a
+// padded LDS stage (row stride 1040 bytes: the 16 rows of a fragment read
+// fall in distinct bank groups), one barrier, and read back in the MFMA
+// layout: wave w takes 64-k block w of the step for all 3 tiles, with its
+// x fragments loaded from L2 up front. k order within a block as in
+// k_stream. The 16 partial tiles are summed in wave order (deterministic).
+// Requirements (host): K % 1024 == 0, K <= 4096, 16-byte aligned x and wq,
+// M <= 16.
+constexpr int kStream1Rows = 48;
+constexpr int kStream1Stride = 1040;
+constexpr int kStream1MaxSteps = 4;
+
+template <int ACT>
+__global__ __launch_bounds__(1024) void k_stream1(GemmArgs a) {
+  constexpr int RT = 3, SB = kStream1Rows * kStream1Stride, NST = kStream1MaxSteps;
+  static_assert(2 * SB <= 2 * 49920, "two LDS stages");
+  static_assert(16 * RT * 64 * 16 <= 2 * SB, "reduction fits in the stages");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * SB];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int row = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * kStream1Rows;
+  const int nsteps = a.K / 1024;
+
+  // Weight rows n0 + 3 wave + i (clamped), issued row by row so that each
+  // row's 4 KiB is requested in sequence.
+  u32x4 wr[NST][RT];
+#pragma unroll
+  for (int i = 0; i < RT; ++i)
+#pragma unroll
+    for (int s = 0; s < NST; ++s) {
+      const int n = min(n0 + 3 * wave + i, a.N - 1);
+      const int sc = min(s, nsteps - 1);
+      wr[s][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+          a.wq + static_cast<int64_t>(n) * a.K + sc * 1024 + lane * 16));
+    }
+  // x fragments of block `wave` of every step (row `row`, rows past M
+  // repeat row M - 1; their outputs are never stored).
+  const int mr = min(row, a.M - 1);
+  u32x4 xl[NST], xh[NST];
+#pragma unroll
+  for (int s = 0; s < NST; ++s) {
+    const int sc = min(s, nsteps - 1);
+    const u32x4* xp = reinterpret_cast<const u32x4*>(
+        a.x + static_cast<int64_t>(mr) * a.K + sc * 1024 + wave * 64 + 16 * g);
+    xl[s] = xp[0];
+    xh[s] = xp[1];
+  }
+  // Scale and bias of this lane's outputs (wave r < 3 finishes tile r).
+  const int nq = n0 + wave * 16 + g * 4;
+  const uint16_t* bsrc = a.bias ? a.bias : a.scales;
+  uint16_t sraw[4], braw[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int n = min(nq + q, a.N - 1);
+    sraw[q] = a.scales[n];
+    braw[q] = bsrc[n];
+  }
+
+  f4 acc[RT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r) acc[r] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < NST; ++s) {
+    if (s >= nsteps) break;
+    uint8_t* st = smem + (s & 1) * SB;
+    // Stage s: rows 3 wave + i. The previous use of this stage (step
+    // s - 2) ended before the barrier of step s - 1.
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+      *reinterpret_cast<u32x4*>(st + (3 * wave + i) * kStream1Stride + lane * 16) = wr[s][i];
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+      const u32x4 wf =
+          *reinterpret_cast<const u32x4*>(st + (r * 16 + row) * kStream1Stride + wave * 64 + 16 * g);
+      uint32_t o[8];
+      i8x4_to_act<ACT>(wf.x, o[0], o[1]);
+      i8x4_to_act<ACT>(wf.y, o[2], o[3]);
+      i8x4_to_act<ACT>(wf.z, o[4], o[5]);
+      i8x4_to_act<ACT>(wf.w, o[6], o[7]);
+      const u32x4 lo = {o[0], o[1], o[2], o[3]}, hi = {o[4], o[5], o[6], o[7]};
+      acc[r] = mfma16x16x32<ACT>(lo, xl[s], acc[r]);
+      acc[r] = mfma16x16x32<ACT>(hi, xh[s], acc[r]);
+    }
+  }
+
+  // Partial tiles through LDS; wave r (< 3) sums tile r in wave order.
+  __syncthreads();
+  f4* red = reinterpret_cast<f4*>(smem);
+#pragma unroll
+  for (int r = 0; r < RT; ++r) red[(r * 16 + wave) * 64 + lane] = acc[r];
+  __syncthreads();
+  if (wave < RT && n0 + wave * 16 < a.N && row < a.M) {
+    const f4* src = red + wave * 16 * 64 + lane;
+    f4 sum = src[0];
+    for (int w2 = 1; w2 < 16; ++w2) sum += src[w2 * 64];
+    f4 v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = sum[q] * act_to_f32<ACT>(sraw[q]);
+    if (a.n_out > 0) v = outlier_quad<ACT>(a, row, nq, v);
+    if (a.bias) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] += act_to_f32<ACT>(braw[q]);
+    }
+    uint16_t* dst = a.y + static_cast<int64_t>(row) * a.N + nq;
+    if ((a.N % 4) == 0 && nq + 3 < a.N) {
+      *reinterpret_cast<uint2*>(dst) = make_uint2(pack2_out<ACT>(v[0], v[1]),
+                                                  pack2_out<ACT>(v[2], v[3]));
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (nq + q < a.N) dst[q] = out1<ACT>(v[q]);
+    }
+  }
+}
+
+template <int ACT>
+void launch_stream1(GemmArgs a, hipStream_t s) {
+  const unsigned grid = static_cast<unsigned>(cdiv(a.N, kStream1Rows));
+  k_stream1<ACT><<<dim3(grid), dim3(1024), 0, s>>>(a);
+}
+
+template <int ACT, int TM>
+void launch_stream(GemmArgs a, hipStream_t s) {
+  const int tiles = static_cast<int>(cdiv(a.N, 16));
+  int grid = std::min(tiles, device_cus());
+  grid = std::max(grid, static_cast<int>(cdiv(tiles, kStreamMaxTiles)));
+  k_stream<ACT, TM><<<dim3(static_cast<unsigned>(grid)), dim3(64 * kStreamWaves), 0, s>>>(a);
+}
+
 // Any shape or activation dtype (fp32 activations, K not a multiple of 16,
 // unaligned pointers): one output per thread, fp32 accumulation in k order.
 template <int ACT>
@@ -764,11 +1089,22 @@ __global__ __launch_bounds__(kBlock) void k_w8a16_simple(
 // Host side
 // ---------------------------------------------------------------------------
 // Kernel choice by M (measured on MI355X at N = 11008, K = 4096):
-//   M <= 64       k_skinny (weight streaming), TM = ceil(M / 16)
+//   M <= 16       k_stream1 when the weight is at least 8 MB, K % 1024 == 0,
+//                 K <= 4096 and the 48-row groups fit one wave of
+//                 workgroups; else k_skinny (TM = 1)
+//   M <= 64       k_stream<2 or 4> under the same size rules (3 row tiles
+//                 per workgroup); else k_skinny, TM = ceil(M / 16)
 //   64 < M < 1024 k_gemm 128 x 64 x 64, 2 x 2 waves
 //   M >= 1024     k_gemm_dma (K % 64 == 0 and 32-bit operand offsets),
 //                 else k_gemm 256 x 256 x 64, 4 x 2 waves
-enum Kind { kSkinny1, kSkinny2, kSkinny4, kTileMid, kTileLarge, kTileDma };
+enum Kind { kSkinny1, kSkinny2, kSkinny4, kTileMid, kTileLarge, kTileDma, kStream1, kStream2,
+            kStream4 };
+
+// The streaming kernels pay a fixed cost for their large workgroups; below
+// 8 MB of weight the k_skinny kernels are faster.
+bool stream_ok(int64_t M, int64_t N, int64_t K) {
+  return K % 1024 == 0 && N * K >= (8LL << 20) && M * K * 2 < (1LL << 31);
+}
 
 // k_gemm_dma addresses x and wq with 32-bit byte offsets from a scalar base
 // and needs whole 64-k steps.
@@ -778,9 +1114,13 @@ bool dma_ok(int64_t M, int64_t N, int64_t K) {
 }
 
 Kind choose(int64_t M, int64_t N, int64_t K) {
-  if (M <= 16) return kSkinny1;
-  if (M <= 32) return kSkinny2;
-  if (M <= 64) return kSkinny4;
+  const int64_t cus = device_cus();
+  const bool stream = stream_ok(M, N, K);
+  if (M <= 16)
+    return (stream && K <= 4096 && cdiv(N, kStream1Rows) <= cus) ? kStream1 : kSkinny1;
+  const bool tiles_fit = cdiv(N, 16) <= kStreamMaxTiles * cus;
+  if (M <= 32) return (stream && tiles_fit) ? kStream2 : kSkinny2;
+  if (M <= 64) return (stream && tiles_fit) ? kStream4 : kSkinny4;
   if (M < 1024) return kTileMid;
   return dma_ok(M, N, K) ? kTileDma : kTileLarge;
 }
@@ -799,6 +1139,9 @@ void launch_kind(Kind k, const GemmArgs& a, hipStream_t s) {
     case kSkinny1: launch_skinny<ACT, 1, 1, 4>(a, s); break;
     case kSkinny2: launch_skinny<ACT, 2, 1, 4>(a, s); break;
     case kSkinny4: launch_skinny<ACT, 4, 1, 2>(a, s); break;
+    case kStream1: launch_stream1<ACT>(a, s); break;
+    case kStream2: launch_stream<ACT, 2>(a, s); break;
+    case kStream4: launch_stream<ACT, 4>(a, s); break;
     case kTileMid: launch_gemm<ACT, 128, 64, 64, 2, 2, 1>(a, s); break;
     case kTileDma: launch_gemm_dma<ACT>(a, s); break;
     default: launch_gemm<ACT, 256, 256, 64, 4, 2, 1>(a, s); break;

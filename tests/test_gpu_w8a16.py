@@ -117,7 +117,9 @@ def test_golden(meta, arr):
                                    (256, 512, 384), (300, 160, 257),               # 128 x 64 tiles
                                    (1030, 128, 300), (1024, 320, 512),             # DMA 256 x 256
                                    (1031, 192, 1000), (1024, 64, 256), (1290, 448, 520),
-                                   (1024, 80, 300), (1100, 208, 264)])             # K % 64 != 0
+                                   (1024, 80, 300), (1100, 208, 264),              # K % 64 != 0
+                                   (7, 2048, 8200), (1, 4096, 4000), (13, 1024, 9000),  # k_stream1
+                                   (24, 4096, 5000), (64, 2048, 6000), (40, 1024, 9000)])  # k_stream
 def test_mfma_shapes(dt, M, K, N):
     run_and_check(M, K, N, dt, seed=M * 31 + K + N, bias=(M % 2 == 1))
 
@@ -127,6 +129,8 @@ def test_outlier_side_gemm(dt):
     run_and_check(64, 256, 96, dt, seed=5, bias=True, n_out=6)
     run_and_check(130, 512, 200, dt, seed=6, bias=False, n_out=17)
     run_and_check(1100, 256, 300, dt, seed=7, bias=True, n_out=5)      # DMA tile kernel
+    run_and_check(16, 2048, 4400, dt, seed=8, bias=True, n_out=4)      # k_stream1
+    run_and_check(40, 1024, 9000, dt, seed=9, bias=False, n_out=3)     # k_stream
 
 
 @pytest.mark.parametrize("M,K,N", [(5, 100, 40), (33, 24, 17)])
