@@ -40,6 +40,7 @@
 // the waves of a workgroup and reduced through LDS (see below). A split of K
 // across workgroups was measured slower on MI355X: publishing partial tiles
 // needs agent-scope release fences, which write back the whole L2.
+#include <algorithm>
 #include <type_traits>
 
 #include "cbq_device.h"
@@ -101,8 +102,10 @@ struct GemmArgs {
   const int64_t* oc;        // [n_out]
   const uint16_t* w_out;    // [N, n_out]
   uint16_t* y;              // [M, N]
+  float* part;              // split-K partial tiles (k_gemm_dma<ACT, true>)
   int M, N, K, n_out;
   int tiles_m, tiles_n;
+  int splits, split_steps;  // split-K: number of k-ranges, 64-k steps per range
 };
 
 // Workgroup -> (tile m, tile n); see the file comment.
@@ -394,7 +397,7 @@ __device__ __forceinline__ f16x mfma32x32x16(const u32x4& a, const u32x4& b, f16
                                                    __builtin_bit_cast(b8, b), c, 0, 0, 0);
 }
 
-template <int ACT>
+template <int ACT, bool SPLIT>
 __global__ __launch_bounds__(256) void k_gemm_dma(GemmArgs a) {
   constexpr int BM = 256, BN = 256, BK = 64, NS = 3;
   constexpr int XB = BM * BK * 2;          // x stage bytes (32 KiB)
@@ -409,10 +412,24 @@ __global__ __launch_bounds__(256) void k_gemm_dma(GemmArgs a) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
-  int tm, tn;
-  decode_tile(blockIdx.x, a, tm, tn);
+  // Split-K: workgroup b covers tile b % tiles of k-range b / tiles (after
+  // the XCD renumbering, so the workgroups of one XCD share a k-range of x).
+  int tm, tn, split = 0;
+  if constexpr (SPLIT) {
+    const int tiles = a.tiles_m * a.tiles_n;
+    const int total = tiles * a.splits;
+    const int per = total >> 3;
+    int b = blockIdx.x;
+    if (b < per * 8) b = (b & 7) * per + (b >> 3);
+    split = b / tiles;
+    tm = (b % tiles) % a.tiles_m;
+    tn = (b % tiles) / a.tiles_m;
+  } else {
+    decode_tile(blockIdx.x, a, tm, tn);
+  }
   const int m0 = tm * BM, n0 = tn * BN;
-  const int nk = a.K / BK;
+  const int kb = SPLIT ? split * a.split_steps : 0;          // first 64-k step
+  const int nk = SPLIT ? min(a.split_steps, a.K / BK - kb) : a.K / BK;
   const uint32_t sbase = __builtin_amdgcn_readfirstlane(lds_addr(smem));
 
   // Per-lane DMA source offsets (bytes from the k0 column of the tile).
@@ -434,9 +451,9 @@ __global__ __launch_bounds__(256) void k_gemm_dma(GemmArgs a) {
   // DMA instruction u (0..XL+WL-1) of tile t into `stage`.
   auto issue_one = [&](int t, int stage, int u) {
     if (u < XL)
-      lds_dma16(xo[u], uniform_ptr(a.x + t * BK), sbase + stage * SB + wave * 1024 + u * 4096);
+      lds_dma16(xo[u], uniform_ptr(a.x + (kb + t) * BK), sbase + stage * SB + wave * 1024 + u * 4096);
     else
-      lds_dma16(wo[u - XL], uniform_ptr(a.wq + t * BK),
+      lds_dma16(wo[u - XL], uniform_ptr(a.wq + (kb + t) * BK),
                 sbase + stage * SB + XB + wave * 1024 + (u - XL) * 4096);
   };
   auto issue = [&](int t, int stage) {
@@ -575,6 +592,22 @@ __global__ __launch_bounds__(256) void k_gemm_dma(GemmArgs a) {
   }
   for (int t = 0; t < nk; ++t) step(t);
 
+  if constexpr (SPLIT) {
+    // Partial tile in lane order: f4 (split, tile, wave, i, j, q, lane), one
+    // contiguous 1 KiB store per (i, j, q); k_splitk_reduce finishes it.
+    f4* dst = reinterpret_cast<f4*>(a.part) +
+              ((static_cast<int64_t>(split) * a.tiles_m * a.tiles_n + tn * a.tiles_m + tm) * 4 + wave) *
+                  (TN * TM * 4 * 64) + lane;
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+      for (int j = 0; j < TM; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          dst[((i * TM + j) * 4 + q) * 64] =
+              f4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+    return;
+  }
   // Epilogue. Accumulator values 4q .. 4q+3 of tile (i, j) are the wave's
   // outputs (m, n .. n+3) with m = 32 j + r32, n = 32 i + 8 q + 4 h. Each is
   // finished in fp32 (scale, outlier sum, bias, in that order), rounded once,
@@ -639,7 +672,47 @@ void launch_gemm_dma(GemmArgs a, hipStream_t s) {
   a.tiles_m = static_cast<int>(cdiv(a.M, 256));
   a.tiles_n = static_cast<int>(cdiv(a.N, 256));
   const unsigned grid = static_cast<unsigned>(a.tiles_m) * a.tiles_n;
-  k_gemm_dma<ACT><<<dim3(grid), dim3(256), 0, s>>>(a);
+  k_gemm_dma<ACT, false><<<dim3(grid), dim3(256), 0, s>>>(a);
+}
+
+// Split-K finish: one thread per partial f4 (4 outputs y[m, n .. n+3]); sums
+// the splits in order (deterministic), then scale, outliers, bias and one
+// rounding, as in the tile kernels' epilogue.
+template <int ACT>
+__global__ __launch_bounds__(kBlock) void k_splitk_reduce(GemmArgs a) {
+  const int64_t per_split = static_cast<int64_t>(a.tiles_m) * a.tiles_n * 16384;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (idx >= per_split) return;
+  const f4* src = reinterpret_cast<const f4*>(a.part) + idx;
+  f4 sum = src[0];
+  for (int sp = 1; sp < a.splits; ++sp) sum += src[sp * per_split];
+  const int lane = static_cast<int>(idx & 63), q = static_cast<int>((idx >> 6) & 3);
+  const int j = static_cast<int>((idx >> 8) & 3), i = static_cast<int>((idx >> 10) & 3);
+  const int wave = static_cast<int>((idx >> 12) & 3);
+  const int tile = static_cast<int>(idx >> 14);
+  const int tm = tile % a.tiles_m, tn = tile / a.tiles_m;
+  const int m = tm * 256 + (wave & 1) * 128 + j * 32 + (lane & 31);
+  const int nb = tn * 256 + (wave >> 1) * 128 + i * 32 + 8 * q + 4 * (lane >> 5);
+  if (m >= a.M || nb >= a.N) return;
+  store_quad<ACT>(a, sum, m, nb, (a.N % 4) == 0);
+}
+
+// Bytes of split-K partials for `splits` k-ranges.
+int64_t splitk_bytes(int64_t M, int64_t N, int splits) {
+  return cdiv(M, 256) * cdiv(N, 256) * splits * 16384 * 16;
+}
+
+template <int ACT>
+void launch_gemm_dma_splitk(GemmArgs a, int splits, hipStream_t s) {
+  a.tiles_m = static_cast<int>(cdiv(a.M, 256));
+  a.tiles_n = static_cast<int>(cdiv(a.N, 256));
+  const int nk = a.K / 64;
+  a.split_steps = static_cast<int>(cdiv(nk, splits));
+  a.splits = static_cast<int>(cdiv(nk, a.split_steps));   // no empty ranges
+  const unsigned grid = static_cast<unsigned>(a.tiles_m) * a.tiles_n * a.splits;
+  k_gemm_dma<ACT, true><<<dim3(grid), dim3(256), 0, s>>>(a);
+  const int64_t n4 = static_cast<int64_t>(a.tiles_m) * a.tiles_n * 16384;
+  k_splitk_reduce<ACT><<<dim3(static_cast<unsigned>(cdiv(n4, kBlock))), dim3(kBlock), 0, s>>>(a);
 }
 
 // Small M (M <= 16 * TM): weight streaming. A workgroup owns 16 * TN weight
@@ -1094,11 +1167,15 @@ __global__ __launch_bounds__(kBlock) void k_w8a16_simple(
 //                 workgroups; else k_skinny (TM = 1)
 //   M <= 64       k_stream<2 or 4> under the same size rules (3 row tiles
 //                 per workgroup); else k_skinny, TM = ceil(M / 16)
-//   64 < M < 1024 k_gemm 128 x 64 x 64, 2 x 2 waves
+//   64 < M < 1024 k_gemm_dma split over K (2-4 k-ranges, partial tiles in
+//                 the workspace, k_splitk_reduce) when the 256 x 256 tiles
+//                 alone would leave at least half of the CUs idle and the
+//                 caller's workspace holds the partials; else k_gemm_dma
+//                 from M = 384 on; else k_gemm 128 x 64 x 64, 2 x 2 waves
 //   M >= 1024     k_gemm_dma (K % 64 == 0 and 32-bit operand offsets),
 //                 else k_gemm 256 x 256 x 64, 4 x 2 waves
 enum Kind { kSkinny1, kSkinny2, kSkinny4, kTileMid, kTileLarge, kTileDma, kStream1, kStream2,
-            kStream4 };
+            kStream4, kTileDmaSplit };
 
 // The streaming kernels pay a fixed cost for their large workgroups; below
 // 8 MB of weight the k_skinny kernels are faster.
@@ -1113,7 +1190,16 @@ bool dma_ok(int64_t M, int64_t N, int64_t K) {
   return K % 64 == 0 && M * K * 2 < kLim && N * K < kLim;
 }
 
-Kind choose(int64_t M, int64_t N, int64_t K) {
+// k-ranges for the split-K tile path (0: not used). More ranges than 4 cost
+// more in partial traffic than they gain in occupancy.
+int splitk_count(int64_t M, int64_t N, int64_t K) {
+  if (M <= 64 || M >= 1024 || !dma_ok(M, N, K)) return 0;
+  const int64_t tiles = cdiv(M, 256) * cdiv(N, 256);
+  const int64_t sp = std::min<int64_t>({4, device_cus() / tiles, K / 64 / 4});
+  return sp >= 2 ? static_cast<int>(sp) : 0;
+}
+
+Kind choose(int64_t M, int64_t N, int64_t K, size_t ws_bytes) {
   const int64_t cus = device_cus();
   const bool stream = stream_ok(M, N, K);
   if (M <= 16)
@@ -1121,7 +1207,12 @@ Kind choose(int64_t M, int64_t N, int64_t K) {
   const bool tiles_fit = cdiv(N, 16) <= kStreamMaxTiles * cus;
   if (M <= 32) return (stream && tiles_fit) ? kStream2 : kSkinny2;
   if (M <= 64) return (stream && tiles_fit) ? kStream4 : kSkinny4;
-  if (M < 1024) return kTileMid;
+  if (M < 1024) {
+    const int sp = splitk_count(M, N, K);
+    if (sp && ws_bytes >= static_cast<size_t>(CBQ_WS_CTRL_BYTES + splitk_bytes(M, N, sp)))
+      return kTileDmaSplit;
+    return (M >= 384 && dma_ok(M, N, K)) ? kTileDma : kTileMid;
+  }
   return dma_ok(M, N, K) ? kTileDma : kTileLarge;
 }
 
@@ -1144,6 +1235,7 @@ void launch_kind(Kind k, const GemmArgs& a, hipStream_t s) {
     case kStream4: launch_stream<ACT, 4>(a, s); break;
     case kTileMid: launch_gemm<ACT, 128, 64, 64, 2, 2, 1>(a, s); break;
     case kTileDma: launch_gemm_dma<ACT>(a, s); break;
+    case kTileDmaSplit: launch_gemm_dma_splitk<ACT>(a, a.splits, s); break;
     default: launch_gemm<ACT, 256, 256, 64, 4, 2, 1>(a, s); break;
   }
 }
@@ -1172,7 +1264,7 @@ bool mfma_path(int64_t M, int64_t N, int64_t K, const void* x, const int8_t* wq,
 template <int ACT>
 int w8a16_t(const void* x, const int8_t* wq, const void* scales, const void* bias,
             const int64_t* oc, int64_t n_out, const void* w_out, int64_t M, int64_t N, int64_t K,
-            void* y, hipStream_t s) {
+            void* ws, size_t ws_bytes, void* y, hipStream_t s) {
   if (!mfma_path(M, N, K, x, wq, y))
     return w8a16_simple<ACT>(x, wq, scales, bias, oc, n_out, w_out, M, N, K, y, s);
   GemmArgs a{};
@@ -1187,7 +1279,12 @@ int w8a16_t(const void* x, const int8_t* wq, const void* scales, const void* bia
   a.N = static_cast<int>(N);
   a.K = static_cast<int>(K);
   a.n_out = static_cast<int>(n_out);
-  launch_kind<ACT>(choose(M, N, K), a, s);
+  const Kind kind = choose(M, N, K, ws ? ws_bytes : 0);
+  if (kind == kTileDmaSplit) {
+    a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + CBQ_WS_CTRL_BYTES);
+    a.splits = splitk_count(M, N, K);
+  }
+  launch_kind<ACT>(kind, a, s);
   return launch_status("cbq_w8a16_linear");
 }
 
@@ -1197,8 +1294,10 @@ int w8a16_t(const void* x, const int8_t* wq, const void* scales, const void* bia
 using namespace cbq;
 
 extern "C" size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_out) {
-  (void)M; (void)N; (void)K; (void)n_out;
-  return CBQ_WS_CTRL_BYTES;
+  (void)n_out;
+  if (M <= 0 || N <= 0 || K <= 0) return CBQ_WS_CTRL_BYTES;
+  const int sp = splitk_count(M, N, K);
+  return CBQ_WS_CTRL_BYTES + (sp ? static_cast<size_t>(splitk_bytes(M, N, sp)) : 0);
 }
 
 extern "C" int cbq_w8a16_linear(const void* x, int act_dtype, const int8_t* wq,
@@ -1207,8 +1306,6 @@ extern "C" int cbq_w8a16_linear(const void* x, int act_dtype, const int8_t* wq,
                                 int64_t M, int64_t N, int64_t K, void* ws, size_t ws_bytes,
                                 void* y, cbq_stream_t stream) {
   clear_error();
-  (void)ws;
-  (void)ws_bytes;
   const char* what = "cbq_w8a16_linear";
   CBQ_REQUIRE(act_dtype == kF16 || act_dtype == kBF16 || act_dtype == kF32,
               "%s: activation dtype must be fp16, bf16 or fp32 (code %d)", what, act_dtype);
@@ -1221,9 +1318,12 @@ extern "C" int cbq_w8a16_linear(const void* x, int act_dtype, const int8_t* wq,
   if (act_dtype == kF32)
     return w8a16_simple<kF32>(x, wq, scales, bias, outlier_cols, n_out, w_out, M, N, K, y,
                               as_stream(stream));
+  // The split-K partials go after the control block; a workspace that is
+  // missing, unaligned or too small selects a path without partials.
+  if (ws && !aligned(ws, 256)) ws = nullptr;
   return act_dtype == kF16
-             ? w8a16_t<kF16>(x, wq, scales, bias, outlier_cols, n_out, w_out, M, N, K, y,
-                             as_stream(stream))
-             : w8a16_t<kBF16>(x, wq, scales, bias, outlier_cols, n_out, w_out, M, N, K, y,
-                              as_stream(stream));
+             ? w8a16_t<kF16>(x, wq, scales, bias, outlier_cols, n_out, w_out, M, N, K, ws,
+                             ws_bytes, y, as_stream(stream))
+             : w8a16_t<kBF16>(x, wq, scales, bias, outlier_cols, n_out, w_out, M, N, K, ws,
+                              ws_bytes, y, as_stream(stream));
 }

@@ -131,7 +131,10 @@ int cbq_dequant_int8_group(const int8_t* q, const float* scale,
 
 /* ---- W8A16 linear ------------------------------------------------------- */
 
-/* Workspace bytes needed by cbq_w8a16_linear for this shape. */
+/* Workspace bytes for cbq_w8a16_linear at this shape: the control block,
+ * plus, for 64 < M < 1024, fp32 partial tiles of a split-K launch (up to
+ * 4 x ceil(M/256) x ceil(N/256) x 256 KiB). The reference allocates its
+ * temporaries inside the forward (linear.py:105-131). */
 size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_out);
 
 /* Replaces the forward chain of cuBladeW8A16LinearLayer
@@ -148,7 +151,9 @@ size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_out);
  * wq: int8 [N,K] row-major; its outlier columns hold 0.
  * scales, bias (nullable): [N] act_dtype. outlier_cols: n_out int64 indices in
  * [0, K) (nullable when n_out == 0); w_out: [N, n_out] act_dtype.
- * ws: cbq_w8a16_ws_bytes(...) bytes, control block zeroed. */
+ * ws: cbq_w8a16_ws_bytes(...) bytes, 256-byte aligned, control block zeroed;
+ * a smaller or missing workspace selects a kernel without split-K (same
+ * results within fp32 accumulation order, slower for 64 < M < 1024). */
 int cbq_w8a16_linear(const void* x, int act_dtype, const int8_t* wq,
                      const void* scales, const void* bias,
                      const int64_t* outlier_cols, int64_t n_out,

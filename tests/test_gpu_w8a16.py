@@ -119,7 +119,9 @@ def test_golden(meta, arr):
                                    (1031, 192, 1000), (1024, 64, 256), (1290, 448, 520),
                                    (1024, 80, 300), (1100, 208, 264),              # K % 64 != 0
                                    (7, 2048, 8200), (1, 4096, 4000), (13, 1024, 9000),  # k_stream1
-                                   (24, 4096, 5000), (64, 2048, 6000), (40, 1024, 9000)])  # k_stream
+                                   (24, 4096, 5000), (64, 2048, 6000), (40, 1024, 9000),  # k_stream
+                                   (200, 4096, 1000), (700, 1024, 3000), (500, 2048, 2600),  # split-K
+                                   (800, 256, 3000)])                               # DMA, M < 1024
 def test_mfma_shapes(dt, M, K, N):
     run_and_check(M, K, N, dt, seed=M * 31 + K + N, bias=(M % 2 == 1))
 
@@ -142,6 +144,27 @@ def test_general_path_odd_k(M, K, N):
 def test_general_path_fp32_and_unaligned():
     run_and_check(20, 128, 64, torch.float32, seed=2, bias=True, n_out=2)
     run_and_check(40, 256, 72, torch.float16, seed=3, bias=True, x_offset=3)
+
+
+def test_splitk_workspace_fallback():
+    """A control-block-only workspace selects the no-split kernel; same
+    results within fp32 accumulation order."""
+    from cublade_amd import _abi
+    M, K, N = 256, 2048, 1500
+    x, wq, s, b, _, _ = make_case(M, K, N, torch.float16, 21, bias=True)
+    xd, wd, sd, bd = x.to(DEV), wq.to(DEV), s.to(DEV), b.to(DEV)
+    L = _abi.lib()
+    assert L.cbq_w8a16_ws_bytes(M, N, K, 0) > _abi.WS_CTRL_BYTES     # split-K shape
+    y_split = w8a16(xd, wd, sd, bd)
+    y_small = torch.empty_like(y_split)
+    ws = torch.zeros(_abi.WS_CTRL_BYTES, dtype=torch.uint8, device=DEV)
+    rc = L.cbq_w8a16_linear(_abi.ptr(xd), CODE_OF[torch.float16], _abi.ptr(wd), _abi.ptr(sd),
+                            _abi.ptr(bd), None, 0, None, M, N, K, _abi.ptr(ws), ws.numel(),
+                            _abi.ptr(y_small), _abi.stream_handle(xd.device))
+    assert rc == 0
+    torch.testing.assert_close(y_small.float(), y_split.float(), **TOL)
+    ref = oracle_y(bits(x), oracle.F16, wq.numpy(), bits(s), bits(b), rows=np.array([0, 99, 255]))
+    np.testing.assert_allclose(y_split.float().cpu().numpy()[[0, 99, 255]], ref, **TOL)
 
 
 def test_mfma_bit_stability_across_calls():

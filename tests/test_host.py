@@ -87,7 +87,13 @@ def test_workspace_sizes():
     assert L.cbq_quant_tensor_ws_bytes() == C + 4 * 2048
     big = L.cbq_quant_int8_channel_ws_bytes(28672, 8192, 1)
     assert big >= C + 8192 * 4 * 2 and big < 64 << 20
-    assert L.cbq_w8a16_ws_bytes(16, 11008, 4096, 0) >= C
+    assert L.cbq_w8a16_ws_bytes(16, 11008, 4096, 0) == C
+    assert L.cbq_w8a16_ws_bytes(4096, 11008, 4096, 0) == C
+    # split-K tile path (64 < M < 1024): 4 k-ranges x 43 tiles of 256 KiB
+    # fp32 partials (256 CUs, also the CPU-only fallback count)
+    assert L.cbq_w8a16_ws_bytes(256, 11008, 4096, 0) == C + 4 * 43 * 256 * 1024
+    assert L.cbq_w8a16_ws_bytes(512, 11008, 4096, 3) == C + 2 * 86 * 256 * 1024
+    assert L.cbq_w8a16_ws_bytes(256, 11008, 4000, 0) == C      # K % 64 != 0
 
 
 def test_loader_memoises_failures(tmp_path):
