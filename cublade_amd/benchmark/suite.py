@@ -8,7 +8,7 @@ groups): per-tensor quant 2N read (amax) + 2N read + N written + 4 (cast);
 row / group quant 2N + N + 4C (one pass); column quant 2N + 2N + N + 4F (two
 passes); dequant N + 2N + 4 * scales. W8A16: 2 * M * N * K FLOPs.
 
-    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5 [--json out.json]
+    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5,f1 [--json out.json]
 """
 from __future__ import annotations
 
@@ -92,13 +92,49 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
             out.append(r)
             print(json.dumps(r), flush=True)
             del layer, xd
+    if "f1" in selected:
+        # LLaMA-style MLP block, down(silu(gate(x)) * up(x)), 4096 -> 11008 ->
+        # 4096, fp16, random N(0, 0.02) weights: W8A16 (quantize_model) next
+        # to the fp16 block (PyTorch's own GEMMs).
+        import torch.nn as nn
+        from cublade_amd.quantization import quantize_model
+
+        class Mlp(nn.Module):
+            def __init__(self):
+                super().__init__()
+                self.gate_proj = nn.Linear(4096, 11008, bias=False)
+                self.up_proj = nn.Linear(4096, 11008, bias=False)
+                self.down_proj = nn.Linear(11008, 4096, bias=False)
+
+            def forward(self, t):
+                return self.down_proj(torch.nn.functional.silu(self.gate_proj(t)) * self.up_proj(t))
+
+        g = torch.Generator().manual_seed(5)
+        block = Mlp()
+        with torch.no_grad():
+            for prm in block.parameters():
+                prm.copy_(0.02 * torch.randn(prm.shape, generator=g))
+        block = block.half().to(dev).eval()
+        qblock = quantize_model(block, "w8a16", inplace=False)
+        for M in (16, 256, 4096):
+            x = torch.randn(M, 4096, generator=g).half().to(dev)
+            flops = 3 * 2.0 * M * 4096 * 11008
+            with torch.no_grad():
+                us_q = time_op(lambda: qblock(x), reps, warmup, flush)
+                us_f = time_op(lambda: block(x), reps, warmup, flush)
+            rq = _rec("f1", f"mlp_w8a16_m{M}", us_q, 3 * 4096 * 11008, flops)
+            rf = _rec("f1", f"mlp_fp16_m{M}", us_f, 3 * 2 * 4096 * 11008, flops)
+            rq["speedup_vs_fp16"] = round(statistics.median(us_f) / statistics.median(us_q), 3)
+            out += [rq, rf]
+            print(json.dumps(rq), json.dumps(rf), sep="\n", flush=True)
+        del block, qblock
     torch.cuda.synchronize()
     return out
 
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,f1")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--json", default=None)

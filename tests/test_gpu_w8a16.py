@@ -290,3 +290,96 @@ def test_toy_flow_cpu_model():
     with torch.no_grad():
         y_g = qg(x.to(DEV)).cpu()
     torch.testing.assert_close(y_g, y_q, rtol=1e-4, atol=1e-4)
+
+
+class _LlamaMLP(nn.Module):
+    """LLaMA-style MLP block: down(silu(gate(x)) * up(x)), 4096 -> 11008 -> 4096."""
+
+    def __init__(self, d=4096, h=11008, bias=False):
+        super().__init__()
+        self.gate_proj = nn.Linear(d, h, bias=bias)
+        self.up_proj = nn.Linear(d, h, bias=bias)
+        self.down_proj = nn.Linear(h, d, bias=bias)
+
+    def forward(self, x):
+        return self.down_proj(torch.nn.functional.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+def _dequant_forward(block, x):
+    """Forward of a block with each W8A16 layer replaced by an fp32 product
+    x @ (wq * s)^T (+ bias) rounded once to fp16, i.e. the layer's contract;
+    SiLU and the product run in fp16 as in the model."""
+    from cublade_amd.quantization import cuBladeW8A16LinearLayer
+
+    def lin(m, t):
+        if isinstance(m, cuBladeW8A16LinearLayer):
+            w = m.int8_weights.float() * m.scales.float()[:, None]
+            b = None if m.bias is None else m.bias.float()
+        else:
+            w, b = m.weight.float(), None if m.bias is None else m.bias.float()
+        y = t.float() @ w.t().contiguous()
+        return (y if b is None else y + b).half()
+    return lin(block.down_proj, torch.nn.functional.silu(lin(block.gate_proj, x)) *
+               lin(block.up_proj, x))
+
+
+def test_llama_mlp_stack_end_to_end():
+    """quantize_model on two LLaMA-style MLP blocks (4096 -> 11008 -> 4096) in
+    fp16 on the GPU, with a target filter and an exclude filter, one biased
+    block, and forwards at M = 16 / 256 / 1024 (the streaming, split-K and
+    tile kernels). Every W8A16 layer is checked at its real input inside the
+    stack against an fp32 product rounded once (rtol/atol 1e-2), the chained
+    output against the same computation in norm, and one layer against the
+    oracle."""
+    from cublade_amd.quantization import cuBladeW8A16LinearLayer, quantize_model
+    torch.manual_seed(7)
+    model = nn.Sequential(_LlamaMLP(), _LlamaMLP(bias=True))
+    for p in model.parameters():
+        nn.init.normal_(p, std=0.02)
+    model = model.half().to(DEV)
+    qm = quantize_model(model, "w8a16", target_modules=["proj"], exclude_modules=["1.down"],
+                        inplace=False)
+    for name in ("0.gate_proj", "0.up_proj", "0.down_proj", "1.gate_proj", "1.up_proj"):
+        layer = qm.get_submodule(name)
+        assert isinstance(layer, cuBladeW8A16LinearLayer), name
+        assert layer.int8_weights.is_cuda and layer.scales.is_cuda
+        assert layer.int8_weights.dtype == torch.int8 and layer.scales.dtype == torch.float16
+    assert isinstance(qm.get_submodule("1.down_proj"), nn.Linear)
+    assert qm[1].up_proj.bias is not None
+    # every W8A16 layer's input and output inside the stack
+    seen = []
+    hooks = [m.register_forward_hook(lambda mod, inp, out: seen.append((mod, inp[0], out)))
+             for m in qm.modules() if isinstance(m, cuBladeW8A16LinearLayer)]
+    for M in (16, 256, 1024):
+        x = torch.randn(M, 4096, device=DEV).half()
+        seen.clear()
+        with torch.no_grad():
+            y = qm(x)
+            y_fp = model(x).float()
+            ref = _dequant_forward(qm[1], _dequant_forward(qm[0], x)).float()
+        assert y.dtype == torch.float16 and tuple(y.shape) == (M, 4096)
+        assert len(seen) == 5
+        # each layer at its real input: fp32 product rounded once (north-star gate)
+        for mod, inp, out in seen:
+            w = mod.int8_weights.float() * mod.scales.float()[:, None]
+            r = inp.float() @ w.t().contiguous()
+            if mod.bias is not None:
+                r = r + mod.bias.float()
+            torch.testing.assert_close(out.float(), r.half().float(), **TOL)
+        # the chained stack: ulp-level differences of the fp16 intermediates only
+        assert ((y.float() - ref).norm() / ref.norm()).item() < 2e-3
+        # quantization error of the whole stack next to the fp16 model: the
+        # per-channel INT8 step is ~amax/127 ~ 4 sigma/127, i.e. ~0.9% relative
+        # error per layer; five quantized layers compound to ~2.5%
+        rel = ((y.float() - y_fp).norm() / y_fp.norm()).item()
+        assert rel < 5e-2, rel
+    for h in hooks:
+        h.remove()
+    # the first gate projection against the oracle on a few rows
+    x = torch.randn(256, 4096).half()
+    with torch.no_grad():
+        y0 = qm[0].gate_proj(x.to(DEV))
+    rows = np.array([0, 17, 255], np.int64)
+    ref0 = oracle_y(bits(x), oracle.F16, bits(qm[0].gate_proj.int8_weights),
+                    bits(qm[0].gate_proj.scales), rows=rows)
+    np.testing.assert_allclose(y0.float().cpu().numpy()[rows], ref0, **TOL)
