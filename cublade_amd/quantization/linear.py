@@ -10,10 +10,11 @@ never runs it, and raises if the HIP library is unavailable.
 
 Storage (buffer names and dtypes as in the reference, linear.py:25-33):
   int8_weights  int8 [out, in]. With outliers, the outlier columns hold 0
-                (the reference stores only the normal columns, [out, in -
-                n_out]; that layout is accepted by load_state_dict and
-                expanded). Codes and scales are identical either way: a zero
-                column changes no row maximum.
+                in memory; state_dict() saves the reference's layout (only
+                the normal columns, [out, in - n_out]) and load_state_dict
+                expands it again. Codes and scales are identical either way:
+                a zero column changes no row maximum. Any in - n_out works
+                (the reference needs it 16-byte aligned).
   scales        [out] in the layer dtype (fp32 scale rounded to it, :79-81)
   outlier_weights [out, n_out] in the weight's dtype, normal_cols /
                 outlier_cols int64 (None without outliers)
@@ -115,6 +116,16 @@ class cuBladeW8A16LinearLayer(nn.Module):
         if self.bias is not None:
             y2d = y2d + self.bias.to(y2d.dtype)
         return y2d
+
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        # Save the reference's layout (linear.py:48-66): with outliers,
+        # int8_weights holds only the normal columns, [out, in - n_out].
+        super()._save_to_state_dict(destination, prefix, keep_vars)
+        key = prefix + "int8_weights"
+        if key in destination and self.normal_cols is not None and self.outlier_cols is not None \
+                and self.outlier_cols.numel() > 0:
+            wq = destination[key]
+            destination[key] = wq[:, self.normal_cols.to(wq.device)].contiguous()
 
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
                               unexpected_keys, error_msgs):

@@ -235,14 +235,35 @@ def test_layer_outlier_mode_and_state_dict():
     cpu.load_state_dict({k: v.cpu() for k, v in layer.state_dict().items()})
     y_cpu = cpu(x.float()).detach().float().numpy()
     np.testing.assert_allclose(y_cpu, ref, **TOL)
-    # reference compact layout [N, K - n_out] loads and gives the same output
+    # the saved layout is the reference's compact [N, K - n_out]; it loads
+    # back and gives the same output
     sd = {k: v.cpu() for k, v in layer.state_dict().items()}
-    sd["int8_weights"] = sd["int8_weights"][:, normal].contiguous()
+    assert tuple(sd["int8_weights"].shape) == (N, K - len(oc))
+    assert torch.equal(sd["int8_weights"], layer.int8_weights.cpu()[:, normal])
     fresh = cuBladeW8A16LinearLayer(K, N, bias=True, dtype=torch.float16, handle_outliers=True)
     fresh.load_state_dict(sd)
     fresh = fresh.to(DEV)
     assert torch.equal(fresh.int8_weights, layer.int8_weights)
     assert torch.equal(fresh(x.to(DEV)), y)
+
+
+def test_outlier_mode_unaligned_normal_width():
+    """K - n_out not 16-byte aligned (4096 - 3 columns) works on the MFMA path;
+    the reference rejects it (quantize_int8.cu:496-498)."""
+    from cublade_amd.quantization import cuBladeW8A16LinearLayer
+    g = torch.Generator().manual_seed(13)
+    K, N, M = 4096, 512, 64
+    w = 0.02 * torch.randn(N, K, generator=g)
+    oc = [10, 2000, 4095]
+    w[7, oc] = torch.tensor([8.0, -7.0, 9.5])
+    layer = cuBladeW8A16LinearLayer(K, N, bias=False, dtype=torch.float16, handle_outliers=True)
+    layer.quantize(w.half().to(DEV))
+    assert layer.outlier_cols.tolist() == oc and layer.normal_cols.numel() == K - 3
+    x = torch.randn(M, K, generator=g).half()
+    y = layer(x.to(DEV))
+    ref = oracle_y(bits(x), oracle.F16, bits(layer.int8_weights), bits(layer.scales), oc=oc,
+                   w_out=bits(layer.outlier_weights))
+    np.testing.assert_allclose(y.float().cpu().numpy(), ref, **TOL)
 
 
 def test_quantize_model_mlp():

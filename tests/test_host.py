@@ -214,16 +214,32 @@ def test_layer_cpu_branch_matches_oracle(outliers):
 def test_state_dict_compact_layout_expands():
     from cublade_amd.quantization import cuBladeW8A16LinearLayer
     src = _cpu_layer(16, 6, torch.float16, True, 7, outliers=(2, 11))
-    sd = src.state_dict()
-    normal = src.normal_cols
-    sd = dict(sd)
-    sd["int8_weights"] = sd["int8_weights"][:, normal].contiguous()   # reference layout
+    sd = src.state_dict()                 # the reference layout [out, in - n_out]
+    assert tuple(sd["int8_weights"].shape) == (6, 14)
     dst = cuBladeW8A16LinearLayer(16, 6, bias=True, dtype=torch.float16, handle_outliers=True)
     dst.load_state_dict(sd)
     assert torch.equal(dst.int8_weights, src.int8_weights)
     assert torch.equal(dst.outlier_cols, src.outlier_cols)
     x = torch.randn(3, 16)
     torch.testing.assert_close(dst(x), src(x))
+
+
+def test_state_dict_saves_reference_layout():
+    """With outliers, state_dict() holds the reference's compact
+    int8_weights [out, in - n_out] (linear.py:48-66); without, [out, in]."""
+    from cublade_amd.quantization import cuBladeW8A16LinearLayer
+    src = _cpu_layer(16, 6, torch.float16, True, 7, outliers=(2, 11))
+    sd = src.state_dict()
+    assert tuple(sd["int8_weights"].shape) == (6, 14)
+    assert torch.equal(sd["int8_weights"], src.int8_weights[:, src.normal_cols])
+    assert tuple(src.int8_weights.shape) == (6, 16)          # memory layout unchanged
+    assert set(sd) == {"int8_weights", "scales", "outlier_weights", "normal_cols",
+                       "outlier_cols", "bias"}
+    dst = cuBladeW8A16LinearLayer(16, 6, bias=True, dtype=torch.float16, handle_outliers=True)
+    dst.load_state_dict(sd)
+    assert torch.equal(dst.int8_weights, src.int8_weights)
+    plain = _cpu_layer(16, 6, torch.float16, True, 8, outliers=())
+    assert tuple(plain.state_dict()["int8_weights"].shape) == (6, 16)
 
 
 def test_oracle_not_imported_by_product():
