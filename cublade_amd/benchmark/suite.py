@@ -8,7 +8,7 @@ groups): per-tensor quant 2N read (amax) + 2N read + N written + 4 (cast);
 row / group quant 2N + N + 4C (one pass); column quant 2N + 2N + N + 4F (two
 passes); dequant N + 2N + 4 * scales. W8A16: 2 * M * N * K FLOPs.
 
-    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5,f1 [--json out.json]
+    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5,f1,f3 [--json out.json]
 """
 from __future__ import annotations
 
@@ -128,13 +128,52 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
             out += [rq, rf]
             print(json.dumps(rq), json.dumps(rf), sep="\n", flush=True)
         del block, qblock
+    if "f3" in selected:
+        # Non-default axes in place: groups along axis 0 of config 4's tensor
+        # and channels on the middle axis of config 3's tensor seen as
+        # [7, 4096, 8192]. Each is timed next to the transposing route
+        # (quantizers.py:122-132 / dequantizers.py:58-72): move the axis last,
+        # contiguous copy, the same kernels, copy back.
+        x = configs.c4_int8_group().to(dev)
+        n = x.numel()
+        G = n // 128
+        qkw = dict(dtype=torch.int8, mode="group", group_size=128, ch_axis=0)
+        q_and_dq("f3", x, qkw, 2 * n + n + 4 * G, n + 2 * n + 4 * G, "_group_axis0")
+        lkw = dict(dtype=torch.int8, mode="group", group_size=128, ch_axis=-1)
+
+        def group_via_copies():
+            qt = quantize_tensor(x.movedim(0, -1).contiguous(), **lkw)
+            return qt.data.movedim(-1, 0).contiguous()
+
+        r = _rec("f3", "quant_group_axis0_via_copies",
+                 time_op(group_via_copies, reps, warmup, flush), 2 * n + n + 4 * G)
+        r["speedup_in_place"] = round(r["us_median"] / out[-2]["us_median"], 3)
+        out.append(r)
+        print(json.dumps(r), flush=True)
+        del x
+        x = configs.c3_int8_channel().to(dev).view(7, 4096, 8192)
+        n, C = x.numel(), 4096
+        q_and_dq("f3", x, dict(dtype=torch.int8, mode="channel", ch_axis=1),
+                 2 * n + 2 * n + n + 4 * C, n + 2 * n + 4 * C, "_channel_axis1_3d")
+
+        def channel_via_copies():
+            qt = quantize_tensor(x.movedim(1, 0).contiguous(), dtype=torch.int8,
+                                 mode="channel", ch_axis=0)
+            return qt.data.movedim(0, 1).contiguous()
+
+        r = _rec("f3", "quant_channel_axis1_3d_via_copies",
+                 time_op(channel_via_copies, reps, warmup, flush), 2 * n + 2 * n + n + 4 * C)
+        r["speedup_in_place"] = round(r["us_median"] / out[-2]["us_median"], 3)
+        out.append(r)
+        print(json.dumps(r), flush=True)
+        del x
     torch.cuda.synchronize()
     return out
 
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,f1")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,f1,f3")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--json", default=None)

@@ -98,3 +98,70 @@ def dequantize_per_group_int8(
                                       _abi.ptr(y), out, _abi.stream_handle(q_grouped.device))
     _abi.check(rc, "dequantize_per_group_int8")
     return y
+
+
+def dequantize_per_channel_int8_nd(
+    q: torch.Tensor,
+    scale: torch.Tensor,
+    axis: int,
+    dtype: torch.dtype = torch.bfloat16,
+) -> torch.Tensor:
+    """Per-channel dequantization along any axis (scale (q.size(axis),)),
+    without copies; an extension of the reference's axis-0 mode."""
+    from .quantize_int8 import _axis_view
+    _check_q(q)
+    scale = check_scale(scale, q)
+    out = check_out_dtype(dtype)
+    if q.dim() < 1:
+        raise RuntimeError("q must have at least 1 dim")
+    axis = axis + q.dim() if axis < 0 else axis
+    if not 0 <= axis < q.dim():
+        raise RuntimeError(f"axis {axis} out of range for a {q.dim()}-D tensor")
+    outer, C, inner = _axis_view(q.shape, axis)
+    if scale.numel() != C:
+        raise RuntimeError(f"scale must have {C} elements (size({axis}) of q)")
+    y = torch.empty(q.shape, dtype=dtype, device=q.device)
+    if q.numel() == 0:
+        return y
+    L = _abi.lib()
+    with torch.cuda.device(q.device):
+        rc = L.cbq_dequant_int8_channel_nd(_abi.ptr(q), _abi.ptr(scale), outer, C, inner,
+                                           _abi.ptr(y), out, _abi.stream_handle(q.device))
+    _abi.check(rc, "dequantize_per_channel_int8_nd")
+    return y
+
+
+def dequantize_per_group_int8_nd(
+    q: torch.Tensor,
+    scale: torch.Tensor,
+    axis: int,
+    group_size: int,
+    dtype: torch.dtype = torch.bfloat16,
+) -> torch.Tensor:
+    """Per-group dequantization with groups along any axis (scales in the
+    reference's movedim order), without the copies of dequantizers.py:58-72."""
+    from .quantize_int8 import _axis_view
+    _check_q(q)
+    scale = check_scale(scale, q)
+    out = check_out_dtype(dtype)
+    axis = axis + q.dim() if axis < 0 else axis
+    if not 0 <= axis < q.dim():
+        raise RuntimeError(f"axis {axis} out of range for a {q.dim()}-D tensor")
+    if not 0 < group_size <= 4096:
+        raise RuntimeError(f"group_size must be in (0, 4096], got {group_size}")
+    outer, Lq, inner = _axis_view(q.shape, axis)
+    if Lq % group_size != 0:
+        raise RuntimeError(f"group_size {group_size} must evenly divide axis length {Lq}")
+    ng = outer * inner * (Lq // group_size)
+    if scale.numel() != ng:
+        raise RuntimeError(f"scale must have {ng} elements (one per group)")
+    y = torch.empty(q.shape, dtype=dtype, device=q.device)
+    if ng == 0:
+        return y
+    L = _abi.lib()
+    with torch.cuda.device(q.device):
+        rc = L.cbq_dequant_int8_group_nd(_abi.ptr(q), _abi.ptr(scale), outer, Lq, inner,
+                                         group_size, _abi.ptr(y), out,
+                                         _abi.stream_handle(q.device))
+    _abi.check(rc, "dequantize_per_group_int8_nd")
+    return y

@@ -106,3 +106,81 @@ def quantize_per_group_int8(
                                     _abi.ptr(q), _abi.ptr(scale), _abi.stream_handle(dev))
     _abi.check(rc, "quantize_per_group_int8")
     return q, scale
+
+
+def _axis_view(shape, axis: int) -> tuple[int, int, int]:
+    """(outer, length, inner) of an N-D shape around `axis`."""
+    outer = 1
+    for d in shape[:axis]:
+        outer *= int(d)
+    inner = 1
+    for d in shape[axis + 1:]:
+        inner *= int(d)
+    return outer, int(shape[axis]), inner
+
+
+def quantize_per_channel_int8_nd(
+    x: torch.Tensor,
+    axis: int,
+    eps: float = 1e-12,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-channel symmetric INT8 quantization along any axis of a contiguous
+    N-D tensor, without transposing copies: one scale per position of
+    `axis`, the maximum taken over all other dims. Returns (q int8 of x's
+    shape, scale float32 (x.size(axis),)). An extension of the reference,
+    whose channel mode is axis 0 only (quantizers.py:116-121)."""
+    code = check_float_input(x, allow_f32=True)
+    if x.dim() < 1:
+        raise RuntimeError("x must have at least 1 dim for per-channel quant")
+    axis = axis + x.dim() if axis < 0 else axis
+    if not 0 <= axis < x.dim():
+        raise RuntimeError(f"axis {axis} out of range for a {x.dim()}-D tensor")
+    dev = x.device
+    outer, C, inner = _axis_view(x.shape, axis)
+    q = torch.empty(x.shape, dtype=torch.int8, device=dev)
+    if x.numel() == 0:
+        return q, torch.zeros((C,), dtype=torch.float32, device=dev)
+    scale = torch.empty((C,), dtype=torch.float32, device=dev)
+    L = _abi.lib()
+    with torch.cuda.device(dev):
+        ws = _abi.workspace(dev, L.cbq_quant_int8_channel_nd_ws_bytes(outer, C, inner))
+        rc = L.cbq_quant_int8_channel_nd(_abi.ptr(x), code, outer, C, inner, float(eps),
+                                         _abi.ptr(ws), ws.numel(), _abi.ptr(q), _abi.ptr(scale),
+                                         _abi.stream_handle(dev))
+    _abi.check(rc, "quantize_per_channel_int8_nd")
+    return q, scale
+
+
+def quantize_per_group_int8_nd(
+    x: torch.Tensor,
+    axis: int,
+    group_size: int,
+    eps: float = 1e-12,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-group symmetric INT8 quantization with groups of `group_size`
+    consecutive positions along any axis of a contiguous N-D tensor, without
+    the reference's movedim / contiguous copies (quantizers.py:122-132).
+    Returns (q int8 of x's shape, scale float32 (num_groups,)) with the
+    scales in the reference's order (groups of x.movedim(axis, -1))."""
+    code = check_float_input(x, allow_f32=True)
+    axis = axis + x.dim() if axis < 0 else axis
+    if not 0 <= axis < x.dim():
+        raise RuntimeError(f"axis {axis} out of range for a {x.dim()}-D tensor")
+    if not 0 < group_size <= 4096:
+        raise RuntimeError(f"group_size must be in (0, 4096], got {group_size}")
+    dev = x.device
+    outer, Lx, inner = _axis_view(x.shape, axis)
+    if Lx % group_size != 0:
+        raise RuntimeError(f"group_size {group_size} must evenly divide axis length {Lx}")
+    q = torch.empty(x.shape, dtype=torch.int8, device=dev)
+    ng = outer * inner * (Lx // group_size)
+    scale = torch.empty((ng,), dtype=torch.float32, device=dev)
+    if ng == 0:
+        return q, scale
+    L = _abi.lib()
+    with torch.cuda.device(dev):
+        rc = L.cbq_quant_int8_group_nd(_abi.ptr(x), code, outer, Lx, inner, group_size,
+                                       float(eps), _abi.ptr(q), _abi.ptr(scale),
+                                       _abi.stream_handle(dev))
+    _abi.check(rc, "quantize_per_group_int8_nd")
+    return q, scale

@@ -95,6 +95,15 @@ template <> struct Raw8<kF32> { uint4 a, b; };
 
 template <int DT> constexpr int elem_bytes() { return DT == kF32 ? 4 : 2; }
 
+// Marks a held chunk as changed, so that a second conversion of it is
+// recomputed from the raw words instead of keeping the first conversion's
+// fp32 values live (which doubles the registers a held row or group needs).
+template <int DT>
+__device__ __forceinline__ void reload_barrier(Raw8<DT>& r) {
+  asm volatile("" : "+v"(r.a.x), "+v"(r.a.y), "+v"(r.a.z), "+v"(r.a.w));
+  if constexpr (DT == kF32) asm volatile("" : "+v"(r.b.x), "+v"(r.b.y), "+v"(r.b.z), "+v"(r.b.w));
+}
+
 template <int DT, bool NT = (CBQ_NT_LOADS != 0)>
 __device__ __forceinline__ Raw8<DT> ld8(const void* base, int64_t elem) {
   Raw8<DT> r;
@@ -287,6 +296,16 @@ __device__ __forceinline__ float block_max(float m, float* red) {
   for (int w = 1; w < static_cast<int>(blockDim.x) / kWave; ++w) r = fmaxf(r, red[w]);
   __syncthreads();
   return r;
+}
+
+// Workgroup order for grids whose neighbouring workgroups share cache lines
+// (scales of adjacent groups): the dispatcher deals workgroups to the 8 XCDs
+// round-robin, so hardware index b runs on XCD b % 8. The remap gives XCD k a
+// contiguous run of logical indices; the last nb % 8 indices map to
+// themselves.
+__device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t nb) {
+  const int64_t per = nb >> 3;
+  return b < (per << 3) ? (b & 7) * per + (b >> 3) : b;
 }
 
 // Reciprocal scale and stored scale, both correctly rounded fp32 divisions

@@ -24,6 +24,17 @@
 //                   per-column (axis 1) quant: partial column maxima per row
 //                   block, one finalize pass, then the cast with each
 //                   thread's eight column multipliers held in registers
+//   k_segmax / k_chan_finalize
+//                   per-channel maxima of an N-D tensor seen as
+//                   [outer, channels, inner] with inner >= 512: one wave per
+//                   contiguous run, then the maximum over outer (the cast is
+//                   k_cast_cols with inner columns per channel; shorter runs
+//                   take k_colmax). The reference supports ch_axis = 0 only.
+//   k_group_tile    groups along a non-last axis in place (the reference moves
+//                   the axis last with two copies, quantizers.py:122-132):
+//                   a workgroup holds one group x 512 inner positions in
+//                   registers, one pass over x
+//   k_group_strided the same for inner % 8 != 0 or unaligned buffers
 //
 // Numerics: see cbq_device.h. Every kernel guards its indices against the
 // sizes it is given; the entry points check shapes, dtypes and alignment.
@@ -343,10 +354,12 @@ __global__ __launch_bounds__(kBlock) void k_col_finalize(
   }
 }
 
+// inner: adjacent columns sharing one scale (1 for per-column scales; the
+// N-D channel path views [outer, channels, inner] as [outer, channels * inner]).
 template <int DT>
 __global__ __launch_bounds__(kBlock) void k_cast_cols(
     const void* __restrict__ x, int64_t rows, int64_t cols, int64_t RB, int vec,
-    const float* __restrict__ inv_c, int8_t* __restrict__ q) {
+    const float* __restrict__ inv_c, int64_t inner, int8_t* __restrict__ q) {
   const int64_t r0 = static_cast<int64_t>(blockIdx.y) * RB;
   const int64_t r1 = r0 + RB < rows ? r0 + RB : rows;
   if (vec) {
@@ -354,7 +367,7 @@ __global__ __launch_bounds__(kBlock) void k_cast_cols(
     if (c >= cols) return;
     float inv[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) inv[k] = inv_c[c + k];
+    for (int k = 0; k < 8; ++k) inv[k] = inv_c[(c + k) / inner];
     int64_t r = r0;
     for (; r + 4 <= r1; r += 4) {
       Raw8<DT> raw[4];
@@ -379,9 +392,203 @@ __global__ __launch_bounds__(kBlock) void k_cast_cols(
   } else {
     const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (c >= cols) return;
-    const float inv = inv_c[c];
+    const float inv = inv_c[c / inner];
     for (int64_t r = r0; r < r1; ++r)
       q[r * cols + c] = static_cast<int8_t>(q_int8(ld1<DT>(x, r * cols + c) * inv));
+  }
+}
+
+// Channel maxima of the N-D channel path: channel ch owns columns
+// [ch * inner, ch * inner + inner) of the partial maxima; one workgroup per
+// channel reduces its nrb * inner partials (block reduce), then writes inv
+// and scale.
+__global__ __launch_bounds__(kBlock) void k_chan_finalize(
+    const float* __restrict__ partial, int64_t nrb, int64_t cols, int64_t inner, float eps,
+    float* __restrict__ inv_out, float* __restrict__ scale) {
+  __shared__ float red[kBlock / kWave];
+  const int64_t ch = blockIdx.x;
+  float m = 0.0f;
+  const int64_t n = nrb * inner;
+  for (int64_t e = threadIdx.x; e < n; e += kBlock) {
+    const int64_t b = e / inner, j = e % inner;
+    m = fmaxf(m, partial[b * cols + ch * inner + j]);
+  }
+  m = block_max(m, red);
+  if (threadIdx.x == 0) {
+    const float inv = inv_scale(m, eps, kQmaxInt8);
+    inv_out[ch] = inv;
+    scale[ch] = 1.0f / inv;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Groups along a non-last axis: x viewed as [outer, len, inner], groups of G
+// consecutive positions along len. One thread per group (o, g, i) with i
+// fastest, so that a wave's loads of one position are contiguous in x. The
+// scale index follows the reference's movedim layout,
+// (o * inner + i) * (len / G) + g (quantizers.py:123-130).
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_group_strided(
+    const void* __restrict__ x, int64_t outer, int64_t len, int64_t inner, int64_t G, float eps,
+    int8_t* __restrict__ q, float* __restrict__ scale) {
+  const int64_t ng = len / G;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (t >= outer * ng * inner) return;
+  const int64_t i = t % inner, g = (t / inner) % ng, o = t / (inner * ng);
+  const int64_t base = (o * len + g * G) * inner + i;
+  float m = 0.0f;
+  for (int64_t k = 0; k < G; ++k) m = fmaxf(m, __builtin_fabsf(ld1<DT>(x, base + k * inner)));
+  const float inv = inv_scale(m, eps, kQmaxInt8);
+  scale[(o * inner + i) * ng + g] = 1.0f / inv;
+  for (int64_t k = 0; k < G; ++k)
+    q[base + k * inner] = static_cast<int8_t>(q_int8(ld1<DT>(x, base + k * inner) * inv));
+}
+
+// Groups along a non-last axis, tiled (inner % 8 == 0, 16-byte aligned x,
+// 8-byte aligned q). A workgroup of NW waves covers kGtCols adjacent inner
+// positions (64 lanes x 8) of one group: G = NW * rpt positions along len,
+// wave w holding positions w, w + NW, ..., so each load instruction of a wave
+// reads one contiguous 1 KiB (2-byte types) run of x. HOLD (rpt <= kGtHold):
+// the group stays in registers between the max and the cast, so x is read
+// once; otherwise the cast reads the tile again (L2 / Infinity Cache).
+// Logical workgroup index, after xcd_remap: g fastest, then the inner tile,
+// then o, so the scales of neighbouring groups - adjacent in the movedim
+// layout - are written from one XCD's L2.
+constexpr int kGtCols = kWave * 8;
+constexpr int kGtHold = 16;
+
+template <int DT, int NW, bool HOLD>
+__global__ __launch_bounds__(NW * kWave) void k_group_tile(
+    const void* __restrict__ x, int64_t len, int64_t inner, int64_t G, int rpt, int64_t ng,
+    int64_t tiles, int64_t nblocks, float eps, int8_t* __restrict__ q,
+    float* __restrict__ scale) {
+  const int64_t b = xcd_remap(blockIdx.x, nblocks);
+  const int64_t g = b % ng, ti = (b / ng) % tiles, o = b / (ng * tiles);
+  const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+  const int64_t i = ti * kGtCols + lane * 8;
+  const bool act = i < inner;
+  const int64_t base = (o * len + g * G + w) * inner + i;
+  const int64_t rs = static_cast<int64_t>(NW) * inner;
+  float m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  Raw8<DT> r[HOLD ? kGtHold : 8];
+  if constexpr (HOLD) {
+#pragma unroll
+    for (int k = 0; k < kGtHold; ++k)
+      if (k < rpt && act) r[k] = ld8<DT>(x, base + k * rs);
+#pragma unroll
+    for (int k = 0; k < kGtHold; ++k)
+      if (k < rpt && act) {
+        float f[8];
+        cvt8<DT>(r[k], f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) m[j] = fmaxf(m[j], __builtin_fabsf(f[j]));
+      }
+  } else if (act) {
+    for (int k0 = 0; k0 < rpt; k0 += 8) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (k0 + k < rpt) r[k] = ld8<DT>(x, base + (k0 + k) * rs);
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (k0 + k < rpt) {
+          float f[8];
+          cvt8<DT>(r[k], f);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) m[j] = fmaxf(m[j], __builtin_fabsf(f[j]));
+        }
+    }
+  }
+  if constexpr (NW > 1) {
+    __shared__ float4 red[NW][kWave][2];
+    red[w][lane][0] = make_float4(m[0], m[1], m[2], m[3]);
+    red[w][lane][1] = make_float4(m[4], m[5], m[6], m[7]);
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      const float4 a = red[v][lane][0], c = red[v][lane][1];
+      m[0] = fmaxf(m[0], a.x); m[1] = fmaxf(m[1], a.y); m[2] = fmaxf(m[2], a.z);
+      m[3] = fmaxf(m[3], a.w); m[4] = fmaxf(m[4], c.x); m[5] = fmaxf(m[5], c.y);
+      m[6] = fmaxf(m[6], c.z); m[7] = fmaxf(m[7], c.w);
+    }
+  }
+  if (!act) return;
+  float inv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) inv[j] = inv_scale(m[j], eps, kQmaxInt8);
+  if (w == 0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) scale[(o * inner + i + j) * ng + g] = 1.0f / inv[j];
+  }
+  if constexpr (HOLD) {
+#pragma unroll
+    for (int k = 0; k < kGtHold; ++k)
+      if (k < rpt) {
+        float f[8];
+        reload_barrier<DT>(r[k]);
+        cvt8<DT>(r[k], f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] *= inv[j];
+        stg8(q + base + k * rs, pack8_int8(f, 1.0f));
+      }
+  } else {
+    for (int k0 = 0; k0 < rpt; k0 += 8) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (k0 + k < rpt) r[k] = ld8<DT>(x, base + (k0 + k) * rs);
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (k0 + k < rpt) {
+          float f[8];
+          cvt8<DT>(r[k], f);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) f[j] *= inv[j];
+          stg8(q + base + (k0 + k) * rs, pack8_int8(f, 1.0f));
+        }
+    }
+  }
+}
+
+// Segment maxima for the N-D channel path when inner is long: x viewed as
+// segs = outer * channels contiguous segments of inner elements; one wave per
+// segment (grid-stride over waves), so partial is [outer, channels] and the
+// channel maxima come from k_chan_finalize with inner = 1. vec: inner % 8 == 0
+// and 16-byte aligned x; a wave then reads 1 KiB (2-byte types) per load.
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_segmax(
+    const void* __restrict__ x, int64_t segs, int64_t inner, int vec,
+    float* __restrict__ partial) {
+  constexpr int kWpb = kBlock / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kWpb;
+  for (int64_t sg = static_cast<int64_t>(blockIdx.x) * kWpb + threadIdx.x / kWave; sg < segs;
+       sg += nwaves) {
+    const int64_t e0 = sg * inner;
+    float m = 0.0f;
+    if (vec) {
+      const int64_t n8 = inner >> 3;
+      int64_t c = lane;
+      for (; c + 3 * kWave < n8; c += 4 * kWave) {
+        Raw8<DT> raw[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) raw[u] = ld8<DT>(x, e0 + (c + u * kWave) * 8);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          float f[8];
+          cvt8<DT>(raw[u], f);
+          m = absmax8(f, m);
+        }
+      }
+      for (; c < n8; c += kWave) {
+        float f[8];
+        cvt8<DT>(ld8<DT>(x, e0 + c * 8), f);
+        m = absmax8(f, m);
+      }
+    } else {
+      for (int64_t e = lane; e < inner; e += kWave) m = fmaxf(m, __builtin_fabsf(ld1<DT>(x, e0 + e)));
+    }
+    m = group_max<kWave>(m);
+    if (lane == 0) partial[sg] = m;
   }
 }
 
@@ -528,19 +735,100 @@ size_t col_ws_bytes(int64_t rows, int64_t cols) {
   return CBQ_WS_CTRL_BYTES + static_cast<size_t>(nrb) * cols * 4 + static_cast<size_t>(cols) * 4;
 }
 
+// Column path: per-column scales (inner == 1), or per-channel scales of the
+// [rows, cols / inner, inner] view (inner adjacent columns per channel).
 template <int DT>
-int cols_quant_t(const void* x, int64_t rows, int64_t cols, float eps, void* ws, int8_t* q,
-                 float* scale, hipStream_t s) {
+int cols_quant_t(const void* x, int64_t rows, int64_t cols, int64_t inner, float eps, void* ws,
+                 int8_t* q, float* scale, hipStream_t s, const char* what) {
   const bool vec = (cols % 8 == 0) && aligned(x, 16) && aligned(q, 8);
   const ColGeom g = col_geom(rows, cols, vec);
   float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + CBQ_WS_CTRL_BYTES);
   float* inv = partial + g.nrb * cols;
   const dim3 grid2(static_cast<unsigned>(g.col_blocks), static_cast<unsigned>(g.nrb));
   k_colmax<DT><<<grid2, dim3(kBlock), 0, s>>>(x, rows, cols, g.RB, vec ? 1 : 0, partial);
-  k_col_finalize<<<dim3(static_cast<unsigned>(cdiv(cols, kFinCols))), dim3(kBlock), 0, s>>>(
-      partial, g.nrb, cols, eps, inv, scale);
-  k_cast_cols<DT><<<grid2, dim3(kBlock), 0, s>>>(x, rows, cols, g.RB, vec ? 1 : 0, inv, q);
-  return launch_status("cbq_quant_int8_channel");
+  if (inner == 1)
+    k_col_finalize<<<dim3(static_cast<unsigned>(cdiv(cols, kFinCols))), dim3(kBlock), 0, s>>>(
+        partial, g.nrb, cols, eps, inv, scale);
+  else
+    k_chan_finalize<<<dim3(static_cast<unsigned>(cols / inner)), dim3(kBlock), 0, s>>>(
+        partial, g.nrb, cols, inner, eps, inv, scale);
+  k_cast_cols<DT><<<grid2, dim3(kBlock), 0, s>>>(x, rows, cols, g.RB, vec ? 1 : 0, inv, inner, q);
+  return launch_status(what);
+}
+
+// Launch shape of k_group_tile for group size G: NW = the largest power of
+// two <= 8 dividing G, rpt = G / NW positions per wave.
+int group_tile_waves(int64_t G) { return G % 8 == 0 ? 8 : G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1; }
+
+template <int DT, int NW>
+void launch_group_tile(const void* x, int64_t outer, int64_t len, int64_t inner, int64_t G,
+                       float eps, int8_t* q, float* scale, hipStream_t s) {
+  const int64_t ng = len / G, tiles = cdiv(inner, kGtCols);
+  const int64_t nblocks = outer * tiles * ng;
+  const int rpt = static_cast<int>(G / NW);
+  const dim3 grid(static_cast<unsigned>(nblocks)), block(NW * kWave);
+  if (rpt <= kGtHold)
+    k_group_tile<DT, NW, true><<<grid, block, 0, s>>>(x, len, inner, G, rpt, ng, tiles, nblocks,
+                                                      eps, q, scale);
+  else
+    k_group_tile<DT, NW, false><<<grid, block, 0, s>>>(x, len, inner, G, rpt, ng, tiles, nblocks,
+                                                       eps, q, scale);
+}
+
+template <int DT>
+int group_strided_t(const void* x, int64_t outer, int64_t len, int64_t inner, int64_t G,
+                    float eps, int8_t* q, float* scale, hipStream_t s, const char* what) {
+  const int64_t ng = len / G;
+  const bool tile = inner % 8 == 0 && aligned(x, 16) && aligned(q, 8) &&
+                    outer * cdiv(inner, kGtCols) * ng < (1LL << 31);
+  if (tile) {
+    switch (group_tile_waves(G)) {
+      case 8: launch_group_tile<DT, 8>(x, outer, len, inner, G, eps, q, scale, s); break;
+      case 4: launch_group_tile<DT, 4>(x, outer, len, inner, G, eps, q, scale, s); break;
+      case 2: launch_group_tile<DT, 2>(x, outer, len, inner, G, eps, q, scale, s); break;
+      default: launch_group_tile<DT, 1>(x, outer, len, inner, G, eps, q, scale, s); break;
+    }
+    return launch_status(what);
+  }
+  const int64_t threads = outer * ng * inner;
+  k_group_strided<DT><<<dim3(static_cast<unsigned>(cdiv(threads, kBlock))), dim3(kBlock), 0, s>>>(
+      x, outer, len, inner, G, eps, q, scale);
+  return launch_status(what);
+}
+
+// N-D channel path, inner >= kSegInner: segment maxima (one wave per
+// contiguous run of inner elements), channel maxima over outer, then the
+// column cast with inner adjacent columns per channel. Shorter inner runs
+// take the column path (column maxima per row block).
+constexpr int64_t kSegInner = 512;
+constexpr int64_t kSegMaxWg = 2048;
+
+size_t seg_ws_bytes(int64_t outer, int64_t channels) {
+  return CBQ_WS_CTRL_BYTES + static_cast<size_t>(outer * channels + channels) * 4;
+}
+
+size_t channel_nd_ws_bytes(int64_t outer, int64_t channels, int64_t inner) {
+  return inner >= kSegInner ? seg_ws_bytes(outer, channels) : col_ws_bytes(outer, channels * inner);
+}
+
+template <int DT>
+int seg_quant_t(const void* x, int64_t outer, int64_t channels, int64_t inner, float eps,
+                void* ws, int8_t* q, float* scale, hipStream_t s, const char* what) {
+  const int64_t segs = outer * channels, cols = channels * inner;
+  float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + CBQ_WS_CTRL_BYTES);
+  float* inv = partial + segs;
+  const bool seg_vec = inner % 8 == 0 && aligned(x, 16);
+  int64_t wg = cdiv(segs, kBlock / kWave);
+  if (wg > kSegMaxWg) wg = kSegMaxWg;
+  k_segmax<DT><<<dim3(static_cast<unsigned>(wg)), dim3(kBlock), 0, s>>>(x, segs, inner,
+                                                                      seg_vec ? 1 : 0, partial);
+  k_chan_finalize<<<dim3(static_cast<unsigned>(channels)), dim3(kBlock), 0, s>>>(
+      partial, outer, channels, 1, eps, inv, scale);
+  const bool vec = (cols % 8 == 0) && aligned(x, 16) && aligned(q, 8);
+  const ColGeom g = col_geom(outer, cols, vec);
+  const dim3 grid2(static_cast<unsigned>(g.col_blocks), static_cast<unsigned>(g.nrb));
+  k_cast_cols<DT><<<grid2, dim3(kBlock), 0, s>>>(x, outer, cols, g.RB, vec ? 1 : 0, inv, inner, q);
+  return launch_status(what);
 }
 
 }  // namespace
@@ -586,9 +874,53 @@ extern "C" int cbq_quant_int8_channel(const void* x, int dtype, int64_t rows, in
               "%s: axis 1 needs a 16-byte aligned workspace of %zu bytes, got %zu", what, need,
               ws_bytes);
   switch (dtype) {
-    case kF16: return cols_quant_t<kF16>(x, rows, cols, eps, ws, q, scale, as_stream(stream));
-    case kBF16: return cols_quant_t<kBF16>(x, rows, cols, eps, ws, q, scale, as_stream(stream));
-    default: return cols_quant_t<kF32>(x, rows, cols, eps, ws, q, scale, as_stream(stream));
+    case kF16: return cols_quant_t<kF16>(x, rows, cols, 1, eps, ws, q, scale, as_stream(stream), what);
+    case kBF16: return cols_quant_t<kBF16>(x, rows, cols, 1, eps, ws, q, scale, as_stream(stream), what);
+    default: return cols_quant_t<kF32>(x, rows, cols, 1, eps, ws, q, scale, as_stream(stream), what);
+  }
+}
+
+extern "C" size_t cbq_quant_int8_channel_nd_ws_bytes(int64_t outer, int64_t channels,
+                                                     int64_t inner) {
+  if (outer <= 1 || channels <= 0 || inner <= 0) return CBQ_WS_CTRL_BYTES;
+  return channel_nd_ws_bytes(outer, channels, inner);
+}
+
+extern "C" int cbq_quant_int8_channel_nd(const void* x, int dtype, int64_t outer,
+                                         int64_t channels, int64_t inner, float eps, void* ws,
+                                         size_t ws_bytes, int8_t* q, float* scale,
+                                         cbq_stream_t stream) {
+  clear_error();
+  const char* what = "cbq_quant_int8_channel_nd";
+  CBQ_REQUIRE(valid_dtype(dtype, true), "%s: unsupported input dtype code %d", what, dtype);
+  CBQ_REQUIRE(outer >= 0 && channels >= 0 && inner >= 0, "%s: negative shape", what);
+  if (outer == 0 || channels == 0 || inner == 0) return CBQ_OK;
+  CBQ_REQUIRE(x && q && scale, "%s: null pointer", what);
+  if (outer == 1)   // channel axis leading: one row per channel
+    return rows_quant(x, dtype, channels, inner, eps, q, scale, as_stream(stream), what);
+  const size_t need = channel_nd_ws_bytes(outer, channels, inner);
+  CBQ_REQUIRE(ws && ws_bytes >= need && aligned(ws, 16),
+              "%s: needs a 16-byte aligned workspace of %zu bytes, got %zu", what, need, ws_bytes);
+  CBQ_REQUIRE(channels <= 0x7fffffffLL, "%s: too many channels (%lld)", what,
+              (long long)channels);
+  const int64_t cols = channels * inner;
+  if (inner >= kSegInner) {
+    switch (dtype) {
+      case kF16:
+        return seg_quant_t<kF16>(x, outer, channels, inner, eps, ws, q, scale, as_stream(stream), what);
+      case kBF16:
+        return seg_quant_t<kBF16>(x, outer, channels, inner, eps, ws, q, scale, as_stream(stream), what);
+      default:
+        return seg_quant_t<kF32>(x, outer, channels, inner, eps, ws, q, scale, as_stream(stream), what);
+    }
+  }
+  switch (dtype) {
+    case kF16:
+      return cols_quant_t<kF16>(x, outer, cols, inner, eps, ws, q, scale, as_stream(stream), what);
+    case kBF16:
+      return cols_quant_t<kBF16>(x, outer, cols, inner, eps, ws, q, scale, as_stream(stream), what);
+    default:
+      return cols_quant_t<kF32>(x, outer, cols, inner, eps, ws, q, scale, as_stream(stream), what);
   }
 }
 
@@ -604,4 +936,29 @@ extern "C" int cbq_quant_int8_group(const void* x, int dtype, int64_t num_groups
   if (num_groups == 0) return CBQ_OK;
   CBQ_REQUIRE(x && q && scale, "%s: null pointer", what);
   return rows_quant(x, dtype, num_groups, group_size, eps, q, scale, as_stream(stream), what);
+}
+
+extern "C" int cbq_quant_int8_group_nd(const void* x, int dtype, int64_t outer, int64_t len,
+                                       int64_t inner, int64_t group_size, float eps, int8_t* q,
+                                       float* scale, cbq_stream_t stream) {
+  clear_error();
+  const char* what = "cbq_quant_int8_group_nd";
+  CBQ_REQUIRE(valid_dtype(dtype, true), "%s: unsupported input dtype code %d", what, dtype);
+  CBQ_REQUIRE(group_size > 0 && group_size <= 4096, "%s: group_size must be in (0, 4096], got %lld",
+              what, (long long)group_size);
+  CBQ_REQUIRE(outer >= 0 && len >= 0 && inner >= 0, "%s: negative shape", what);
+  CBQ_REQUIRE(len % group_size == 0, "%s: group_size %lld must divide the axis length %lld", what,
+              (long long)group_size, (long long)len);
+  if (outer == 0 || len == 0 || inner == 0) return CBQ_OK;
+  CBQ_REQUIRE(x && q && scale, "%s: null pointer", what);
+  CBQ_REQUIRE(cdiv(outer * (len / group_size) * inner, kBlock) < (1LL << 31),
+              "%s: too many groups", what);
+  if (inner == 1)   // groups along the last axis are contiguous rows
+    return rows_quant(x, dtype, outer * (len / group_size), group_size, eps, q, scale,
+                      as_stream(stream), what);
+  switch (dtype) {
+    case kF16: return group_strided_t<kF16>(x, outer, len, inner, group_size, eps, q, scale, as_stream(stream), what);
+    case kBF16: return group_strided_t<kBF16>(x, outer, len, inner, group_size, eps, q, scale, as_stream(stream), what);
+    default: return group_strided_t<kF32>(x, outer, len, inner, group_size, eps, q, scale, as_stream(stream), what);
+  }
 }

@@ -16,6 +16,8 @@ from cublade_amd.bindings.hip.dequantize_int8 import (
     dequantize_per_tensor_int8 as _hip_dequant_int8_tensor,
     dequantize_per_channel_int8 as _hip_dequant_int8_channel,
     dequantize_per_group_int8 as _hip_dequant_int8_group,
+    dequantize_per_channel_int8_nd as _hip_dequant_int8_channel_nd,
+    dequantize_per_group_int8_nd as _hip_dequant_int8_group_nd,
 )
 
 _INT8_DTYPES = (torch.int8,)
@@ -52,22 +54,31 @@ def dequantize_tensor(qt: QuantizedTensor) -> torch.Tensor:
             axis = channel_kernel_axis(qt.data.dim(), qt.axis)
             if axis == 0:
                 return _hip_dequant_int8_channel(qt.data, qt.scale, qt.original_dtype)
-            F = qt.data.shape[-1]
-            y2 = _hip_dequant_int8_channel(qt.data.view(-1, F), qt.scale, qt.original_dtype,
-                                           axis=1)
-            return y2.view(qt.data.shape)
+            if axis == 1:
+                F = qt.data.shape[-1]
+                y2 = _hip_dequant_int8_channel(qt.data.view(-1, F), qt.scale,
+                                               qt.original_dtype, axis=1)
+                return y2.view(qt.data.shape)
+            return _hip_dequant_int8_channel_nd(qt.data, qt.scale, qt.axis, qt.original_dtype)
         if qt.mode == "group":
             if qt.group_size is None:
                 raise ValueError("INT8 group dequant needs qt.group_size")
-            moved = qt.data.movedim(qt.axis, -1).contiguous()
-            lead, F = moved.shape[:-1], moved.shape[-1]
+            q = qt.data
+            ax = qt.axis + q.dim() if qt.axis < 0 else qt.axis
+            if not 0 <= ax < max(q.dim(), 1):
+                raise IndexError(f"axis {qt.axis} out of range for a {q.dim()}-D tensor")
+            F = q.shape[ax] if q.dim() else 1
             if F % qt.group_size != 0:
                 raise ValueError(
                     f"group_size {qt.group_size} must evenly divide axis length {F}"
                 )
-            y_grouped = _hip_dequant_int8_group(moved.view(-1, qt.group_size), qt.scale,
-                                                qt.group_size, qt.original_dtype)
-            return y_grouped.view(*lead, F).movedim(-1, qt.axis).contiguous()
+            if q.dim() == 0 or ax == q.dim() - 1:
+                y_grouped = _hip_dequant_int8_group(q.reshape(-1, qt.group_size), qt.scale,
+                                                    qt.group_size, qt.original_dtype)
+                return y_grouped.view(q.shape)
+            # any other axis: strided groups, no movedim copies
+            # (dequantizers.py:61-72 makes two full copies here)
+            return _hip_dequant_int8_group_nd(q, qt.scale, ax, qt.group_size, qt.original_dtype)
         raise ValueError(f"Unsupported INT8 mode '{qt.mode}'")
 
     raise ValueError(f"No dequant kernel registered for dtype={qt.dtype}")

@@ -21,6 +21,8 @@ from cublade_amd.bindings.hip.quantize_int8 import (
     quantize_per_tensor_int8 as _hip_quant_int8_tensor,
     quantize_per_channel_int8 as _hip_quant_int8_channel,
     quantize_per_group_int8 as _hip_quant_int8_group,
+    quantize_per_channel_int8_nd as _hip_quant_int8_channel_nd,
+    quantize_per_group_int8_nd as _hip_quant_int8_group_nd,
 )
 
 # (mode, storage dtype) -> kernel wrapper (quantizers.py:22-27).
@@ -73,17 +75,20 @@ def _zero_scalar(device: torch.device) -> torch.Tensor:
 
 
 def channel_kernel_axis(ndim: int, ch_axis: int) -> int:
-    """Map a user ``ch_axis`` to the channel kernel's axis: 0 -> one scale per
-    row of the (size(0), numel/size(0)) view; the last axis of an N-D tensor
-    (N >= 2) -> one scale per column of the (numel/F, F) view."""
+    """Map a user ``ch_axis`` to the channel kernel path: 0 -> one scale per
+    row of the (size(0), numel/size(0)) view; 1 -> the last axis of an N-D
+    tensor (N >= 2), one scale per column of the (numel/F, F) view; 2 -> any
+    other axis, the N-D kernel on the (outer, C, inner) view. The reference
+    supports axis 0 only (quantizers.py:116-121); the others are extensions
+    without transposing copies."""
     ax = ch_axis + ndim if ch_axis < 0 else ch_axis
+    if not 0 <= ax < max(ndim, 1):
+        raise IndexError(f"ch_axis {ch_axis} out of range for a {ndim}-D tensor")
     if ax == 0:
         return 0
-    if ndim >= 2 and ax == ndim - 1:
+    if ax == ndim - 1:
         return 1
-    raise NotImplementedError(
-        "INT8 channel quant requires ch_axis=0 or the last axis; got ch_axis=" + str(ch_axis)
-    )
+    return 2
 
 
 def quantize_tensor(
@@ -117,17 +122,27 @@ def quantize_tensor(
         axis = channel_kernel_axis(x.dim(), ch_axis)
         if axis == 0:
             q, scale = kernel(x, eps)
-        else:
+        elif axis == 1:
             F = x.shape[-1]
             q2, scale = kernel(x.view(-1, F), eps, axis=1)
             q = q2.view(x.shape)
+        else:
+            q, scale = _hip_quant_int8_channel_nd(x, ch_axis, eps)
     elif mode == "group":
-        moved = x.movedim(ch_axis, -1).contiguous()
-        lead, F = moved.shape[:-1], moved.shape[-1]
+        ax = ch_axis + x.dim() if ch_axis < 0 else ch_axis
+        if not 0 <= ax < max(x.dim(), 1):
+            raise IndexError(f"ch_axis {ch_axis} out of range for a {x.dim()}-D tensor")
+        F = x.shape[ax] if x.dim() else 1
         if F % group_size != 0:
             raise ValueError(f"group_size {group_size} must evenly divide axis length {F}")
-        q_grouped, scale = kernel(moved.view(-1, group_size), group_size, eps)
-        q = q_grouped.view(*lead, F).movedim(-1, ch_axis).contiguous()
+        if x.dim() == 0 or ax == x.dim() - 1:
+            # groups along the last axis are contiguous rows
+            q_grouped, scale = kernel(x.reshape(-1, group_size), group_size, eps)
+            q = q_grouped.view(x.shape)
+        else:
+            # any other axis: strided groups, no movedim copies
+            # (quantizers.py:123-132 makes two full copies here)
+            q, scale = _hip_quant_int8_group_nd(x, ax, group_size, eps)
     else:
         raise ValueError(f"Unsupported mode '{mode}'; expected tensor / channel / group")
 

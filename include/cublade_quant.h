@@ -108,6 +108,35 @@ int cbq_quant_int8_group(const void* x, int dtype, int64_t num_groups,
                          int64_t group_size, float eps, int8_t* q, float* scale,
                          cbq_stream_t stream);
 
+/* ---- N-D axes without transposing copies --------------------------------- */
+
+/* Channel quant over any axis of an N-D tensor, viewed as outer x channels x
+ * inner (channels = the axis length, outer/inner the products of the dims
+ * before/after it); one fp32 scale per channel. The reference only supports
+ * the leading axis (quantizers.py:116-121, quantize_int8.cu:487-509); this is
+ * the same math with the channel maximum taken over outer and inner, and no
+ * copies. outer == 1 runs the row kernels (no workspace). Otherwise the
+ * workspace below holds, for inner >= 512, [outer, channels] segment maxima
+ * plus [channels] multipliers; for shorter inner, the column path's partial
+ * maxima over outer x (channels * inner). */
+size_t cbq_quant_int8_channel_nd_ws_bytes(int64_t outer, int64_t channels,
+                                          int64_t inner);
+int cbq_quant_int8_channel_nd(const void* x, int dtype, int64_t outer,
+                              int64_t channels, int64_t inner, float eps,
+                              void* ws, size_t ws_bytes, int8_t* q,
+                              float* scale, cbq_stream_t stream);
+
+/* Group quant along any axis, viewed as outer x len x inner with groups of
+ * group_size consecutive positions along len. Replaces the reference's
+ * movedim(ch_axis, -1).contiguous() / view(-1, G) / kernel / movedim-back
+ * sequence (quantizers.py:122-132, two full copies) with no copies. scale:
+ * outer * inner * (len / group_size) fp32 in the reference's order,
+ * index (o * inner + i) * (len / group_size) + g. */
+int cbq_quant_int8_group_nd(const void* x, int dtype, int64_t outer,
+                            int64_t len, int64_t inner, int64_t group_size,
+                            float eps, int8_t* q, float* scale,
+                            cbq_stream_t stream);
+
 /* Replaces dequantize_per_tensor_int8_cuda (dequantize_int8.cu:210-225; kernel
  * :29-64), bound as dequantize_int8.dequantize_per_tensor_int8
  * (bindings/cuda/dequantize_int8.py:18-38). */
@@ -128,6 +157,20 @@ int cbq_dequant_int8_channel(const int8_t* q, const float* scale, int64_t rows,
 int cbq_dequant_int8_group(const int8_t* q, const float* scale,
                            int64_t num_groups, int64_t group_size, void* y,
                            int out_dtype, cbq_stream_t stream);
+
+/* Channel dequant over any axis (outer x channels x inner, scale[channels]);
+ * the reference only dequantizes axis 0 (dequantizers.py:51-57). */
+int cbq_dequant_int8_channel_nd(const int8_t* q, const float* scale,
+                                int64_t outer, int64_t channels, int64_t inner,
+                                void* y, int out_dtype, cbq_stream_t stream);
+
+/* Group dequant along any axis (outer x len x inner, scale order as in
+ * cbq_quant_int8_group_nd). Replaces the movedim / view / kernel / movedim
+ * sequence of dequantizers.py:58-72 (two full copies). */
+int cbq_dequant_int8_group_nd(const int8_t* q, const float* scale,
+                              int64_t outer, int64_t len, int64_t inner,
+                              int64_t group_size, void* y, int out_dtype,
+                              cbq_stream_t stream);
 
 /* ---- W8A16 linear ------------------------------------------------------- */
 

@@ -398,9 +398,12 @@ def test_api_errors():
     with pytest.raises(RuntimeError):
         quantize_tensor(torch.randn(2, 5000, device=DEV).bfloat16().view(-1, 5000),
                         dtype=torch.int8, mode="group", group_size=5000, ch_axis=-1)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(IndexError):
         quantize_tensor(torch.randn(4, 5, 6, device=DEV), dtype=torch.int8, mode="channel",
-                        ch_axis=1)
+                        ch_axis=3)
+    with pytest.raises(ValueError):
+        quantize_tensor(torch.randn(4, 6, 5, device=DEV), dtype=torch.int8, mode="group",
+                        group_size=4, ch_axis=1)
     qt = quantize_tensor(x, dtype=torch.float8_e4m3fn)
     bad = QuantizedTensor(qt.data, qt.scale, qt.zero_point, "channel", 0, 32, qt.dtype,
                           torch.bfloat16)
@@ -463,3 +466,126 @@ def test_config4_int8_group_full():
     xb = bits(x.bfloat16())
     del x
     check_int8_group(xb.reshape(-1, 128), oracle.BF16, 128, what="C4")
+
+
+# ---------------------------------------------------------------------------
+# N-D axes without transposing copies (channel on any axis, groups along any
+# axis): bit-exact against the oracle applied to the moved tensor
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("code", [oracle.BF16, oracle.F16, oracle.F32])
+@pytest.mark.parametrize("shape,axis", [
+    # inner < 512: column maxima per row block over the [outer, C * inner] view
+    ((6, 40, 24), 1), ((3, 5, 7, 8), 2), ((3, 5, 7, 8), 1), ((64, 3, 5), 1), ((2, 300, 3), 1),
+    ((5, 1, 9), 1),
+    # inner >= 512: one wave per contiguous segment (vector and scalar loads)
+    ((3, 17, 512), 1), ((2, 5, 1000), 1), ((4, 3, 1001), 1), ((2, 64, 4096), 1),
+    ((3, 2, 600, 2), 1)])
+def test_channel_any_axis(code, shape, axis):
+    from cublade_amd.quantization import dequantize_tensor, quantize_tensor
+    x = rand_bits(shape, code, seed=sum(shape) + axis)
+    xt = from_bits(x.reshape(-1), code, DEV).view(*shape)
+    qt = quantize_tensor(xt, dtype=torch.int8, mode="channel", ch_axis=axis)
+    C = shape[axis]
+    moved = np.ascontiguousarray(np.moveaxis(x.reshape(shape), axis, 0)).reshape(C, -1)
+    qo, so = oracle.quant_int8_channel(moved, code, axis=0)
+    mshape = (C,) + tuple(d for i, d in enumerate(shape) if i != axis)
+    assert_array_equal(bits(qt.data), np.moveaxis(qo.reshape(mshape), 0, axis), "channel nd q")
+    assert tuple(qt.scale.shape) == (C,)
+    assert_array_equal(bits(qt.scale).view(np.uint32), np.asarray(so, np.float32).view(np.uint32),
+                       "channel nd scale")
+    out = oracle.BF16 if code == oracle.F32 else code
+    qt.original_dtype = DTYPE_OF[out]
+    y = dequantize_tensor(qt)
+    yo = oracle.dequant_int8_channel(qo, so, out, axis=0).reshape(mshape)
+    assert_bits_equal_16(bits(y), np.moveaxis(yo, 0, axis), out, "channel nd y")
+
+
+@pytest.mark.parametrize("code", [oracle.BF16, oracle.F16, oracle.F32])
+@pytest.mark.parametrize("shape,axis,G", [
+    # inner % 8 != 0: one thread per group
+    ((6, 64, 3), 1, 32), ((4, 128, 100), 1, 128), ((2, 8, 6, 5), 2, 2), ((96, 7), 0, 32),
+    ((2, 4096, 2), 1, 4096),
+    # inner == 1: contiguous rows
+    ((3, 256, 1), 1, 64),
+    # tiled: 8 / 4 / 2 / 1 waves per group, groups held in registers (<= 16
+    # positions per wave) or read twice, partial inner tiles
+    ((256, 64), 0, 32), ((6, 96, 520), 1, 96), ((512, 1024), 0, 128), ((2, 384, 16), 1, 384),
+    ((136, 8), 0, 136), ((3, 10, 24), 1, 5), ((4, 36, 8), 1, 6), ((2, 12, 1032), 1, 12)])
+def test_group_any_axis(code, shape, axis, G):
+    from cublade_amd.quantization import dequantize_tensor, quantize_tensor
+    x = rand_bits(shape, code, seed=sum(shape) * 3 + axis + G)
+    xt = from_bits(x.reshape(-1), code, DEV).view(*shape)
+    qt = quantize_tensor(xt, dtype=torch.int8, mode="group", group_size=G, ch_axis=axis)
+    moved = np.ascontiguousarray(np.moveaxis(x.reshape(shape), axis, -1))
+    qo, so = oracle.quant_int8_group(moved.reshape(-1, G), code, G)
+    assert_array_equal(bits(qt.data), np.moveaxis(qo.reshape(moved.shape), -1, axis), "group nd q")
+    assert_array_equal(bits(qt.scale).view(np.uint32), np.asarray(so, np.float32).view(np.uint32),
+                       "group nd scale")
+    out = oracle.BF16 if code == oracle.F32 else code
+    qt.original_dtype = DTYPE_OF[out]
+    y = dequantize_tensor(qt)
+    yo = oracle.dequant_int8_group(qo, so, G, out).reshape(moved.shape)
+    assert_bits_equal_16(bits(y), np.moveaxis(yo, -1, axis), out, "group nd y")
+
+
+@pytest.mark.parametrize("mode,axis", [("group", 0), ("channel", 1)])
+def test_any_axis_unaligned_view(mode, axis):
+    """A view whose data pointer is not 16-byte aligned takes the scalar
+    kernels; codes and scales match those of an aligned copy bit for bit."""
+    from cublade_amd.quantization import dequantize_tensor, quantize_tensor
+    shape = (64, 4, 520)
+    n = int(np.prod(shape))
+    base = torch.randn(n + 1, generator=torch.Generator().manual_seed(9)).half().to(DEV)
+    xv = base[1:].view(shape)
+    xa = xv.clone()
+    kw = dict(dtype=torch.int8, mode=mode, ch_axis=axis)
+    if mode == "group":
+        kw["group_size"] = 32
+    qv, qa = quantize_tensor(xv, **kw), quantize_tensor(xa, **kw)
+    assert_array_equal(bits(qv.data), bits(qa.data), "unaligned q")
+    assert_array_equal(bits(qv.scale).view(np.uint32), bits(qa.scale).view(np.uint32),
+                       "unaligned scale")
+    assert_array_equal(bits(dequantize_tensor(qv)), bits(dequantize_tensor(qa)), "unaligned y")
+
+
+@pytest.mark.parametrize("mode,axis,G", [("group", 0, 32), ("group", 0, 8), ("channel", 1, None)])
+def test_any_axis_special_values(mode, axis, G):
+    """NaN, +-inf, all-zero and subnormal columns through the tiled group
+    kernels and the segment-max channel path, bit-exact against the oracle."""
+    from cublade_amd.quantization import dequantize_tensor, quantize_tensor
+    shape = (64, 520) if mode == "group" else (3, 4, 640)
+    v = torch.randn(*shape, generator=torch.Generator().manual_seed(11)).bfloat16()
+    if mode == "group":
+        v[3, 5] = float("nan")
+        v[40, 7] = float("inf")
+        v[41, 7] = -float("inf")
+        v[:, 9] = 0.0
+        v[:, 10] = 1e-39          # bf16 subnormal
+        v[:32, 11] = float("nan")
+    else:
+        v[1, 2, 5] = float("nan")
+        v[2, 0, 600] = -float("inf")
+        v[:, 3, :] = 0.0
+        v[:, 1, :] = 1e-39
+    x = bits(v)
+    xt = from_bits(x.reshape(-1), oracle.BF16, DEV).view(*shape)
+    if mode == "group":
+        qt = quantize_tensor(xt, dtype=torch.int8, mode="group", group_size=G, ch_axis=axis)
+        moved = np.ascontiguousarray(np.moveaxis(x, axis, -1))
+        qo, so = oracle.quant_int8_group(moved.reshape(-1, G), oracle.BF16, G)
+        qo = np.moveaxis(qo.reshape(moved.shape), -1, axis)
+        yo = np.moveaxis(oracle.dequant_int8_group(np.moveaxis(qo, axis, -1).reshape(-1, G), so, G,
+                                                   oracle.BF16).reshape(moved.shape), -1, axis)
+    else:
+        qt = quantize_tensor(xt, dtype=torch.int8, mode="channel", ch_axis=axis)
+        C = shape[axis]
+        mshape = (C,) + tuple(d for i, d in enumerate(shape) if i != axis)
+        moved = np.ascontiguousarray(np.moveaxis(x, axis, 0)).reshape(C, -1)
+        qo, so = oracle.quant_int8_channel(moved, oracle.BF16, axis=0)
+        yo = np.moveaxis(oracle.dequant_int8_channel(qo, so, oracle.BF16, axis=0).reshape(mshape),
+                         0, axis)
+        qo = np.moveaxis(qo.reshape(mshape), 0, axis)
+    assert_array_equal(bits(qt.data), qo, "special q")
+    assert_array_equal(bits(qt.scale).view(np.uint32), np.asarray(so, np.float32).view(np.uint32),
+                       "special scale")
+    assert_bits_equal_16(bits(dequantize_tensor(qt)), yo, oracle.BF16, "special y")

@@ -34,7 +34,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     L = _lib()
     names = declared_symbols()
-    assert len(names) == 14
+    assert len(names) == 19
     for n in names:
         assert hasattr(L, n), n
     from cublade_amd import _abi
@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_slot():
     L = _lib()
-    assert L.cbq_abi_version() == 101
+    assert L.cbq_abi_version() == 102
     assert L.cbq_last_error() in (b"",) or isinstance(L.cbq_last_error(), bytes)
 
 
@@ -96,6 +96,41 @@ def test_workspace_sizes():
     assert L.cbq_w8a16_ws_bytes(256, 11008, 4000, 0) == C      # K % 64 != 0
 
 
+def test_nd_entry_points_validate_and_size():
+    """The N-D channel / group entry points: workspace sizes and argument
+    checks (no device work)."""
+    L = _lib()
+    from cublade_amd import _abi
+    C = _abi.WS_CTRL_BYTES
+    # outer == 1 runs the row kernels (no workspace); inner < 512 takes the
+    # column path on outer x (channels * inner), sized like axis 1; longer
+    # inner runs take the segment path: [outer, channels] segment maxima plus
+    # [channels] multipliers
+    assert L.cbq_quant_int8_channel_nd_ws_bytes(1, 64, 128) == C
+    assert L.cbq_quant_int8_channel_nd_ws_bytes(6, 40, 24) == \
+        L.cbq_quant_int8_channel_ws_bytes(6, 40 * 24, 1)
+    assert L.cbq_quant_int8_channel_nd_ws_bytes(6, 40, 511) == \
+        L.cbq_quant_int8_channel_ws_bytes(6, 40 * 511, 1)
+    assert L.cbq_quant_int8_channel_nd_ws_bytes(7, 4096, 8192) == C + 4 * (7 * 4096 + 4096)
+    assert L.cbq_quant_int8_channel_nd_ws_bytes(2, 3, 512) == C + 4 * (2 * 3 + 3)
+    F16 = _abi.DTYPE_CODE[torch.float16]
+    dummy = ctypes.c_void_p(16)
+    _einval(L.cbq_quant_int8_group_nd(dummy, F16, 2, 100, 3, 32, 1e-12, dummy, dummy, None),
+            "must divide")
+    _einval(L.cbq_quant_int8_group_nd(dummy, F16, 2, 96, 3, 0, 1e-12, dummy, dummy, None),
+            "group_size")
+    _einval(L.cbq_quant_int8_channel_nd(dummy, 9, 2, 3, 4, 1e-12, None, 0, dummy, dummy, None),
+            "dtype")
+    _einval(L.cbq_quant_int8_channel_nd(dummy, F16, 2, 3, 4, 1e-12, None, 0, dummy, dummy, None),
+            "workspace")
+    _einval(L.cbq_dequant_int8_group_nd(dummy, dummy, 2, 100, 3, 32, dummy, F16, None),
+            "must divide")
+    _einval(L.cbq_dequant_int8_channel_nd(dummy, dummy, 2, 3, 4, dummy, 0, None), "out_dtype")
+    # empty shapes are no-ops
+    assert L.cbq_quant_int8_group_nd(None, F16, 0, 64, 3, 32, 1e-12, None, None, None) == 0
+    assert L.cbq_dequant_int8_channel_nd(None, None, 5, 0, 3, None, F16, None) == 0
+
+
 def test_loader_memoises_failures(tmp_path):
     from cublade_amd import _loader
     bad = tmp_path / "bad.hip"
@@ -130,8 +165,11 @@ def test_channel_axis_mapping():
     assert channel_kernel_axis(2, 0) == 0 and channel_kernel_axis(2, 1) == 1
     assert channel_kernel_axis(2, -1) == 1 and channel_kernel_axis(3, -1) == 1
     assert channel_kernel_axis(1, 0) == 0 and channel_kernel_axis(1, -1) == 0
-    with pytest.raises(NotImplementedError):
-        channel_kernel_axis(3, 1)
+    assert channel_kernel_axis(3, 1) == 2 and channel_kernel_axis(4, -2) == 2   # N-D path
+    with pytest.raises(IndexError):
+        channel_kernel_axis(3, 3)
+    with pytest.raises(IndexError):
+        channel_kernel_axis(3, -4)
 
 
 def test_outlier_utils_match_definition():
