@@ -22,12 +22,16 @@ SOURCES = [
     CSRC / "cbq_quant.hip",
     CSRC / "cbq_dequant.hip",
     CSRC / "cbq_w8a16.hip",
+    CSRC / "cbq_gemm.hip",
 ]
 
 WS_CTRL_BYTES = 16384
 
 F32, F16, BF16 = 0, 1, 2
+I8, U8, I32 = 3, 4, 5
 DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+MM_DTYPE_CODE = {torch.int8: I8, torch.uint8: U8, torch.int32: I32, **DTYPE_CODE}
+MM_B_KN, MM_B_NK = 0, 1
 
 _P, _I64, _I32, _F, _SZ = (ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float,
                            ctypes.c_size_t)
@@ -54,6 +58,8 @@ SIGNATURES = {
     "cbq_w8a16_ws_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
     "cbq_w8a16_linear": (_I32, [_P, _I32, _P, _P, _P, _P, _I64, _P, _I64, _I64, _I64,
                                 _P, _SZ, _P, _P]),
+    "cbq_mm_ws_bytes": (_SZ, [_I64, _I64, _I64, _I32, _I32]),
+    "cbq_mm": (_I32, [_P, _P, _I32, _I32, _I64, _I64, _I64, _P, _I32, _P, _SZ, _P]),
 }
 
 _lib = None

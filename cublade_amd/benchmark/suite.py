@@ -6,9 +6,10 @@ second and as a fraction of the MI355X roofline (8 TB/s HBM, 2.5 PFLOP/s
 dense fp16 MFMA). Algorithmic bytes per op (N elements, C channels, G
 groups): per-tensor quant 2N read (amax) + 2N read + N written + 4 (cast);
 row / group quant 2N + N + 4C (one pass); column quant 2N + 2N + N + 4F (two
-passes); dequant N + 2N + 4 * scales. W8A16: 2 * M * N * K FLOPs.
+passes); dequant N + 2N + 4 * scales. W8A16 and the dense GEMM: 2 * M * N * K
+FLOPs (int8 GEMMs against the 5.0 POP/s dense int8 peak).
 
-    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5,f1,f3 [--json out.json]
+    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5,f1,f3,f4 [--json out.json]
 """
 from __future__ import annotations
 
@@ -20,7 +21,7 @@ import sys
 import torch
 
 from . import configs
-from .core import FP16_MFMA_PEAK_FLOP_S, HBM_PEAK_BYTES_S, MallFlush, time_op
+from .core import FP16_MFMA_PEAK_FLOP_S, HBM_PEAK_BYTES_S, I8_MFMA_PEAK_OP_S, MallFlush, time_op
 
 
 def _rec(cfg, op, us, bytes_=None, flops=None):
@@ -167,13 +168,48 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
         out.append(r)
         print(json.dumps(r), flush=True)
         del x
+    if "f4" in selected:
+        # Dense GEMM (wmma_gemm's replacement) at 8192^3: int8 -> int32 with B
+        # as an [N, K] weight (read in place) and as [K, N] (transposed into
+        # the workspace first, inside the timed call), uint8, fp16 -> fp32.
+        # Next to PyTorch's own GEMMs (torch._int_mm, torch.matmul).
+        from cublade_amd.bindings.hip.wmma import wmma_gemm
+        M = N = K = 8192
+        g = torch.Generator().manual_seed(6)
+        flops = 2.0 * M * N * K
+        a8 = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int16).to(torch.int8).to(dev)
+        w8 = torch.randint(-128, 128, (N, K), generator=g, dtype=torch.int16).to(torch.int8).to(dev)
+        b8 = w8.t().contiguous()
+        cases = [("mm_i8_nk", lambda: wmma_gemm(a8, w8.t())),
+                 ("mm_i8_kn", lambda: wmma_gemm(a8, b8)),
+                 ("mm_u8_nk", lambda: wmma_gemm(a8.view(torch.uint8), w8.view(torch.uint8).t()))]
+        try:
+            torch._int_mm(a8[:32], w8.t()[:, :32].contiguous())
+            cases.append(("torch_int_mm_i8", lambda: torch._int_mm(a8, w8.t())))
+        except RuntimeError:
+            pass
+        for name, fn in cases:
+            r = _rec("f4", name, time_op(fn, reps, warmup, flush), None, flops)
+            r["tops"] = r.pop("tflops")
+            r["mfma_frac"] = round(r["tops"] * 1e12 / I8_MFMA_PEAK_OP_S, 4)
+            out.append(r)
+            print(json.dumps(r), flush=True)
+        del a8, w8, b8
+        ah = torch.randn(M, K, generator=g).half().to(dev)
+        wh = torch.randn(N, K, generator=g).half().to(dev)
+        for name, fn in [("mm_f16_f32_nk", lambda: wmma_gemm(ah, wh.t())),
+                         ("torch_matmul_f16", lambda: torch.matmul(ah, wh.t()))]:
+            r = _rec("f4", name, time_op(fn, reps, warmup, flush), None, flops)
+            out.append(r)
+            print(json.dumps(r), flush=True)
+        del ah, wh
     torch.cuda.synchronize()
     return out
 
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,f1,f3")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,f1,f3,f4")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--json", default=None)

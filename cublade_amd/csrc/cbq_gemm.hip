@@ -1,0 +1,511 @@
+// cbq_gemm.hip - dense GEMM on gfx950 matrix cores: C[M, N] = A[M, K] . B[K, N].
+//
+// Replaces the reference's WMMA GEMM (kernels/cuda/wmma.cu:29-169, host
+// wmma_gemm :186-261, bound as bindings/cuda/wmma.py:15-43) and keeps its
+// precision table:
+//   int8  x int8  -> int32   v_mfma_i32_32x32x32_i8
+//   uint8 x uint8 -> int32   the same on u ^ 0x80 (= u - 128), corrected exactly
+//                            by k_u8_fix:
+//        sum_k ua ub = sum_k sa sb + 128 (sum_k sa + sum_k sb) + 16384 K
+//   fp16  x fp16  -> fp32    v_mfma_f32_32x32x16_f16
+//   fp16  x fp16  -> fp16    fp32 accumulation, one rounding at the end (the
+//                            reference accumulates in fp16 fragments)
+//   bf16  x bf16  -> fp32    v_mfma_f32_32x32x16_bf16
+// Integer results are exact modulo 2^32 (int32 wrap-around, as the int32
+// accumulators of the reference).
+//
+// k_mm_dma<IN, OUT>: 256 x 256 output tiles, 4 waves of 128 x 128 (4 x 4
+// tiles of 32 x 32), k-steps of 64 bytes per row (64 int8 or 32 fp16 k), four
+// LDS stages of 32 KiB filled by LDS DMA (global_load_lds_dwordx4), three
+// k-steps in flight. Both operands are K-contiguous rows: A [M, K] as given
+// and B as B^T [N, K]. A B that is stored [N, K] (B = W^T, the usual weight
+// layout) is read in place; a [K, N] B is transposed into the workspace
+// first (k_stage_bt). uint8 operands and row lengths that are not a multiple
+// of 64 bytes are staged too (k_stage_rows: offset to int8, zero padding).
+//
+// LDS layout of a stage: A rows (64 B each) then B^T rows; 16-byte chunk c of
+// row r sits at chunk c ^ ((r >> 2) & 3), so that the fragment reads of 16
+// consecutive rows hit distinct banks. In a k-step, MFMA s (0, 1) of lane
+// half h (lane / 32) takes chunk 2 h + s of its A row and of its B^T row: A
+// and B see the same k order, which is all the contraction needs.
+//
+// The MFMA A operand is the A fragment (D rows = m) and B the B^T fragment
+// (D columns = n): lane l holds C[m][n] for n = l % 32 and m = 8 (v / 4) +
+// 4 (l / 32) + v % 4, so each store instruction writes two 128-byte runs of a
+// row (int32 / fp32).
+#include <algorithm>
+
+#include "cbq_device.h"
+#include "cbq_host.h"
+#include "cbq_lds_dma.h"
+
+namespace cbq {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+typedef float f16x __attribute__((ext_vector_type(16)));
+typedef int i4v __attribute__((ext_vector_type(4)));
+typedef int i16x __attribute__((ext_vector_type(16)));
+
+// Input kinds of the kernels (the C ABI's dtype codes map onto these).
+enum : int { kInI8 = 0, kInF16 = 1, kInBF16 = 2 };
+// Output kinds.
+enum : int { kOutI32 = 0, kOutF32 = 1, kOutF16 = 2 };
+
+template <int IN> struct AccOf { typedef f16x type; };
+template <> struct AccOf<kInI8> { typedef i16x type; };
+
+template <int IN>
+__device__ __forceinline__ typename AccOf<IN>::type mfma32(const u32x4& a, const u32x4& b,
+                                                           typename AccOf<IN>::type c) {
+  if constexpr (IN == kInI8)
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i4v, a),
+                                                 __builtin_bit_cast(i4v, b), c, 0, 0, 0);
+  else if constexpr (IN == kInF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8, a),
+                                                  __builtin_bit_cast(h8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(b8, a),
+                                                   __builtin_bit_cast(b8, b), c, 0, 0, 0);
+}
+
+struct MmArgs {
+  const uint8_t* a;      // [M, ldk] bytes, K-contiguous rows
+  const uint8_t* bt;     // [N, ldk] bytes (B^T)
+  void* c;               // [M, N] row-major, OUT elements
+  const int* row_sum;    // uint8 correction: sum_k of each signed A row [M]
+  const int* col_sum;    // and of each signed B^T row [N] (null: none)
+  int M, N;
+  int ldk;               // row pitch of a and bt in bytes (multiple of 64)
+  int nk;                // 64-byte k-steps
+  int K;                 // true K (the uint8 correction's 16384 K term)
+  int tiles_m, tiles_n;
+};
+
+// Workgroup -> (tile m, tile n): XCD b % 8 gets a contiguous run of logical
+// tiles, which run in groups of 8 m-tiles so that the workgroups resident on
+// one XCD share A and B^T k-slices in its L2.
+__device__ __forceinline__ void mm_tile(int b, const MmArgs& a, int& tm, int& tn) {
+  const int total = a.tiles_m * a.tiles_n;
+  const int per = total >> 3;
+  if (b < per * 8) b = (b & 7) * per + (b >> 3);
+  constexpr int G = 8;
+  const int group = b / (G * a.tiles_n);
+  const int first_m = group * G;
+  const int gsize = min(a.tiles_m - first_m, G);
+  const int r = b % (G * a.tiles_n);
+  tm = first_m + r % gsize;
+  tn = r / gsize;
+}
+
+constexpr int kMmNS = 4;                 // LDS stages
+constexpr int kMmHalf = 256 * 64;        // bytes of one operand per stage
+constexpr int kMmSB = 2 * kMmHalf;       // stage bytes (32 KiB)
+constexpr int kMmL = kMmHalf / (256 * 16);   // DMA instructions per operand per thread (4)
+
+template <int IN, int OUT>
+__global__ __launch_bounds__(256) void k_mm_dma(MmArgs a) {
+  typedef typename AccOf<IN>::type Acc;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kMmNS * kMmSB];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  int tm, tn;
+  mm_tile(blockIdx.x, a, tm, tn);
+  const int m0 = tm * 256, n0 = tn * 256;
+  const int nk = a.nk;
+  const uint32_t sbase = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+
+  // DMA sources: instruction u of an operand fills rows (u * 4 + wave) * 16
+  // + lane / 4, chunk slot lane % 4, which holds source chunk slot ^ swizzle.
+  // Rows past M or N are clamped to the last row; their products land in
+  // outputs that are never stored.
+  uint32_t ao[kMmL], bo[kMmL];
+#pragma unroll
+  for (int u = 0; u < kMmL; ++u) {
+    const int row = (u * 4 + wave) * 16 + (lane >> 2);
+    const int c = (lane & 3) ^ ((row >> 2) & 3);
+    ao[u] = static_cast<uint32_t>(min(m0 + row, a.M - 1)) * static_cast<uint32_t>(a.ldk) + c * 16u;
+    bo[u] = static_cast<uint32_t>(min(n0 + row, a.N - 1)) * static_cast<uint32_t>(a.ldk) + c * 16u;
+  }
+  auto issue = [&](int t, int stage) {
+    const uint32_t dst = sbase + stage * kMmSB + wave * 1024;
+    const uint8_t* pa = uniform_ptr(a.a + t * 64);
+    const uint8_t* pb = uniform_ptr(a.bt + t * 64);
+#pragma unroll
+    for (int u = 0; u < kMmL; ++u) lds_dma16(ao[u], pa, dst + u * 4096);
+#pragma unroll
+    for (int u = 0; u < kMmL; ++u) lds_dma16(bo[u], pb, dst + kMmHalf + u * 4096);
+  };
+
+  // Fragment read offsets: row r32 of 32-row tile j (A) / i (B^T), chunk
+  // 2 h + s.
+  const int r32 = lane & 31, h = lane >> 5;
+  uint32_t ar[2], br[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const uint32_t slot = static_cast<uint32_t>((2 * h + s) ^ ((r32 >> 2) & 3)) << 4;
+    ar[s] = (wm * 128 + r32) * 64 + slot;
+    br[s] = kMmHalf + (wn * 128 + r32) * 64 + slot;
+  }
+
+  const int mw = m0 + wm * 128, nw = n0 + wn * 128;
+  Acc acc[4][4];   // [j: m-tile][i: n-tile]
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[j][i] = Acc{};
+
+  struct Frags {
+    u32x4 x[4];   // A, m-tiles
+    u32x4 w[4];   // B^T, n-tiles
+  };
+  auto read = [&](int stage, int s, Frags& f) {
+    const uint8_t* st = smem + stage * kMmSB;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.x[j] = *reinterpret_cast<const u32x4*>(st + ar[s] + j * 2048);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f.w[i] = *reinterpret_cast<const u32x4*>(st + br[s] + i * 2048);
+  };
+  // 16 MFMAs; an accumulator is reused every 16th, so no back-to-back
+  // dependent MFMA.
+  auto mma = [&](const Frags& f) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[j][i] = mfma32<IN>(f.x[j], f.w[i], acc[j][i]);
+  };
+
+  // Prologue: tiles 0 .. NS - 2 in flight.
+#pragma unroll
+  for (int t = 0; t < kMmNS - 1; ++t)
+    if (t < nk) issue(t, t);
+  Frags f0, f1;
+  for (int t = 0; t < nk; ++t) {
+    // Tile t has landed once only the DMAs of the (at most two) later tiles
+    // issued so far are outstanding; the barrier also means every wave is
+    // done reading stage (t - 1) % NS, which tile t + 3 overwrites.
+    const int later = min(kMmNS - 2, nk - 1 - t);
+    if (later >= 2) dma_wait_barrier<2 * 2 * kMmL>();
+    else if (later == 1) dma_wait_barrier<2 * kMmL>();
+    else dma_wait_barrier<0>();
+    const int stage = t % kMmNS;
+    read(stage, 0, f0);
+    read(stage, 1, f1);
+    if (t + kMmNS - 1 < nk) issue(t + kMmNS - 1, (t + kMmNS - 1) % kMmNS);
+    mma(f0);
+    mma(f1);
+  }
+
+  // Epilogue: C[m][n], n = 32 i + r32, m = 32 j + 8 (v / 4) + 4 h + v % 4.
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n = nw + 32 * i + r32;
+      if (n >= a.N) continue;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int m = mw + 32 * j + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (m >= a.M) continue;
+        const int64_t off = static_cast<int64_t>(m) * a.N + n;
+        if constexpr (OUT == kOutI32)
+          static_cast<int*>(a.c)[off] = acc[j][i][v];
+        else if constexpr (OUT == kOutF32)
+          static_cast<float*>(a.c)[off] = acc[j][i][v];
+        else
+          static_cast<_Float16*>(a.c)[off] = static_cast<_Float16>(acc[j][i][v]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Staging into the workspace
+// ---------------------------------------------------------------------------
+
+// Rows of kb bytes (multiple of 16) -> rows of ldk bytes (multiple of 64),
+// zero-padded; XOR flips the sign bit of every byte (uint8 -> int8 offset).
+// Grid-stride over 16-byte chunks of the destination.
+template <bool XOR>
+__global__ __launch_bounds__(kBlock) void k_stage_rows(const uint8_t* __restrict__ src,
+                                                       int64_t rows, int64_t kb, int64_t ldk,
+                                                       uint8_t* __restrict__ dst) {
+  const int64_t cpr = ldk >> 4;
+  const int64_t total = rows * cpr;
+  for (int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; c < total;
+       c += static_cast<int64_t>(gridDim.x) * kBlock) {
+    const int64_t r = c / cpr, k = (c % cpr) * 16;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (k < kb) {
+      v = *reinterpret_cast<const u32x4*>(src + r * kb + k);
+      if constexpr (XOR) v ^= 0x80808080u;
+    }
+    *reinterpret_cast<u32x4*>(dst + r * ldk + k) = v;
+  }
+}
+
+// B [K, N] (ES-byte elements, row-major) -> B^T [N, ldk bytes], zero-padded
+// past K; XOR as above (ES == 1 only). A workgroup transposes a 64 (k) x 64 (n)
+// element tile through LDS: 16-byte loads along n, element reads down k,
+// 16-byte stores along k.
+template <int ES, bool XOR>
+__global__ __launch_bounds__(kBlock) void k_stage_bt(const uint8_t* __restrict__ b, int64_t K,
+                                                     int64_t N, int64_t ldk,
+                                                     uint8_t* __restrict__ dst) {
+  constexpr int T = 64;                        // elements per tile side
+  constexpr int RB = T * ES;                   // bytes per tile row
+  constexpr int PITCH = RB + 4;                // LDS row pitch
+  constexpr int CPR = RB / 16;                 // 16-byte chunks per tile row
+  __shared__ uint8_t tile[T * PITCH];
+  const int64_t k0 = static_cast<int64_t>(blockIdx.y) * T;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * T;
+  // Load: T rows (k) x CPR chunks.
+  for (int c = threadIdx.x; c < T * CPR; c += kBlock) {
+    const int kr = c / CPR, ch = c % CPR;
+    const int64_t k = k0 + kr, n = n0 + (ch * 16) / ES;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (k < K && n < N) v = *reinterpret_cast<const u32x4*>(b + (k * N + n) * ES);
+    uint32_t* d = reinterpret_cast<uint32_t*>(tile + kr * PITCH + ch * 16);
+    d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+  }
+  __syncthreads();
+  // Store: T rows (n) x CPR chunks of k.
+  for (int c = threadIdx.x; c < T * CPR; c += kBlock) {
+    const int nr = c / CPR, ch = c % CPR;
+    const int64_t n = n0 + nr;
+    const int kc = (ch * 16) / ES;             // first k of the chunk in the tile
+    if (n >= N) continue;
+    const int64_t kbyte = (k0 + kc) * ES;
+    if (kbyte >= ldk) continue;
+    uint8_t bytes[16];
+#pragma unroll
+    for (int e = 0; e < 16 / ES; ++e) {
+#pragma unroll
+      for (int x = 0; x < ES; ++x) {
+        const bool in = k0 + kc + e < K;
+        bytes[e * ES + x] = in ? tile[(kc + e) * PITCH + nr * ES + x] : 0;
+      }
+    }
+    u32x4 v;
+    v.x = bytes[0] | (bytes[1] << 8) | (bytes[2] << 16) | (static_cast<uint32_t>(bytes[3]) << 24);
+    v.y = bytes[4] | (bytes[5] << 8) | (bytes[6] << 16) | (static_cast<uint32_t>(bytes[7]) << 24);
+    v.z = bytes[8] | (bytes[9] << 8) | (bytes[10] << 16) | (static_cast<uint32_t>(bytes[11]) << 24);
+    v.w = bytes[12] | (bytes[13] << 8) | (bytes[14] << 16) | (static_cast<uint32_t>(bytes[15]) << 24);
+    if constexpr (XOR) {
+      // Flip the sign bit of the bytes that hold data (k < K); padding stays 0.
+      uint32_t m[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (k0 + kc + e < K) m[e >> 2] |= 0x80u << (8 * (e & 3));
+      v.x ^= m[0]; v.y ^= m[1]; v.z ^= m[2]; v.w ^= m[3];
+    }
+    *reinterpret_cast<u32x4*>(dst + n * ldk + kbyte) = v;
+  }
+}
+
+// Sum of the signed bytes of each row of a staged [rows, ldk] int8 buffer
+// (padding is 0): one workgroup per row (grid-stride), dot4 with 1s.
+__global__ __launch_bounds__(kBlock) void k_row_sums(const uint8_t* __restrict__ src,
+                                                     int64_t rows, int64_t ldk,
+                                                     int* __restrict__ sums) {
+  __shared__ int red[kBlock / kWave];
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    int s = 0;
+    for (int64_t k = threadIdx.x * 16; k < ldk; k += kBlock * 16) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(src + r * ldk + k);
+      s = __builtin_amdgcn_sdot4(static_cast<int>(v.x), 0x01010101, s, false);
+      s = __builtin_amdgcn_sdot4(static_cast<int>(v.y), 0x01010101, s, false);
+      s = __builtin_amdgcn_sdot4(static_cast<int>(v.z), 0x01010101, s, false);
+      s = __builtin_amdgcn_sdot4(static_cast<int>(v.w), 0x01010101, s, false);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, kWave);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) sums[r] = red[0] + red[1] + red[2] + red[3];
+    __syncthreads();
+  }
+}
+
+// uint8 correction, after the int8 GEMM on the offset operands:
+// C[m][n] += 128 (row_sum[m] + col_sum[n]) + 16384 K (int32 wrap-around).
+// N % 16 == 0 and C 16-byte aligned: four outputs per thread.
+__global__ __launch_bounds__(kBlock) void k_u8_fix(int* __restrict__ c, int64_t M, int64_t N,
+                                                   const int* __restrict__ row_sum,
+                                                   const int* __restrict__ col_sum, int64_t K) {
+  const int64_t n4 = N >> 2, total = M * n4;
+  const uint32_t kk = static_cast<uint32_t>(K) * 16384u;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; t < total;
+       t += static_cast<int64_t>(gridDim.x) * kBlock) {
+    const int64_t m = t / n4, n = (t % n4) * 4;
+    u32x4 v = *reinterpret_cast<const u32x4*>(c + m * N + n);
+    const uint32_t r = static_cast<uint32_t>(row_sum[m]) * 128u + kk;
+    v.x += r + static_cast<uint32_t>(col_sum[n]) * 128u;
+    v.y += r + static_cast<uint32_t>(col_sum[n + 1]) * 128u;
+    v.z += r + static_cast<uint32_t>(col_sum[n + 2]) * 128u;
+    v.w += r + static_cast<uint32_t>(col_sum[n + 3]) * 128u;
+    *reinterpret_cast<u32x4*>(c + m * N + n) = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host
+// ---------------------------------------------------------------------------
+struct MmPlan {
+  int in, es;          // kernel input kind, element bytes
+  bool u8;
+  int64_t kb, ldk;     // row bytes, padded row bytes
+  bool stage_a, stage_b;
+  size_t a_off, b_off, rs_off, cs_off, bytes;
+};
+
+size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+bool mm_plan(int64_t M, int64_t N, int64_t K, int in_dtype, int b_layout, MmPlan& p) {
+  switch (in_dtype) {
+    case CBQ_I8: p.in = kInI8; p.es = 1; p.u8 = false; break;
+    case CBQ_U8: p.in = kInI8; p.es = 1; p.u8 = true; break;
+    case CBQ_F16: p.in = kInF16; p.es = 2; p.u8 = false; break;
+    case CBQ_BF16: p.in = kInBF16; p.es = 2; p.u8 = false; break;
+    default: return false;
+  }
+  p.kb = K * p.es;
+  p.ldk = cdiv(p.kb, 64) * 64;
+  const bool padded = p.ldk != p.kb;
+  p.stage_a = p.u8 || padded;
+  p.stage_b = p.u8 || padded || b_layout == CBQ_MM_B_KN;
+  size_t off = CBQ_WS_CTRL_BYTES;
+  p.a_off = off;
+  if (p.stage_a) off = align256(off + static_cast<size_t>(M) * p.ldk);
+  p.b_off = off;
+  if (p.stage_b) off = align256(off + static_cast<size_t>(N) * p.ldk);
+  p.rs_off = off;
+  if (p.u8) off = align256(off + static_cast<size_t>(M) * 4);
+  p.cs_off = off;
+  if (p.u8) off = align256(off + static_cast<size_t>(N) * 4);
+  p.bytes = off;
+  return true;
+}
+
+template <int IN, int OUT>
+void launch_mm(const MmArgs& a, hipStream_t s) {
+  k_mm_dma<IN, OUT><<<dim3(static_cast<unsigned>(a.tiles_m * a.tiles_n)), dim3(256), 0, s>>>(a);
+}
+
+unsigned grid_for(int64_t work, int64_t per_block) {
+  int64_t g = cdiv(work, per_block);
+  const int64_t cap = static_cast<int64_t>(device_cus()) * 16;
+  if (g > cap) g = cap;
+  return static_cast<unsigned>(g < 1 ? 1 : g);
+}
+
+}  // namespace
+}  // namespace cbq
+
+using namespace cbq;
+
+extern "C" size_t cbq_mm_ws_bytes(int64_t M, int64_t N, int64_t K, int in_dtype, int b_layout) {
+  MmPlan p;
+  if (M <= 0 || N <= 0 || K < 0 || !mm_plan(M, N, K, in_dtype, b_layout, p))
+    return CBQ_WS_CTRL_BYTES;
+  return p.bytes;
+}
+
+extern "C" int cbq_mm(const void* A, const void* B, int in_dtype, int b_layout, int64_t M,
+                      int64_t N, int64_t K, void* C, int out_dtype, void* ws, size_t ws_bytes,
+                      cbq_stream_t stream) {
+  clear_error();
+  const char* what = "cbq_mm";
+  MmPlan p;
+  CBQ_REQUIRE(mm_plan(1, 1, 1, in_dtype, b_layout, p),
+              "%s: unsupported dtype code %d; expected int8, uint8, float16 or bfloat16", what,
+              in_dtype);
+  const bool int_in = in_dtype == CBQ_I8 || in_dtype == CBQ_U8;
+  if (int_in) {
+    CBQ_REQUIRE(out_dtype == CBQ_I32, "%s: int8 / uint8 inputs only support an int32 accumulator",
+                what);
+  } else if (in_dtype == CBQ_BF16) {
+    CBQ_REQUIRE(out_dtype == CBQ_F32, "%s: bfloat16 inputs only support a float32 accumulator",
+                what);
+  } else {
+    CBQ_REQUIRE(out_dtype == CBQ_F32 || out_dtype == CBQ_F16,
+                "%s: float16 inputs support a float32 or float16 accumulator", what);
+  }
+  CBQ_REQUIRE(b_layout == CBQ_MM_B_KN || b_layout == CBQ_MM_B_NK, "%s: bad b_layout %d", what,
+              b_layout);
+  CBQ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative shape", what);
+  CBQ_REQUIRE(M % 16 == 0 && N % 16 == 0 && K % 16 == 0,
+              "%s: dimensions must be multiples of 16 (M=%lld N=%lld K=%lld)", what, (long long)M,
+              (long long)N, (long long)K);
+  if (M == 0 || N == 0) return CBQ_OK;
+  CBQ_REQUIRE(A && B && C, "%s: null pointer", what);
+  CBQ_REQUIRE(aligned(A, 16) && aligned(B, 16) && aligned(C, 16),
+              "%s: A, B and C must be 16-byte aligned", what);
+  mm_plan(M, N, K, in_dtype, b_layout, p);
+  CBQ_REQUIRE(static_cast<uint64_t>(M) * p.ldk < (1ULL << 32) &&
+                  static_cast<uint64_t>(N) * p.ldk < (1ULL << 32),
+              "%s: M * K and N * K must stay below 4 GiB of operand bytes", what);
+  CBQ_REQUIRE(cdiv(M, 256) * cdiv(N, 256) < (1LL << 31), "%s: too many tiles", what);
+  CBQ_REQUIRE(b_layout == CBQ_MM_B_NK || cdiv(p.ldk / p.es, 64) <= 65535,
+              "%s: K too large for a [K, N] B (store B as [N, K])", what);
+  CBQ_REQUIRE(ws && aligned(ws, 256) && ws_bytes >= p.bytes,
+              "%s: workspace must be >= %zu bytes, 256-byte aligned", what, p.bytes);
+  hipStream_t s = as_stream(stream);
+  uint8_t* w = static_cast<uint8_t*>(ws);
+  MmArgs a;
+  a.a = static_cast<const uint8_t*>(A);
+  a.bt = static_cast<const uint8_t*>(B);
+  a.c = C;
+  a.row_sum = nullptr;
+  a.col_sum = nullptr;
+  a.M = static_cast<int>(M);
+  a.N = static_cast<int>(N);
+  a.ldk = static_cast<int>(p.ldk);
+  a.nk = static_cast<int>(p.ldk / 64);
+  a.K = static_cast<int>(K);
+  a.tiles_m = static_cast<int>(cdiv(M, 256));
+  a.tiles_n = static_cast<int>(cdiv(N, 256));
+  if (p.stage_a && K > 0) {
+    uint8_t* da = w + p.a_off;
+    const unsigned g = grid_for(M * (p.ldk / 16), kBlock);
+    if (p.u8) k_stage_rows<true><<<g, kBlock, 0, s>>>(a.a, M, p.kb, p.ldk, da);
+    else k_stage_rows<false><<<g, kBlock, 0, s>>>(a.a, M, p.kb, p.ldk, da);
+    a.a = da;
+  }
+  if (p.stage_b && K > 0) {
+    uint8_t* db = w + p.b_off;
+    if (b_layout == CBQ_MM_B_KN) {
+      const dim3 g(static_cast<unsigned>(cdiv(N, 64)), static_cast<unsigned>(cdiv(p.ldk / p.es, 64)));
+      if (p.es == 2) k_stage_bt<2, false><<<g, kBlock, 0, s>>>(a.bt, K, N, p.ldk, db);
+      else if (p.u8) k_stage_bt<1, true><<<g, kBlock, 0, s>>>(a.bt, K, N, p.ldk, db);
+      else k_stage_bt<1, false><<<g, kBlock, 0, s>>>(a.bt, K, N, p.ldk, db);
+    } else {
+      const unsigned g = grid_for(N * (p.ldk / 16), kBlock);
+      if (p.u8) k_stage_rows<true><<<g, kBlock, 0, s>>>(a.bt, N, p.kb, p.ldk, db);
+      else k_stage_rows<false><<<g, kBlock, 0, s>>>(a.bt, N, p.kb, p.ldk, db);
+    }
+    a.bt = db;
+  }
+  if (p.u8 && K > 0) {   // K == 0: the empty contraction, C = 0, needs no correction
+    int* rs = reinterpret_cast<int*>(w + p.rs_off);
+    int* cs = reinterpret_cast<int*>(w + p.cs_off);
+    k_row_sums<<<grid_for(M, 1), kBlock, 0, s>>>(a.a, M, p.ldk, rs);
+    k_row_sums<<<grid_for(N, 1), kBlock, 0, s>>>(a.bt, N, p.ldk, cs);
+    a.row_sum = rs;
+    a.col_sum = cs;
+  }
+  if (p.in == kInI8) {
+    launch_mm<kInI8, kOutI32>(a, s);
+    if (a.col_sum)
+      k_u8_fix<<<grid_for(M * (N / 4), kBlock), kBlock, 0, s>>>(static_cast<int*>(C), M, N,
+                                                               a.row_sum, a.col_sum, K);
+  }
+  else if (p.in == kInF16 && out_dtype == CBQ_F16) launch_mm<kInF16, kOutF16>(a, s);
+  else if (p.in == kInF16) launch_mm<kInF16, kOutF32>(a, s);
+  else launch_mm<kInBF16, kOutF32>(a, s);
+  return launch_status(what);
+}

@@ -37,6 +37,8 @@ typedef void* cbq_stream_t;
 
 /* Floating-point dtype codes for activations, inputs and outputs. */
 enum { CBQ_F32 = 0, CBQ_F16 = 1, CBQ_BF16 = 2 };
+/* Integer dtype codes (GEMM operands and accumulators). */
+enum { CBQ_I8 = 3, CBQ_U8 = 4, CBQ_I32 = 5 };
 
 /* Status codes. */
 enum { CBQ_OK = 0, CBQ_EINVAL = 1, CBQ_ELAUNCH = 2 };
@@ -202,6 +204,31 @@ int cbq_w8a16_linear(const void* x, int act_dtype, const int8_t* wq,
                      const int64_t* outlier_cols, int64_t n_out,
                      const void* w_out, int64_t M, int64_t N, int64_t K,
                      void* ws, size_t ws_bytes, void* y, cbq_stream_t stream);
+
+/* ---- Dense GEMM on the matrix cores -------------------------------------- */
+
+/* Storage of B for cbq_mm: [K, N] row-major (the reference's layout), or
+ * [N, K] row-major, i.e. B = W^T for a weight W [N, K] (read in place). */
+enum { CBQ_MM_B_KN = 0, CBQ_MM_B_NK = 1 };
+
+/* Workspace bytes for cbq_mm at this shape: the control block, plus staging
+ * buffers when B is [K, N] (transposed copy), the inputs are uint8 (offset
+ * copies and row sums) or K * element bytes is not a multiple of 64 (padded
+ * copies). */
+size_t cbq_mm_ws_bytes(int64_t M, int64_t N, int64_t K, int in_dtype,
+                       int b_layout);
+
+/* Replaces wmma_gemm (kernels/cuda/wmma.cu:186-261, kernel :29-169), bound as
+ * bindings/cuda/wmma.py:15-43: C[M,N] = A[M,K] . B[K,N], row-major A and C.
+ * in_dtype -> out_dtype, as the reference's precision table:
+ *   CBQ_I8 -> CBQ_I32, CBQ_U8 -> CBQ_I32 (exact modulo 2^32),
+ *   CBQ_F16 -> CBQ_F32 or CBQ_F16, CBQ_BF16 -> CBQ_F32
+ * (fp32 accumulation; fp16 output rounded once at the end).
+ * M, N, K multiples of 16 (the reference's WMMA constraint); A and B 16-byte
+ * aligned; ws: cbq_mm_ws_bytes(...) bytes, 256-byte aligned. */
+int cbq_mm(const void* A, const void* B, int in_dtype, int b_layout,
+           int64_t M, int64_t N, int64_t K, void* C, int out_dtype, void* ws,
+           size_t ws_bytes, cbq_stream_t stream);
 
 #ifdef __cplusplus
 }

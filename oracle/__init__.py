@@ -75,6 +75,8 @@ def _declare(L: ctypes.CDLL) -> ctypes.CDLL:
         "cbo_dequant_int8_tensor": (I32, [P, P, I64, P, I32]),
         "cbo_dequant_int8_channel": (I32, [P, P, I64, I64, I32, P, I32]),
         "cbo_dequant_int8_group": (I32, [P, P, I64, I64, P, I32]),
+        "cbo_mm_int8": (I32, [P, P, I32, I32, I64, I64, I64, P]),
+        "cbo_mm_float": (I32, [P, P, I32, I32, I64, I64, I64, P]),
         "cbo_w8a16_linear": (I32, [P, I32, P, I64, P, P, P, P, I64, P,
                                    I64, I64, I64, P, I64, P]),
     }
@@ -270,3 +272,32 @@ def w8a16_linear(x, act_code, wq, scales, bias=None, normal_cols=None,
                                   _ptr(bias), _ptr(oc), n_out, _ptr(wo), M, N, K, _ptr(r),
                                   R, _ptr(y)), "w8a16_linear")
     return y
+
+
+def mm_int8(a: np.ndarray, b: np.ndarray, b_nk: bool = False) -> np.ndarray:
+    """C = a . b for int8 or uint8 operands, int32 accumulation wrapping modulo
+    2^32 (wmma.cu:29-169 with int32 fragments). a: [M, K]; b: [K, N], or [N, K]
+    when b_nk (b holds B^T)."""
+    assert a.dtype == b.dtype and a.dtype in (np.int8, np.uint8)
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b)
+    M, K = a.shape
+    N = b.shape[0] if b_nk else b.shape[1]
+    assert (b.shape[1] if b_nk else b.shape[0]) == K
+    c = np.empty((M, N), np.int32)
+    _check(lib().cbo_mm_int8(_ptr(a), _ptr(b), int(a.dtype == np.uint8), int(b_nk), M, N, K,
+                             _ptr(c)), "mm_int8")
+    return c
+
+
+def mm_float(a: np.ndarray, b: np.ndarray, dtype_code: int, b_nk: bool = False) -> np.ndarray:
+    """C = a . b for fp16 / bf16 bit patterns (np.uint16), accumulated in
+    double (wmma.cu:29-169 with fp32 fragments). Shapes as mm_int8."""
+    a = np.ascontiguousarray(a, np.uint16)
+    b = np.ascontiguousarray(b, np.uint16)
+    M, K = a.shape
+    N = b.shape[0] if b_nk else b.shape[1]
+    c = np.empty((M, N), np.float64)
+    _check(lib().cbo_mm_float(_ptr(a), _ptr(b), dtype_code, int(b_nk), M, N, K, _ptr(c)),
+           "mm_float")
+    return c

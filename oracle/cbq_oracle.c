@@ -344,3 +344,52 @@ int cbo_w8a16_linear(const void* x, int act_dtype, const int8_t* wq,
     }
     return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Dense GEMM (kernels/cuda/wmma.cu:29-169, host :186-261)                  */
+/* ------------------------------------------------------------------------ */
+
+/* C[m][n] = sum_k A[m][k] * B[k][n] with 8-bit integer operands (is_unsigned:
+ * uint8, else int8) and int32 accumulation; the sum wraps modulo 2^32 as the
+ * reference's int32 accumulator fragments do (wmma.cu:229-250). A is [M, K]
+ * row-major; B is [K, N] row-major (b_nk == 0) or stored [N, K] (b_nk != 0). */
+int cbo_mm_int8(const void* A, const void* B, int is_unsigned, int b_nk, int64_t M,
+                int64_t N, int64_t K, int32_t* C) {
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t n = 0; n < N; ++n) {
+            uint32_t acc = 0;
+            for (int64_t k = 0; k < K; ++k) {
+                const int64_t ib = b_nk ? n * K + k : k * N + n;
+                int32_t a, b;
+                if (is_unsigned) {
+                    a = ((const uint8_t*)A)[m * K + k];
+                    b = ((const uint8_t*)B)[ib];
+                } else {
+                    a = ((const int8_t*)A)[m * K + k];
+                    b = ((const int8_t*)B)[ib];
+                }
+                acc += (uint32_t)(a * b);
+            }
+            C[m * N + n] = (int32_t)acc;
+        }
+    return 0;
+}
+
+/* The same for fp16 / bf16 operands (dtype codes as above), accumulated in
+ * double: the exact product sum rounded once to double; callers compare
+ * against it with a tolerance (the reference accumulates in fp32 or fp16
+ * fragments, wmma.cu:173-176). */
+int cbo_mm_float(const void* A, const void* B, int dtype, int b_nk, int64_t M, int64_t N,
+                 int64_t K, double* C) {
+    if (dtype != DT_F16 && dtype != DT_BF16) return 1;
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t n = 0; n < N; ++n) {
+            double acc = 0.0;
+            for (int64_t k = 0; k < K; ++k) {
+                const int64_t ib = b_nk ? n * K + k : k * N + n;
+                acc += (double)load_one(A, dtype, m * K + k) * (double)load_one(B, dtype, ib);
+            }
+            C[m * N + n] = acc;
+        }
+    return 0;
+}

@@ -78,6 +78,14 @@ int cbo_w8a16_linear(const void* x, int act_dtype, const int8_t* wq,
                      const void* w_out, int64_t M, int64_t N, int64_t K,
                      const int64_t* rows_idx, int64_t n_rows, float* y);
 
+/* Dense GEMM restatements (wmma.cu): C = A[M,K] . B, B [K,N] or stored [N,K]
+ * (b_nk). 8-bit integers with wrapping int32 accumulation; fp16 / bf16 with
+ * double accumulation. */
+int cbo_mm_int8(const void* A, const void* B, int is_unsigned, int b_nk, int64_t M,
+                int64_t N, int64_t K, int32_t* C);
+int cbo_mm_float(const void* A, const void* B, int dtype, int b_nk, int64_t M, int64_t N,
+                 int64_t K, double* C);
+
 #ifdef __cplusplus
 }
 #endif

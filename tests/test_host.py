@@ -34,7 +34,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     L = _lib()
     names = declared_symbols()
-    assert len(names) == 19
+    assert len(names) == 21
     for n in names:
         assert hasattr(L, n), n
     from cublade_amd import _abi
@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_slot():
     L = _lib()
-    assert L.cbq_abi_version() == 102
+    assert L.cbq_abi_version() == 103
     assert L.cbq_last_error() in (b"",) or isinstance(L.cbq_last_error(), bytes)
 
 
@@ -129,6 +129,46 @@ def test_nd_entry_points_validate_and_size():
     # empty shapes are no-ops
     assert L.cbq_quant_int8_group_nd(None, F16, 0, 64, 3, 32, 1e-12, None, None, None) == 0
     assert L.cbq_dequant_int8_channel_nd(None, None, 5, 0, 3, None, F16, None) == 0
+
+
+def test_mm_entry_point_validates_and_sizes():
+    """cbq_mm: workspace sizes per staging case and argument checks that fail
+    before any device work (the reference's wmma.cu:188-258 checks)."""
+    L = _lib()
+    from cublade_amd import _abi
+    C = _abi.WS_CTRL_BYTES
+    I8, U8, F16, BF16, F32, I32 = (_abi.I8, _abi.U8, _abi.F16, _abi.BF16, _abi.F32, _abi.I32)
+    KN, NK = _abi.MM_B_KN, _abi.MM_B_NK
+
+    def a256(v):
+        return (v + 255) // 256 * 256
+
+    # int8, B stored [N, K], K * 1 % 64 == 0: both operands read in place
+    assert L.cbq_mm_ws_bytes(8192, 8192, 8192, I8, NK) == C
+    # B [K, N]: transposed copy of B (N rows of K bytes)
+    assert L.cbq_mm_ws_bytes(512, 256, 128, I8, KN) == a256(C + 256 * 128)
+    # K * 1 % 64 != 0: both operands padded to 64-byte rows
+    assert L.cbq_mm_ws_bytes(32, 48, 80, I8, NK) == a256(a256(C + 32 * 128) + 48 * 128)
+    # uint8: offset copies of both plus int32 row / column sums
+    assert L.cbq_mm_ws_bytes(32, 48, 64, U8, NK) == \
+        a256(a256(a256(a256(C + 32 * 64) + 48 * 64) + 32 * 4) + 48 * 4)
+    # fp16: 2-byte elements, K = 48 -> 96 bytes -> 128-byte rows
+    assert L.cbq_mm_ws_bytes(16, 16, 48, F16, NK) == a256(a256(C + 16 * 128) + 16 * 128)
+    assert L.cbq_mm_ws_bytes(16, 16, 64, BF16, NK) == C
+    P = ctypes.c_void_p
+    f = P(0x10000)
+    ws = P(0x100000)
+    _einval(L.cbq_mm(f, f, 9, NK, 16, 16, 16, f, I32, ws, 1 << 20, None), "unsupported dtype")
+    _einval(L.cbq_mm(f, f, I8, NK, 16, 16, 16, f, F32, ws, 1 << 20, None), "int32 accumulator")
+    _einval(L.cbq_mm(f, f, BF16, NK, 16, 16, 16, f, F16, ws, 1 << 20, None), "float32")
+    _einval(L.cbq_mm(f, f, F16, NK, 16, 16, 16, f, I32, ws, 1 << 20, None), "float16")
+    _einval(L.cbq_mm(f, f, I8, 7, 16, 16, 16, f, I32, ws, 1 << 20, None), "b_layout")
+    _einval(L.cbq_mm(f, f, I8, NK, 24, 16, 16, f, I32, ws, 1 << 20, None), "multiples of 16")
+    _einval(L.cbq_mm(P(0x10008), f, I8, NK, 16, 16, 16, f, I32, ws, 1 << 20, None), "aligned")
+    _einval(L.cbq_mm(f, f, I8, KN, 16, 16, 16, f, I32, ws, 100, None), "workspace")
+    _einval(L.cbq_mm(f, f, I8, KN, 16, 16, 16, f, I32, P(0x100010), 1 << 20, None), "workspace")
+    # empty outputs are a no-op
+    assert L.cbq_mm(None, None, I8, NK, 0, 16, 16, None, I32, None, 0, None) == 0
 
 
 def test_loader_memoises_failures(tmp_path):
