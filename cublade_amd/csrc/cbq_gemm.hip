@@ -14,10 +14,15 @@
 // Integer results are exact modulo 2^32 (int32 wrap-around, as the int32
 // accumulators of the reference).
 //
-// k_mm_dma<IN, OUT>: 256 x 256 output tiles, 4 waves of 128 x 128 (4 x 4
-// tiles of 32 x 32), k-steps of 64 bytes per row (64 int8 or 32 fp16 k), four
-// LDS stages of 32 KiB filled by LDS DMA (global_load_lds_dwordx4), three
-// k-steps in flight. Both operands are K-contiguous rows: A [M, K] as given
+// k_mm_dma<IN, OUT>: 256 x 256 output tiles, 8 waves (two per SIMD) of
+// 128 (m) x 64 (n) (4 x 2 tiles of 32 x 32), k-steps of 64 bytes per row (64
+// int8 or 32 fp16 k), four LDS stages of 32 KiB filled by LDS DMA
+// (global_load_lds_dwordx4), three k-steps in flight, one barrier per k-step
+// placed between its two MFMA substeps so that the next k-step's fragment
+// reads overlap the second substep's MFMAs. Measured on MI355X at 8192^3
+// (random data): two waves per SIMD raise rocprof's MfmaUtil from ~47% to
+// 58% (int8) / 65% (fp16); the int8 kernel then runs level with hipBLASLt.
+// Both operands are K-contiguous rows: A [M, K] as given
 // and B as B^T [N, K]. A B that is stored [N, K] (B = W^T, the usual weight
 // layout) is read in place; a [K, N] B is transposed into the workspace
 // first (k_stage_bt). uint8 operands and row lengths that are not a multiple
@@ -34,6 +39,7 @@
 // 4 (l / 32) + v % 4, so each store instruction writes two 128-byte runs of a
 // row (int32 / fp32).
 #include <algorithm>
+#include <type_traits>
 
 #include "cbq_device.h"
 #include "cbq_host.h"
@@ -102,31 +108,32 @@ __device__ __forceinline__ void mm_tile(int b, const MmArgs& a, int& tm, int& tn
 constexpr int kMmNS = 4;                 // LDS stages
 constexpr int kMmHalf = 256 * 64;        // bytes of one operand per stage
 constexpr int kMmSB = 2 * kMmHalf;       // stage bytes (32 KiB)
-constexpr int kMmL = kMmHalf / (256 * 16);   // DMA instructions per operand per thread (4)
+constexpr int kMmThreads = 512;          // 8 waves, two per SIMD
+constexpr int kMmL = kMmHalf / (kMmThreads * 16);   // DMA instructions per operand per thread (2)
 
 template <int IN, int OUT>
-__global__ __launch_bounds__(256) void k_mm_dma(MmArgs a) {
+__global__ __launch_bounds__(kMmThreads) void k_mm_dma(MmArgs a) {
   typedef typename AccOf<IN>::type Acc;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kMmNS * kMmSB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave & 1, wn = wave >> 1;   // 128-row half of m, 64-column quarter of n
   int tm, tn;
   mm_tile(blockIdx.x, a, tm, tn);
   const int m0 = tm * 256, n0 = tn * 256;
   const int nk = a.nk;
   const uint32_t sbase = __builtin_amdgcn_readfirstlane(lds_addr(smem));
 
-  // DMA sources: instruction u of an operand fills rows (u * 4 + wave) * 16
+  // DMA sources: instruction u of an operand fills rows (u * 8 + wave) * 16
   // + lane / 4, chunk slot lane % 4, which holds source chunk slot ^ swizzle.
   // Rows past M or N are clamped to the last row; their products land in
   // outputs that are never stored.
   uint32_t ao[kMmL], bo[kMmL];
 #pragma unroll
   for (int u = 0; u < kMmL; ++u) {
-    const int row = (u * 4 + wave) * 16 + (lane >> 2);
+    const int row = (u * 8 + wave) * 16 + (lane >> 2);
     const int c = (lane & 3) ^ ((row >> 2) & 3);
     ao[u] = static_cast<uint32_t>(min(m0 + row, a.M - 1)) * static_cast<uint32_t>(a.ldk) + c * 16u;
     bo[u] = static_cast<uint32_t>(min(n0 + row, a.N - 1)) * static_cast<uint32_t>(a.ldk) + c * 16u;
@@ -136,9 +143,9 @@ __global__ __launch_bounds__(256) void k_mm_dma(MmArgs a) {
     const uint8_t* pa = uniform_ptr(a.a + t * 64);
     const uint8_t* pb = uniform_ptr(a.bt + t * 64);
 #pragma unroll
-    for (int u = 0; u < kMmL; ++u) lds_dma16(ao[u], pa, dst + u * 4096);
+    for (int u = 0; u < kMmL; ++u) lds_dma16(ao[u], pa, dst + u * 8192);
 #pragma unroll
-    for (int u = 0; u < kMmL; ++u) lds_dma16(bo[u], pb, dst + kMmHalf + u * 4096);
+    for (int u = 0; u < kMmL; ++u) lds_dma16(bo[u], pb, dst + kMmHalf + u * 8192);
   };
 
   // Fragment read offsets: row r32 of 32-row tile j (A) / i (B^T), chunk
@@ -149,76 +156,109 @@ __global__ __launch_bounds__(256) void k_mm_dma(MmArgs a) {
   for (int s = 0; s < 2; ++s) {
     const uint32_t slot = static_cast<uint32_t>((2 * h + s) ^ ((r32 >> 2) & 3)) << 4;
     ar[s] = (wm * 128 + r32) * 64 + slot;
-    br[s] = kMmHalf + (wn * 128 + r32) * 64 + slot;
+    br[s] = kMmHalf + (wn * 64 + r32) * 64 + slot;
   }
 
-  const int mw = m0 + wm * 128, nw = n0 + wn * 128;
-  Acc acc[4][4];   // [j: m-tile][i: n-tile]
+  const int mw = m0 + wm * 128, nw = n0 + wn * 64;
+  Acc acc[4][2];   // [j: m-tile][i: n-tile]
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[j][i] = Acc{};
+    for (int i = 0; i < 2; ++i) acc[j][i] = Acc{};
 
+  // Fragments of one k-substep: 4 A tiles, 2 B^T tiles (6 reads, 8 MFMAs).
   struct Frags {
-    u32x4 x[4];   // A, m-tiles
-    u32x4 w[4];   // B^T, n-tiles
+    u32x4 x[4];
+    u32x4 w[2];
+  };
+  auto read_one = [&](int stage, int s, Frags& f, int r) {
+    const uint8_t* st = smem + stage * kMmSB;
+    if (r < 4) f.x[r] = *reinterpret_cast<const u32x4*>(st + ar[s] + r * 2048);
+    else f.w[r - 4] = *reinterpret_cast<const u32x4*>(st + br[s] + (r - 4) * 2048);
   };
   auto read = [&](int stage, int s, Frags& f) {
-    const uint8_t* st = smem + stage * kMmSB;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) f.x[j] = *reinterpret_cast<const u32x4*>(st + ar[s] + j * 2048);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) f.w[i] = *reinterpret_cast<const u32x4*>(st + br[s] + i * 2048);
+    for (int r = 0; r < 6; ++r) read_one(stage, s, f, r);
   };
-  // 16 MFMAs; an accumulator is reused every 16th, so no back-to-back
-  // dependent MFMA.
-  auto mma = [&](const Frags& f) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[j][i] = mfma32<IN>(f.x[j], f.w[i], acc[j][i]);
+  // MFMA q (0..7) of a substep: tile (j, i) = (q / 2, q % 2); an accumulator
+  // is reused every 8th MFMA.
+  auto mma_one = [&](const Frags& f, int q) {
+    acc[q >> 1][q & 1] = mfma32<IN>(f.x[q >> 1], f.w[q & 1], acc[q >> 1][q & 1]);
   };
 
-  // Prologue: tiles 0 .. NS - 2 in flight.
+  // Step t: F0 / F1 hold the fragments of tile t's substeps 0 / 1. The
+  // substep-0 MFMAs run; then the wait for tile t + 1 and the barrier (which
+  // also means every wave is past its reads of tile t - 1, whose stage tile
+  // t + 3 takes); then the DMA of tile t + 3, the substep-1 MFMAs with tile
+  // t + 1's substep-0 reads between them, and tile t + 1's substep-1 reads.
+  // The other wave of the SIMD fills the MFMA pipe while a wave waits.
+  Frags f0, f1;
+  // One step (see above). DMA: issue tile t + 3; ALL: tile t + 1 is the last
+  // tile in flight (wait for everything).
+  auto step = [&](int t, auto dma, auto all) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) mma_one(f0, q);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (decltype(all)::value) dma_wait_barrier<0>();
+    else dma_wait_barrier<2 * kMmL>();
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (decltype(dma)::value) issue(t + kMmNS - 1, (t + kMmNS - 1) % kMmNS);
+    const int next = (t + 1) % kMmNS;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      mma_one(f1, q);
+      if (q < 6) read_one(next, 0, f0, q);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    read(next, 1, f1);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  using yes = std::true_type;
+  using no = std::false_type;
 #pragma unroll
   for (int t = 0; t < kMmNS - 1; ++t)
     if (t < nk) issue(t, t);
-  Frags f0, f1;
-  for (int t = 0; t < nk; ++t) {
-    // Tile t has landed once only the DMAs of the (at most two) later tiles
-    // issued so far are outstanding; the barrier also means every wave is
-    // done reading stage (t - 1) % NS, which tile t + 3 overwrites.
-    const int later = min(kMmNS - 2, nk - 1 - t);
-    if (later >= 2) dma_wait_barrier<2 * 2 * kMmL>();
-    else if (later == 1) dma_wait_barrier<2 * kMmL>();
+  if (nk > 0) {
+    if (nk > 2) dma_wait_barrier<2 * 2 * kMmL>();
+    else if (nk > 1) dma_wait_barrier<2 * kMmL>();
     else dma_wait_barrier<0>();
-    const int stage = t % kMmNS;
-    read(stage, 0, f0);
-    read(stage, 1, f1);
-    if (t + kMmNS - 1 < nk) issue(t + kMmNS - 1, (t + kMmNS - 1) % kMmNS);
-    mma(f0);
-    mma(f1);
+    read(0, 0, f0);
+    read(0, 1, f1);
+    int t = 0;
+    for (; t + kMmNS - 1 < nk; ++t) step(t, yes{}, no{});    // tiles t + 1, t + 2 in flight
+    if (t + 2 < nk) step(t++, no{}, no{});                  // tile t + 2 still in flight
+    if (t + 1 < nk) step(t++, no{}, yes{});
+#pragma unroll
+    for (int q = 0; q < 8; ++q) mma_one(f0, q);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) mma_one(f1, q);
   }
 
-  // Epilogue: C[m][n], n = 32 i + r32, m = 32 j + 8 (v / 4) + 4 h + v % 4.
+  // Epilogue: C[m][n], n = 32 i + r32, m = 32 j + 8 (v / 4) + 4 h + v % 4;
+  // 32-bit offsets from the wave's corner (128 rows of N elements).
+  constexpr int ES_OUT = OUT == kOutF16 ? 2 : 4;
+  uint8_t* cw = static_cast<uint8_t*>(a.c) + (static_cast<int64_t>(mw) * a.N + nw) * ES_OUT;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int n = nw + 32 * i + r32;
-      if (n >= a.N) continue;
+    for (int i = 0; i < 2; ++i) {
+      const int nl = 32 * i + r32;
+      if (nw + nl < a.N) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int m = mw + 32 * j + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (m >= a.M) continue;
-        const int64_t off = static_cast<int64_t>(m) * a.N + n;
-        if constexpr (OUT == kOutI32)
-          static_cast<int*>(a.c)[off] = acc[j][i][v];
-        else if constexpr (OUT == kOutF32)
-          static_cast<float*>(a.c)[off] = acc[j][i][v];
-        else
-          static_cast<_Float16*>(a.c)[off] = static_cast<_Float16>(acc[j][i][v]);
+        for (int v = 0; v < 16; ++v) {
+          const int ml = 32 * j + 8 * (v >> 2) + 4 * h + (v & 3);
+          if (mw + ml < a.M) {
+            const uint32_t off = (static_cast<uint32_t>(ml) * static_cast<uint32_t>(a.N) + nl) * ES_OUT;
+            if constexpr (OUT == kOutI32)
+              *reinterpret_cast<int*>(cw + off) = acc[j][i][v];
+            else if constexpr (OUT == kOutF32)
+              *reinterpret_cast<float*>(cw + off) = acc[j][i][v];
+            else
+              *reinterpret_cast<_Float16*>(cw + off) = static_cast<_Float16>(acc[j][i][v]);
+          }
+        }
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
@@ -393,7 +433,7 @@ bool mm_plan(int64_t M, int64_t N, int64_t K, int in_dtype, int b_layout, MmPlan
 
 template <int IN, int OUT>
 void launch_mm(const MmArgs& a, hipStream_t s) {
-  k_mm_dma<IN, OUT><<<dim3(static_cast<unsigned>(a.tiles_m * a.tiles_n)), dim3(256), 0, s>>>(a);
+  k_mm_dma<IN, OUT><<<dim3(static_cast<unsigned>(a.tiles_m * a.tiles_n)), dim3(kMmThreads), 0, s>>>(a);
 }
 
 unsigned grid_for(int64_t work, int64_t per_block) {
