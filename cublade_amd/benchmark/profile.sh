@@ -6,9 +6,12 @@
 # 1. kernel trace of bench.py (BASELINE configs[1] step + W8A16 M=4096)
 # 2. FETCH_SIZE and WRITE_SIZE of bench.py (one counter per run), and of a
 #    256 MiB device copy (copy_calib.py) to calibrate both counters
-# 3. kernel trace of the per-config suite (configs 1-5)
+# 3. kernel trace of the per-config suite (configs 1-5 and the next rows)
+# 4. rocprof's derived MfmaUtil counter (MFMA busy cycles over active cycles
+#    x SIMDs) for the MFMA kernels: W8A16 (config 5) and the dense GEMM (f4)
 # Summaries: OUTDIR/bench_c2_kernels.txt, OUTDIR/dequant_int8_c2_traffic.json,
-# OUTDIR/suite_kernels.txt, OUTDIR/suite.json. Raw databases stay in OUTDIR/raw.
+# OUTDIR/suite_kernels.txt, OUTDIR/suite.json, OUTDIR/mfma_util.txt. Raw
+# databases stay in OUTDIR/raw.
 # Run from the repository root on a GPU machine. Every GPU step has its own
 # time limit; the script stops at the first failing step.
 set -u
@@ -40,6 +43,10 @@ step "kernel trace: suite"
 timeout -k 10 500 rocprofv3 --kernel-trace --stats -d "$RAW/suite" -o suite -- \
   $PY -m cublade_amd.benchmark.suite --reps 10 --json "$OUT/suite.json" > "$RAW/suite.log" 2>&1 || exit $?
 
+step "counter MfmaUtil: suite configs c5,f4"
+timeout -s KILL 300 rocprofv3 --pmc MfmaUtil --kernel-trace -d "$RAW/mfma" -o suite -- \
+  $PY -m cublade_amd.benchmark.suite --configs c5,f4 --reps 3 --warmup 1 > "$RAW/mfma.log" 2>&1 || exit $?
+
 step "summaries"
 {
   echo "# rocprofv3 kernel trace of bench.py (BASELINE configs[1] step, W8A16 M=4096 extra)"
@@ -60,4 +67,10 @@ $R traffic "k_deq_tensor<false, 1>" "$RAW/fetch/bench_results.db" "$RAW/write/be
   echo "# durations in microseconds"
   $R kernels "$RAW/suite/suite_results.db"
 } > "$OUT/suite_kernels.txt" || exit $?
+{
+  echo "# rocprof derived counter MfmaUtil = sum(SQ_VALU_MFMA_BUSY_CYCLES) / (max(GRBM_GUI_ACTIVE) * SIMDs) * 100,"
+  echo "# per kernel (mean over dispatches): W8A16 (suite config c5, M = 16 / 256 / 4096) and the dense GEMM (f4, 8192^3)"
+  echo "# command: rocprofv3 --pmc MfmaUtil --kernel-trace -d RAW/mfma -o suite -- python -u -m cublade_amd.benchmark.suite --configs c5,f4 --reps 3 --warmup 1"
+  $R counters "$RAW/mfma/suite_results.db" | grep -E "k_gemm_dma|k_stream|k_skinny|k_gemm<|k_mm_dma|Cijk"
+} > "$OUT/mfma_util.txt" || exit $?
 step "done"

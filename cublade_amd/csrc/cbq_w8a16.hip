@@ -30,8 +30,9 @@
 // workgroups resident on one XCD share activation and weight k-slices in L2.
 //
 // k_gemm_dma<ACT> (M >= 1024, K % 64 == 0): 256 x 256 tiles of
-// v_mfma_f32_32x32x16 fed by LDS DMA, int8 weights widened after the
-// fragment read, explicitly scheduled k-steps (see the kernel's comment).
+// v_mfma_f32_32x32x16 fed by LDS DMA, 8 waves (two per SIMD), int8 weights
+// widened after the fragment read, explicitly scheduled k-steps (see the
+// kernel's comment).
 //
 // k_stream1<ACT> (M <= 16) and k_stream<ACT, TM> (M <= 64): persistent
 // weight streaming for large weights (see the kernels' comments).
@@ -323,17 +324,20 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm(GemmArgs a) {
 // ---------------------------------------------------------------------------
 // k_gemm_dma<ACT>: large-M tile kernel fed by LDS DMA.
 //
-// Tile 256 (m) x 256 (n) x 64 (k), 4 waves in 2 x 2, each wave 128 x 128 as
-// 4 x 4 tiles of v_mfma_f32_32x32x16_{f16,bf16} (256 accumulator registers).
-// On MI355X this MFMA runs at the full dense rate (2.47 PFLOP/s measured),
-// the 16x16x32 form at about half of it. Operand tiles go from global memory
+// Tile 256 (m) x 256 (n) x 64 (k), 8 waves (two per SIMD) in 2 (m) x 4 (n),
+// each wave 128 x 64 as 4 x 2 tiles of v_mfma_f32_32x32x16_{f16,bf16} (128
+// accumulator registers). On MI355X this MFMA runs at the full dense rate
+// (2.47 PFLOP/s measured), the 16x16x32 form at about half of it. With two
+// waves per SIMD one wave's MFMAs run while the other waits at the barrier or
+// for fragments: rocprof's MfmaUtil rose from 38% (4 waves of 128 x 128) to
+// 51% at M = 4096, N = 11008, K = 4096. Operand tiles go from global memory
 // straight into LDS with global_load_lds_dwordx4 (no VGPR staging, no LDS
 // store instructions): x as 256 rows of 128 bytes, the weight tile as 256
 // rows of 64 int8 codes. The codes are widened to the activation dtype after
 // the fragment read, so LDS holds half the bytes of a widened tile. Three
 // LDS stages (3 x 48 KiB): while the MFMAs of tile t run, tiles t + 1 and
 // t + 2 are in flight; each k-half's fragments are read while the previous
-// half is multiplied; one barrier per k-step.
+// half is multiplied; one barrier per k-step, between its two halves.
 //
 // LDS rows are XOR-swizzled at 16-byte granularity so that the 16 lanes of a
 // fragment read phase (16 rows, one 16-byte chunk each) hit 16 distinct
@@ -362,21 +366,24 @@ __device__ __forceinline__ f16x mfma32x32x16(const u32x4& a, const u32x4& b, f16
                                                    __builtin_bit_cast(b8, b), c, 0, 0, 0);
 }
 
+constexpr int kDmaThreads = 512;   // 8 waves, two per SIMD
+constexpr int kDmaTM = 4, kDmaTN = 2;   // 32 x 32 tiles per wave: x (m) x weight (n)
+
 template <int ACT, bool SPLIT>
-__global__ __launch_bounds__(256) void k_gemm_dma(GemmArgs a) {
+__global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
   constexpr int BM = 256, BN = 256, BK = 64, NS = 3;
   constexpr int XB = BM * BK * 2;          // x stage bytes (32 KiB)
   constexpr int WB = BN * BK;              // weight stage bytes (16 KiB)
   constexpr int SB = XB + WB;
-  constexpr int XL = XB / (256 * 16);      // DMA instructions per thread: 8
-  constexpr int WL = WB / (256 * 16);      // 4
-  constexpr int TM = 4, TN = 4;            // 32 x 32 tiles per wave
+  constexpr int XL = XB / (kDmaThreads * 16);   // DMA instructions per thread: 4
+  constexpr int WL = WB / (kDmaThreads * 16);   // 2
+  constexpr int TM = kDmaTM, TN = kDmaTN;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * SB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave & 1, wn = wave >> 1;   // 128 x rows, 64 weight rows
   // Split-K: workgroup b covers tile b % tiles of k-range b / tiles (after
   // the XCD renumbering, so the workgroups of one XCD share a k-range of x).
   int tm, tn, split = 0;
@@ -397,18 +404,22 @@ __global__ __launch_bounds__(256) void k_gemm_dma(GemmArgs a) {
   const int nk = SPLIT ? min(a.split_steps, a.K / BK - kb) : a.K / BK;
   const uint32_t sbase = __builtin_amdgcn_readfirstlane(lds_addr(smem));
 
-  // Per-lane DMA source offsets (bytes from the k0 column of the tile).
+  // Per-lane DMA source offsets (bytes from the k0 column of the tile). x
+  // instruction u fills rows (u * 8 + wave) * 8 + lane / 8 (128-byte rows,
+  // 8 chunks); weight instruction u fills rows (u * 8 + wave) * 16 + lane / 4
+  // (64-byte rows, 4 chunks). Each lane loads the source chunk its LDS slot
+  // holds under the swizzle.
   uint32_t xo[XL], wo[WL];
 #pragma unroll
   for (int u = 0; u < XL; ++u) {
-    const int row = (u * 4 + wave) * 8 + (lane >> 3);
+    const int row = (u * 8 + wave) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((row >> 1) & 7);
     const int m = min(m0 + row, a.M - 1);
     xo[u] = static_cast<uint32_t>(m) * static_cast<uint32_t>(a.K) * 2u + c * 16u;
   }
 #pragma unroll
   for (int u = 0; u < WL; ++u) {
-    const int row = (u * 4 + wave) * 16 + (lane >> 2);
+    const int row = (u * 8 + wave) * 16 + (lane >> 2);
     const int c = (lane & 3) ^ ((row >> 2) & 3);
     const int n = min(n0 + row, a.N - 1);
     wo[u] = static_cast<uint32_t>(n) * static_cast<uint32_t>(a.K) + c * 16u;
@@ -416,26 +427,27 @@ __global__ __launch_bounds__(256) void k_gemm_dma(GemmArgs a) {
   // DMA instruction u (0..XL+WL-1) of tile t into `stage`.
   auto issue_one = [&](int t, int stage, int u) {
     if (u < XL)
-      lds_dma16(xo[u], uniform_ptr(a.x + (kb + t) * BK), sbase + stage * SB + wave * 1024 + u * 4096);
+      lds_dma16(xo[u], uniform_ptr(a.x + (kb + t) * BK), sbase + stage * SB + wave * 1024 + u * 8192);
     else
       lds_dma16(wo[u - XL], uniform_ptr(a.wq + (kb + t) * BK),
-                sbase + stage * SB + XB + wave * 1024 + (u - XL) * 4096);
+                sbase + stage * SB + XB + wave * 1024 + (u - XL) * 8192);
   };
   auto issue = [&](int t, int stage) {
 #pragma unroll
     for (int u = 0; u < XL + WL; ++u) issue_one(t, stage, u);
   };
 
-  // Fragment read offsets within a stage: row r32 of each 32-row tile,
-  // lane half h.
+  // Fragment read offsets within a stage: row r32 of each 32-row tile, lane
+  // half h; x chunk 4 h + 2 e + s (half e, slice s), weight chunk 2 h + e.
   const int r32 = lane & 31, h = lane >> 5;
-  uint32_t xr[4], wr[2];
+  uint32_t xr[2][2], wr[2];
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
-    xr[q] = (wm * 128 + r32) * 128 + (((4 * h + q) ^ ((r32 >> 1) & 7)) << 4);
+  for (int e = 0; e < 2; ++e) {
 #pragma unroll
-  for (int e = 0; e < 2; ++e)
-    wr[e] = XB + (wn * 128 + r32) * 64 + (((2 * h + e) ^ ((r32 >> 2) & 3)) << 4);
+    for (int q = 0; q < 2; ++q)
+      xr[e][q] = (wm * 128 + r32) * 128 + (((4 * h + 2 * e + q) ^ ((r32 >> 1) & 7)) << 4);
+    wr[e] = XB + (wn * 64 + r32) * 64 + (((2 * h + e) ^ ((r32 >> 2) & 3)) << 4);
+  }
 
   f16x acc[TN][TM];
 #pragma unroll
@@ -443,29 +455,28 @@ __global__ __launch_bounds__(256) void k_gemm_dma(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < TM; ++j) acc[i][j] = f16x{};
 
-  // A k-step is two halves: half e takes weight chunk e (k [32 h + 16 e,
-  // +16) of the lane's row) and x chunks 2 e and 2 e + 1, i.e. MFMA k-slices
-  // q = 2 e and 2 e + 1. Two fragment register sets, one per half; the reads
-  // for the next half land in one set while the MFMAs consume the other.
+  // Half e of a k-step: weight chunk e of each lane's rows (k [32 h + 16 e,
+  // +16)) and x chunks 4 h + 2 e, 4 h + 2 e + 1: MFMA k-slices s = 0, 1 of the
+  // half. One fragment set per half: TN weight reads, then 2 TM x reads.
   struct Frags {
     u32x4 x[TM][2];
     u32x4 w[TN];
   };
   Frags fr[2];
-  // Fragment read r (0..11) of half e: 8 x reads (j = r / 2, q = r % 2),
-  // then 4 weight reads (i = r - 8).
   auto read_one = [&](int stage, int e, Frags& f, int r) {
     const uint8_t* st = smem + stage * SB;
-    if (r < 2 * TM)
-      f.x[r >> 1][r & 1] = *reinterpret_cast<const u32x4*>(st + xr[2 * e + (r & 1)] + (r >> 1) * 4096);
-    else
-      f.w[r - 2 * TM] = *reinterpret_cast<const u32x4*>(st + wr[e] + (r - 2 * TM) * 2048);
+    if (r < TN) {
+      f.w[r] = *reinterpret_cast<const u32x4*>(st + wr[e] + r * 2048);
+    } else {
+      const int rx = r - TN;
+      f.x[rx >> 1][rx & 1] = *reinterpret_cast<const u32x4*>(st + xr[e][rx & 1] + (rx >> 1) * 4096);
+    }
   };
   auto read_half = [&](int stage, int e, Frags& f) {
 #pragma unroll
     for (int r = 0; r < 2 * TM + TN; ++r) read_one(stage, e, f, r);
   };
-  // Widen word c (0..3: 4 codes) of row tile i's weight fragment into w.
+  // Widen word c (0..3: 4 codes) of weight tile i into w (slice c / 2).
   auto cvt_word = [&](const Frags& f, int i, int c, u32x4 (&w)[2]) {
     const uint32_t src = c == 0 ? f.w[i].x : c == 1 ? f.w[i].y : c == 2 ? f.w[i].z : f.w[i].w;
     uint32_t lo, hi;
@@ -474,94 +485,88 @@ __global__ __launch_bounds__(256) void k_gemm_dma(GemmArgs a) {
     w[q][k] = lo;
     w[q][k + 1] = hi;
   };
-  auto cvt_row = [&](const Frags& f, int i, u32x4 (&w)[2]) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) cvt_word(f, i, c, w);
+  // MFMA p (0 .. 2 TM - 1) of weight tile i: slice p / TM, x tile p % TM
+  // (an accumulator is reused TM MFMAs later).
+  auto mma_one = [&](const Frags& f, int i, const u32x4 (&w)[2], int p) {
+    const int q = p / TM, j = p % TM;
+    acc[i][j] = mfma32x32x16<ACT>(w[q], f.x[j][q], acc[i][j]);
   };
-  // MFMA pair p (0..3) of row tile i: k-slice q = p / 2, columns j = 2 (p % 2)
-  // and 2 (p % 2) + 1. Within a row tile, an accumulator is reused every
-  // fourth MFMA; a dependent back-to-back MFMA would wait for the whole
-  // latency of the previous one.
-  auto mma_pair = [&](const Frags& f, int i, const u32x4 (&w)[2], int p) {
-    const int q = p >> 1, j0 = (p & 1) * 2;
-    acc[i][j0] = mfma32x32x16<ACT>(w[q], f.x[j0][q], acc[i][j0]);
-    acc[i][j0 + 1] = mfma32x32x16<ACT>(w[q], f.x[j0 + 1][q], acc[i][j0 + 1]);
-  };
-  // Explicit schedule. Row tile i's 8 MFMAs run as 4 pairs; after pair p
-  // the wave issues other work for the next pair's 64 MFMA cycles: word p
-  // of the next row tile's widening, and in the second half the DMA of tile
-  // t + 3 (3 instructions per pair, row tile 0) and the reads of tile t + 1's
-  // first half (3 per pair, row tile 1). sched_barrier pins the order.
-  u32x4 wa[2], wb[2];   // widened weights: current and next row tile
+  // A half: weight tile i's 4 MFMAs, each followed by one word of the next
+  // tile's widening (tile 0 of the next half after the last tile) and by
+  // `extra` (DMA issue / fragment reads); sched_barrier pins the order.
+  u32x4 wa[2], wb[2];   // widened weights: current and next tile
   auto half = [&](Frags& f, Frags* fnext, auto&& extra) {
 #pragma unroll
     for (int i = 0; i < TN; ++i) {
       u32x4 (&cur)[2] = (i & 1) ? wb : wa;
       u32x4 (&nxt)[2] = (i & 1) ? wa : wb;
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        mma_pair(f, i, cur, p);
-        if (i + 1 < TN) cvt_word(f, i + 1, p, nxt);
-        else if (fnext) cvt_word(*fnext, 0, p, nxt);
+      for (int p = 0; p < 2 * TM; ++p) {
+        mma_one(f, i, cur, p);
+        if (p < 4) {
+          if (i + 1 < TN) cvt_word(f, i + 1, p, nxt);
+          else if (fnext) cvt_word(*fnext, 0, p, nxt);
+        }
         extra(i, p);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
-  // Step t: set 0 holds half 0 of tile t, set 1 half 1, wa row tile 0 of
+  // Step t: set 0 holds half 0 of tile t, set 1 half 1, wa weight tile 0 of
   // set 0 widened; tiles t + 1 and t + 2 are in flight. Half 0 (its last
-  // pairs widen row tile 0 of set 1); wait for tile t + 1 and barrier (every
-  // wave is past its reads of tile t's stage); half 1 with the DMA of tile
-  // t + 3 into that stage and the reads of tile t + 1's half 0 into set 0;
-  // then the reads of half 1 into set 1.
-  int stage_next = 1;   // stage of tile t + 1
-  auto step = [&](int t) {
-    const bool more = t + 1 < nk;
+  // tile widens tile 0 of set 1); the wait for tile t + 1 and the barrier,
+  // after which every wave is done with tile t's stage (its fragments were
+  // read during step t - 1), so the DMA of tile t + 3 goes there; half 1 with
+  // the DMA spread over its first tile and the reads of tile t + 1's half 0
+  // over its first two tiles; then the reads of half 1 into set 1. The other
+  // wave of the SIMD keeps the MFMA pipe busy while a wave waits.
+  auto step = [&](int t, auto dma, int nwait) {
     half(fr[0], &fr[1], [&](int, int) {});
-    if (more) {
-      if (t + 2 < nk) dma_wait_barrier<XL + WL>();
-      else dma_wait_barrier<0>();
-    }
     __builtin_amdgcn_sched_barrier(0);
-    const int stage_cur = stage_next == 0 ? NS - 1 : stage_next - 1;
-    const bool dma = t + 3 < nk;
-    half(fr[1], more ? &fr[0] : nullptr, [&](int i, int p) {
-      if (i == 0 && dma) {
-#pragma unroll
-        for (int u = 0; u < 3; ++u) issue_one(t + 3, stage_cur, p * 3 + u);
+    if (nwait >= 1) dma_wait_barrier<XL + WL>();
+    else dma_wait_barrier<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    const int stage_cur = t % NS, stage_next = (t + 1) % NS;
+    half(fr[1], &fr[0], [&](int i, int p) {
+      if constexpr (decltype(dma)::value) {
+        if (i == 0 && p < 3) {
+          issue_one(t + NS, stage_cur, 2 * p);
+          issue_one(t + NS, stage_cur, 2 * p + 1);
+        }
       }
-      if (more && i == 1) {
-#pragma unroll
-        for (int u = 0; u < 3; ++u) read_one(stage_next, 0, fr[0], p * 3 + u);
-      }
+      const int r = i * 2 * TM + p;
+      if (r < 2 * TM + TN) read_one(stage_next, 0, fr[0], r);
     });
-    if (more) {
-      read_half(stage_next, 1, fr[1]);
-      stage_next = stage_next == NS - 1 ? 0 : stage_next + 1;
-    }
+    read_half(stage_next, 1, fr[1]);
     __builtin_amdgcn_sched_barrier(0);
   };
+  using yes = std::true_type;
+  using no = std::false_type;
 
+#pragma unroll
+  for (int t = 0; t < NS; ++t)
+    if (t < nk) issue(t, t);
   if (nk > 0) {
-    issue(0, 0);
-    if (nk > 1) {
-      issue(1, 1);
-      dma_wait_barrier<XL + WL>();
-    } else {
-      dma_wait_barrier<0>();
-    }
-    if (nk > 2) issue(2, 2);
+    if (nk > 2) dma_wait_barrier<2 * (XL + WL)>();
+    else if (nk > 1) dma_wait_barrier<XL + WL>();
+    else dma_wait_barrier<0>();
     read_half(0, 0, fr[0]);
     read_half(0, 1, fr[1]);
-    cvt_row(fr[0], 0, wa);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) cvt_word(fr[0], 0, c, wa);
+    int t = 0;
+    for (; t + NS < nk; ++t) step(t, yes{}, 1);     // tile t + 2 in flight, DMA of t + 3
+    for (; t + 1 < nk; ++t) step(t, no{}, nk - 2 - t);
+    half(fr[0], &fr[1], [&](int, int) {});
+    half(fr[1], nullptr, [&](int, int) {});
   }
-  for (int t = 0; t < nk; ++t) step(t);
 
+  const int mw = m0 + wm * 128, nw = n0 + wn * 64;
   if constexpr (SPLIT) {
     // Partial tile in lane order: f4 (split, tile, wave, i, j, q, lane), one
     // contiguous 1 KiB store per (i, j, q); k_splitk_reduce finishes it.
     f4* dst = reinterpret_cast<f4*>(a.part) +
-              ((static_cast<int64_t>(split) * a.tiles_m * a.tiles_n + tn * a.tiles_m + tm) * 4 + wave) *
+              ((static_cast<int64_t>(split) * a.tiles_m * a.tiles_n + tn * a.tiles_m + tm) * 8 + wave) *
                   (TN * TM * 4 * 64) + lane;
 #pragma unroll
     for (int i = 0; i < TN; ++i)
@@ -576,14 +581,13 @@ __global__ __launch_bounds__(256) void k_gemm_dma(GemmArgs a) {
   // Epilogue. Accumulator values 4q .. 4q+3 of tile (i, j) are the wave's
   // outputs (m, n .. n+3) with m = 32 j + r32, n = 32 i + 8 q + 4 h. Each is
   // finished in fp32 (scale, outlier sum, bias, in that order), rounded once,
-  // and written to an LDS copy of the wave's 128 x 128 output tile; the tile
+  // and written to an LDS copy of the wave's 128 x 64 output tile; the tile
   // is then stored with 16-byte row-contiguous stores. The per-lane scales
   // are loaded once, before any output store.
-  constexpr int EPS = 136;   // LDS row stride of the output tile (halfs)
-  static_assert(4 * 128 * EPS * 2 <= NS * SB, "epilogue tile fits in LDS");
+  constexpr int EPS = 72;    // LDS row stride of the output tile (halfs)
+  static_assert(8 * 128 * EPS * 2 <= NS * SB, "epilogue tile fits in LDS");
   dma_wait_barrier<0>();     // every wave is done with the operand stages
   uint16_t* ep = reinterpret_cast<uint16_t*>(smem) + wave * (128 * EPS);
-  const int mw = m0 + wm * 128, nw = n0 + wn * 128;
 #pragma unroll
   for (int i = 0; i < TN; ++i) {
 #pragma unroll
@@ -612,11 +616,11 @@ __global__ __launch_bounds__(256) void k_gemm_dma(GemmArgs a) {
       }
     }
   }
-  // Row-contiguous stores: 16 lanes cover one 128-wide row (8 outputs each).
+  // Row-contiguous stores: 8 lanes cover one 64-wide row (8 outputs each).
   const bool vec16 = (a.N % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
 #pragma unroll 4
-  for (int u = 0; u < 32; ++u) {
-    const int row = u * 4 + (lane >> 4), c8 = (lane & 15) * 8;
+  for (int u = 0; u < 16; ++u) {
+    const int row = u * 8 + (lane >> 3), c8 = (lane & 7) * 8;
     const int m = mw + row, n = nw + c8;
     if (m >= a.M || n >= a.N) continue;
     const u32x4 val = *reinterpret_cast<const u32x4*>(&ep[row * EPS + c8]);
@@ -637,12 +641,13 @@ void launch_gemm_dma(GemmArgs a, hipStream_t s) {
   a.tiles_m = static_cast<int>(cdiv(a.M, 256));
   a.tiles_n = static_cast<int>(cdiv(a.N, 256));
   const unsigned grid = static_cast<unsigned>(a.tiles_m) * a.tiles_n;
-  k_gemm_dma<ACT, false><<<dim3(grid), dim3(256), 0, s>>>(a);
+  k_gemm_dma<ACT, false><<<dim3(grid), dim3(kDmaThreads), 0, s>>>(a);
 }
 
 // Split-K finish: one thread per partial f4 (4 outputs y[m, n .. n+3]); sums
 // the splits in order (deterministic), then scale, outliers, bias and one
-// rounding, as in the tile kernels' epilogue.
+// rounding, as in the tile kernels' epilogue. Partial index bits, low to
+// high: lane (6), q (2), j (2), i (1), wave (3), tile.
 template <int ACT>
 __global__ __launch_bounds__(kBlock) void k_splitk_reduce(GemmArgs a) {
   const int64_t per_split = static_cast<int64_t>(a.tiles_m) * a.tiles_n * 16384;
@@ -652,12 +657,12 @@ __global__ __launch_bounds__(kBlock) void k_splitk_reduce(GemmArgs a) {
   f4 sum = src[0];
   for (int sp = 1; sp < a.splits; ++sp) sum += src[sp * per_split];
   const int lane = static_cast<int>(idx & 63), q = static_cast<int>((idx >> 6) & 3);
-  const int j = static_cast<int>((idx >> 8) & 3), i = static_cast<int>((idx >> 10) & 3);
-  const int wave = static_cast<int>((idx >> 12) & 3);
+  const int j = static_cast<int>((idx >> 8) & 3), i = static_cast<int>((idx >> 10) & 1);
+  const int wave = static_cast<int>((idx >> 11) & 7);
   const int tile = static_cast<int>(idx >> 14);
   const int tm = tile % a.tiles_m, tn = tile / a.tiles_m;
   const int m = tm * 256 + (wave & 1) * 128 + j * 32 + (lane & 31);
-  const int nb = tn * 256 + (wave >> 1) * 128 + i * 32 + 8 * q + 4 * (lane >> 5);
+  const int nb = tn * 256 + (wave >> 1) * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
   if (m >= a.M || nb >= a.N) return;
   store_quad<ACT>(a, sum, m, nb, (a.N % 4) == 0);
 }
@@ -675,7 +680,7 @@ void launch_gemm_dma_splitk(GemmArgs a, int splits, hipStream_t s) {
   a.split_steps = static_cast<int>(cdiv(nk, splits));
   a.splits = static_cast<int>(cdiv(nk, a.split_steps));   // no empty ranges
   const unsigned grid = static_cast<unsigned>(a.tiles_m) * a.tiles_n * a.splits;
-  k_gemm_dma<ACT, true><<<dim3(grid), dim3(256), 0, s>>>(a);
+  k_gemm_dma<ACT, true><<<dim3(grid), dim3(kDmaThreads), 0, s>>>(a);
   const int64_t n4 = static_cast<int64_t>(a.tiles_m) * a.tiles_n * 16384;
   k_splitk_reduce<ACT><<<dim3(static_cast<unsigned>(cdiv(n4, kBlock))), dim3(kBlock), 0, s>>>(a);
 }
