@@ -354,6 +354,56 @@ __global__ __launch_bounds__(kBlock) void k_col_finalize(
   }
 }
 
+// The same with 4 columns per lane (cols % 4 == 0): 16 lanes x 4 columns per
+// slice, 16 slices striding over the row blocks, so each thread keeps
+// 16-byte loads in flight instead of one 4-byte load per row block.
+// Measured on MI355X (C3 axis 1: 256 row blocks x 8192 columns): 9.6 us for
+// the scalar kernel above.
+constexpr int kFin4Cols = 64;
+__global__ __launch_bounds__(kBlock) void k_col_finalize4(
+    const float* __restrict__ partial, int64_t nrb, int64_t cols, float eps,
+    float* __restrict__ inv_out, float* __restrict__ scale) {
+  constexpr int kLanes = kFin4Cols / 4, kSlices = kBlock / kLanes;
+  __shared__ float4 red[kSlices][kLanes];
+  const int cl = threadIdx.x % kLanes, sl = threadIdx.x / kLanes;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * kFin4Cols + cl * 4;
+  float4 m = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (c < cols) {
+    int64_t b = sl;
+    for (; b + 3 * kSlices < nrb; b += 4 * kSlices) {
+      float4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        v[u] = *reinterpret_cast<const float4*>(partial + (b + u * kSlices) * cols + c);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        m.x = fmaxf(m.x, v[u].x); m.y = fmaxf(m.y, v[u].y);
+        m.z = fmaxf(m.z, v[u].z); m.w = fmaxf(m.w, v[u].w);
+      }
+    }
+    for (; b < nrb; b += kSlices) {
+      const float4 v = *reinterpret_cast<const float4*>(partial + b * cols + c);
+      m.x = fmaxf(m.x, v.x); m.y = fmaxf(m.y, v.y); m.z = fmaxf(m.z, v.z); m.w = fmaxf(m.w, v.w);
+    }
+  }
+  red[sl][cl] = m;
+  __syncthreads();
+  if (sl == 0 && c < cols) {
+#pragma unroll
+    for (int k = 1; k < kSlices; ++k) {
+      const float4 v = red[k][cl];
+      m.x = fmaxf(m.x, v.x); m.y = fmaxf(m.y, v.y); m.z = fmaxf(m.z, v.z); m.w = fmaxf(m.w, v.w);
+    }
+    const float mm[4] = {m.x, m.y, m.z, m.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float inv = inv_scale(mm[k], eps, kQmaxInt8);
+      inv_out[c + k] = inv;
+      scale[c + k] = 1.0f / inv;
+    }
+  }
+}
+
 // inner: adjacent columns sharing one scale (1 for per-column scales; the
 // N-D channel path views [outer, channels, inner] as [outer, channels * inner]).
 template <int DT>
@@ -758,8 +808,12 @@ int cols_quant_t(const void* x, int64_t rows, int64_t cols, int64_t inner, float
   const dim3 grid2(static_cast<unsigned>(g.col_blocks), static_cast<unsigned>(g.nrb));
   k_colmax<DT><<<grid2, dim3(kBlock), 0, s>>>(x, rows, cols, g.RB, vec ? 1 : 0, partial);
   if (inner == 1)
-    k_col_finalize<<<dim3(static_cast<unsigned>(cdiv(cols, kFinCols))), dim3(kBlock), 0, s>>>(
-        partial, g.nrb, cols, eps, inv, scale);
+    if (cols % 4 == 0)
+      k_col_finalize4<<<dim3(static_cast<unsigned>(cdiv(cols, kFin4Cols))), dim3(kBlock), 0, s>>>(
+          partial, g.nrb, cols, eps, inv, scale);
+    else
+      k_col_finalize<<<dim3(static_cast<unsigned>(cdiv(cols, kFinCols))), dim3(kBlock), 0, s>>>(
+          partial, g.nrb, cols, eps, inv, scale);
   else
     k_chan_finalize<<<dim3(static_cast<unsigned>(cols / inner)), dim3(kBlock), 0, s>>>(
         partial, g.nrb, cols, inner, eps, inv, scale);
