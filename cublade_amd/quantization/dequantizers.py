@@ -1,7 +1,8 @@
 """dequantize_tensor (reference: quantization/dequantizers.py:18-75).
 
 Output dtype is ``qt.original_dtype`` (fp16 / bf16 only, as in the
-reference). Channel mode also accepts the last axis (see quantizers).
+reference). Channel mode accepts any axis and group mode any axis, in place
+(see quantizers).
 """
 from __future__ import annotations
 

@@ -1,9 +1,13 @@
 """quantize_tensor / quantize_model (reference: quantization/quantizers.py:22-224).
 
 Same signatures, registry, defaults and exception types as the reference.
-Backed by the HIP C ABI through ``cublade_amd.bindings.hip``. One extension:
-``mode="channel"`` also accepts the LAST axis as ``ch_axis`` (per-column
-scales; the reference raises NotImplementedError for every ch_axis != 0).
+Backed by the HIP C ABI through ``cublade_amd.bindings.hip``. Two extensions:
+``mode="channel"`` accepts any ``ch_axis`` (one scale per position of that
+axis; the reference raises NotImplementedError for every ch_axis != 0), and
+``mode="group"`` along a non-last axis runs in place (the reference moves
+the axis last with two full copies; codes and scale order are the same).
+An out-of-range ``ch_axis`` raises IndexError, as torch's movedim does in the
+reference's group path.
 """
 from __future__ import annotations
 
