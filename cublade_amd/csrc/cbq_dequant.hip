@@ -2,9 +2,9 @@
 // their C-ABI entry points: y = T(float(q) * scale), rounded to nearest even.
 //
 // Kernels (reference kernels they replace, kernels/cuda/quantization/...):
-//   k_deq_tensor     one scale: a full grid, 4 x 8 codes per thread, 8-byte
-//                    loads and 16-byte stores (dequantize_per_tensor_fp8.cu:23-66,
-//                    dequantize_int8.cu:29-64)
+//   k_deq_tensor     one scale: a full grid, 2 or 4 x 8 codes per thread,
+//                    8-byte loads and 16-byte stores
+//                    (dequantize_per_tensor_fp8.cu:23-66, dequantize_int8.cu:29-64)
 //   k_deq_rows_sub   rows of 8..2048 codes (per-group, short per-channel rows)
 //                    owned by power-of-two lane groups; 8-byte loads, 16-byte
 //                    stores (dequantize_int8.cu:118-134, :70-109)
@@ -25,7 +25,6 @@
 namespace cbq {
 namespace {
 
-constexpr int kDU = 4;   // 8-code chunks in flight per thread (per tensor)
 
 template <bool FP8>
 __device__ __forceinline__ void dec4(uint32_t w, float* f) {
@@ -53,28 +52,31 @@ __device__ __forceinline__ void st1(void* y, int64_t i, float v) {
 // ---------------------------------------------------------------------------
 // Per tensor
 // ---------------------------------------------------------------------------
-// Workgroup b covers codes [b * kDeqSpan, (b + 1) * kDeqSpan): each thread
-// loads kDU chunks of 8 codes (8-byte non-temporal loads, all in flight) and
-// writes each as one 16-byte store. A full (non-persistent) grid: measured
-// faster than a grid-stride loop for this write-heavy shape.
-constexpr int kDeqSpan = kBlock * kDU * 8;
-
-template <bool FP8, int OUT>
+// Workgroup b covers codes [b * span, (b + 1) * span), span = kBlock * U * 8:
+// each thread loads U chunks of 8 codes (8-byte non-temporal loads, all in
+// flight) and writes each as one 16-byte store. A full (non-persistent) grid.
+// Measured on MI355X in steady state (launches over distinct 2 GB of
+// buffers, so no input or output stays in the Infinity Cache), 64M codes:
+// U = 2 runs at 33.3 us, as fast as a plain 16-byte copy of the same bytes
+// (33.2 us); U = 4 at 35.4 us, U = 1 or 3 at 34.3-34.7 us, a persistent
+// grid at 33.5-35.4 us. Below 32M codes U = 4 is faster (fewer workgroups
+// to launch).
+template <bool FP8, int OUT, int U>
 __global__ __launch_bounds__(kBlock) void k_deq_tensor(
     const uint8_t* __restrict__ q, const float* __restrict__ scale, int64_t n, int vec,
     void* __restrict__ y) {
   const float s = scale[0];
   if (vec) {
     const int64_t n8 = n >> 3;
-    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * (kBlock * kDU) + threadIdx.x;
-    uint2 r[kDU];
+    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * (kBlock * U) + threadIdx.x;
+    uint2 r[U];
 #pragma unroll
-    for (int u = 0; u < kDU; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
       if (c < n8) r[u] = ldg8(q + c * 8);
     }
 #pragma unroll
-    for (int u = 0; u < kDU; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
       if (c < n8) {
         float f[8];
@@ -309,13 +311,16 @@ unsigned rows_grid(int64_t rows) {
   return static_cast<unsigned>(rows < cap ? rows : cap);
 }
 
+constexpr int64_t kDeqU2Min = 1LL << 25;   // codes from which k_deq_tensor takes U = 2
+
 template <bool FP8, int OUT>
 int deq_tensor_t(const uint8_t* q, const float* scale, int64_t n, void* y, hipStream_t s,
                  const char* what) {
   const bool vec = aligned(q, 8) && aligned(y, 16);
+  const int u = n >= kDeqU2Min ? 2 : 4;
   int64_t grid;
   if (vec) {
-    grid = cdiv(n, kDeqSpan);
+    grid = cdiv(n, static_cast<int64_t>(kBlock) * u * 8);
     if (grid > 0x7fffffffLL / kBlock) {
       set_error("%s: tensor too large (%lld elements)", what, (long long)n);
       return CBQ_EINVAL;
@@ -325,8 +330,9 @@ int deq_tensor_t(const uint8_t* q, const float* scale, int64_t n, void* y, hipSt
     grid = cdiv(n, kBlock) < cap ? cdiv(n, kBlock) : cap;
   }
   if (grid < 1) grid = 1;
-  k_deq_tensor<FP8, OUT><<<dim3(static_cast<unsigned>(grid)), dim3(kBlock), 0, s>>>(
-      q, scale, n, vec ? 1 : 0, y);
+  const dim3 g(static_cast<unsigned>(grid)), b(kBlock);
+  if (u == 2) k_deq_tensor<FP8, OUT, 2><<<g, b, 0, s>>>(q, scale, n, vec ? 1 : 0, y);
+  else k_deq_tensor<FP8, OUT, 4><<<g, b, 0, s>>>(q, scale, n, vec ? 1 : 0, y);
   return launch_status(what);
 }
 

@@ -482,7 +482,8 @@ extern "C" int cbq_mm(const void* A, const void* B, int in_dtype, int b_layout, 
               "%s: dimensions must be multiples of 16 (M=%lld N=%lld K=%lld)", what, (long long)M,
               (long long)N, (long long)K);
   if (M == 0 || N == 0) return CBQ_OK;
-  CBQ_REQUIRE(A && B && C, "%s: null pointer", what);
+  // K == 0 is the empty contraction (C = 0): A and B hold no bytes and may be null.
+  CBQ_REQUIRE(C && (K == 0 || (A && B)), "%s: null pointer", what);
   CBQ_REQUIRE(aligned(A, 16) && aligned(B, 16) && aligned(C, 16),
               "%s: A, B and C must be 16-byte aligned", what);
   mm_plan(M, N, K, in_dtype, b_layout, p);

@@ -1282,9 +1282,19 @@ extern "C" int cbq_w8a16_linear(const void* x, int act_dtype, const int8_t* wq,
   CBQ_REQUIRE(M >= 0 && N >= 0 && K >= 0 && n_out >= 0, "%s: negative size", what);
   CBQ_REQUIRE(n_out <= 0x7fffffffLL, "%s: too many outlier columns", what);
   if (M == 0 || N == 0) return CBQ_OK;
-  CBQ_REQUIRE(x && wq && scales && y, "%s: null pointer", what);
+  // K == 0: the empty contraction, y = bias (or 0); x and wq hold no bytes.
+  CBQ_REQUIRE(scales && y && (K == 0 || (x && wq)), "%s: null pointer", what);
   CBQ_REQUIRE(n_out == 0 || (outlier_cols && w_out), "%s: outlier columns need indices and weights",
               what);
+  if (K == 0) {
+    hipStream_t s = as_stream(stream);
+    return act_dtype == kF32 ? w8a16_simple<kF32>(x, wq, scales, bias, nullptr, 0, nullptr, M, N,
+                                                  K, y, s)
+           : act_dtype == kF16 ? w8a16_simple<kF16>(x, wq, scales, bias, nullptr, 0, nullptr, M,
+                                                    N, K, y, s)
+                               : w8a16_simple<kBF16>(x, wq, scales, bias, nullptr, 0, nullptr, M,
+                                                     N, K, y, s);
+  }
   if (act_dtype == kF32)
     return w8a16_simple<kF32>(x, wq, scales, bias, outlier_cols, n_out, w_out, M, N, K, y,
                               as_stream(stream));

@@ -153,6 +153,19 @@ def test_mm_reference_errors():
         w(a.float(), a.float())
 
 
+@pytest.mark.parametrize("dt,out", [(torch.int8, torch.int32), (torch.uint8, torch.int32),
+                                    (torch.float16, torch.float16), (torch.bfloat16, torch.float32)])
+def test_mm_empty_contraction(dt, out):
+    """K == 0 is a multiple of 16: C = 0 (the reference's zero-filled
+    accumulators are stored); M == 0 gives an empty C."""
+    C = H().wmma_gemm(torch.empty(32, 0, dtype=dt, device=DEV),
+                      torch.empty(0, 48, dtype=dt, device=DEV), out)
+    assert C.dtype == out and tuple(C.shape) == (32, 48) and bool((C == 0).all())
+    C = H().wmma_gemm(torch.empty(0, 16, dtype=dt, device=DEV),
+                      torch.zeros(16, 48, dtype=dt, device=DEV), out)
+    assert tuple(C.shape) == (0, 48)
+
+
 def test_mm_repeated_calls_share_workspace():
     """Back-to-back calls with different staging needs on one workspace."""
     wm = H().wmma_gemm

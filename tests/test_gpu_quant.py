@@ -275,6 +275,15 @@ def test_tensor_sizes(n, code):
     check_int8_tensor(x, code, what=f"int8 n={n}")
 
 
+@pytest.mark.parametrize("n", [(1 << 25) - 8, (1 << 25) + 13])
+def test_tensor_sizes_dequant_chunking(n):
+    """Either side of the size where the per-tensor dequant switches from 4
+    to 2 chunks of 8 codes per thread (2^25 codes), with a ragged tail."""
+    x = rand_bits((n,), oracle.BF16, seed=n, scale=3.0)
+    check_fp8_tensor(x, oracle.BF16, what=f"fp8 n={n}")
+    check_int8_tensor(x, oracle.BF16, what=f"int8 n={n}")
+
+
 @pytest.mark.parametrize("n", [5, 1000, 65537])
 def test_tensor_fp32_int8(n):
     check_int8_tensor(rand_bits((n,), oracle.F32, seed=n, scale=2.0), oracle.F32, what="f32")

@@ -146,6 +146,24 @@ def test_general_path_fp32_and_unaligned():
     run_and_check(40, 256, 72, torch.float16, seed=3, bias=True, x_offset=3)
 
 
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+def test_empty_contraction(dt):
+    """K == 0 (and M == 0 / N == 0): the reference's torch matmul gives
+    zeros, times the scales, plus the bias."""
+    for M, N in [(3, 40), (300, 1100)]:
+        x = torch.empty(M, 0, dtype=dt, device=DEV)
+        wq = torch.empty(N, 0, dtype=torch.int8, device=DEV)
+        s = torch.rand(N, device=DEV).to(dt)
+        b = torch.randn(N, device=DEV).to(dt)
+        y = w8a16(x, wq, s, b)
+        assert y.dtype == dt and tuple(y.shape) == (M, N)
+        assert torch.equal(y, b.expand(M, N))
+        assert bool((w8a16(x, wq, s) == 0).all())
+    assert w8a16(torch.empty(0, 64, dtype=dt, device=DEV),
+                 torch.zeros(8, 64, dtype=torch.int8, device=DEV),
+                 torch.ones(8, dtype=dt, device=DEV)).shape == (0, 8)
+
+
 def test_splitk_workspace_fallback():
     """A control-block-only workspace selects the no-split kernel; same
     results within fp32 accumulation order."""
