@@ -23,6 +23,7 @@ import torch
 HBM_PEAK_BYTES_S = 8.0e12        # MI355X HBM3E
 FP16_MFMA_PEAK_FLOP_S = 2.5e15   # MI355X dense fp16 / bf16 MFMA
 I8_MFMA_PEAK_OP_S = 5.0e15       # MI355X dense int8 MFMA
+FP32_PEAK_FLOP_S = 157.3e12      # MI355X fp32 (published)
 
 
 class MallFlush:

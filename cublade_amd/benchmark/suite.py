@@ -7,9 +7,10 @@ dense fp16 MFMA). Algorithmic bytes per op (N elements, C channels, G
 groups): per-tensor quant 2N read (amax) + 2N read + N written + 4 (cast);
 row / group quant 2N + N + 4C (one pass); column quant 2N + 2N + N + 4F (two
 passes); dequant N + 2N + 4 * scales. W8A16 and the dense GEMM: 2 * M * N * K
-FLOPs (int8 GEMMs against the 5.0 POP/s dense int8 peak).
+FLOPs (int8 GEMMs against the 5.0 POP/s dense int8 peak, the fp32-activation
+W8A16 against the 157.3 TFLOP/s fp32 peak).
 
-    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5,f1,f3,f4 [--json out.json]
+    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5,c5f32,f1,f3,f4 [--json out.json]
 """
 from __future__ import annotations
 
@@ -21,7 +22,8 @@ import sys
 import torch
 
 from . import configs
-from .core import FP16_MFMA_PEAK_FLOP_S, HBM_PEAK_BYTES_S, I8_MFMA_PEAK_OP_S, MallFlush, time_op
+from .core import (FP16_MFMA_PEAK_FLOP_S, FP32_PEAK_FLOP_S, HBM_PEAK_BYTES_S, I8_MFMA_PEAK_OP_S,
+                   MallFlush, time_op)
 
 
 def _rec(cfg, op, us, bytes_=None, flops=None):
@@ -90,6 +92,23 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
             us = time_op(lambda: layer(xd), reps, warmup, flush)
             bytes_ = N * K + 2 * N + 2 * M * K + 2 * M * N
             r = _rec("c5", f"w8a16_m{M}", us, bytes_, 2.0 * M * N * K)
+            out.append(r)
+            print(json.dumps(r), flush=True)
+            del layer, xd
+    if "c5f32" in selected:
+        # The same layer with fp32 activations (an fp32 model under
+        # quantize_model gets fp32 layers, utils.py:46): the general kernel,
+        # fp32 FMA on the VALU, against the 157.3 TFLOP/s fp32 peak.
+        for M in (16, 256, 4096):
+            x, w = configs.c5_w8a16(M)
+            N, K = w.shape
+            layer = cuBladeW8A16LinearLayer(K, N, bias=False, dtype=torch.float32)
+            layer.quantize(w.float().to(dev))
+            xd = x.float().to(dev)
+            us = time_op(lambda: layer(xd), max(3, reps // 4), warmup, flush)
+            r = _rec("c5f32", f"w8a16_f32_m{M}", us, N * K + 4 * N + 4 * M * K + 4 * M * N,
+                     2.0 * M * N * K)
+            r["fp32_frac"] = round(r.pop("mfma_frac") * FP16_MFMA_PEAK_FLOP_S / FP32_PEAK_FLOP_S, 4)
             out.append(r)
             print(json.dumps(r), flush=True)
             del layer, xd
@@ -209,7 +228,7 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,f1,f3,f4")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,c5f32,f1,f3,f4")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--json", default=None)

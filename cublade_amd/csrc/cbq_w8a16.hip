@@ -1107,25 +1107,116 @@ void launch_stream(GemmArgs a, hipStream_t s) {
 }
 
 // Any shape or activation dtype (fp32 activations, K not a multiple of 16,
-// unaligned pointers): one output per thread, fp32 accumulation in k order.
-template <int ACT>
-__global__ __launch_bounds__(kBlock) void k_w8a16_simple(
+// unaligned pointers): k_w8a16_general<ACT, BM>. Output tile BM (m) x 64 (n)
+// per 256-thread workgroup, each thread TM = BM / 16 rows x 4 consecutive n.
+// Per 32-k step the workgroup loads the activation tile (BM x 32, element
+// loads along k, coalesced) and the int8 weight tile (64 x 32) into
+// registers, converts both to fp32 and stores them k-major in LDS; the next
+// step's loads are in flight while the current one is multiplied (two LDS
+// buffers, one barrier per step). fp32 FMA accumulation on the VALU (no
+// MFMA: fp32 operands are the point of this path), then the same epilogue
+// as the MFMA kernels: scale, outlier side-GEMM, bias, one rounding.
+constexpr int kGenBN = 64;
+constexpr int kGenBK = 32;
+constexpr int kGenThreads = 256;
+
+template <int ACT, int BM>
+__global__ __launch_bounds__(kGenThreads) void k_w8a16_general(
     const void* __restrict__ x, const int8_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ bias, const int64_t* __restrict__ oc, int64_t n_out,
-    const void* __restrict__ w_out, void* __restrict__ y, int64_t M, int64_t N, int64_t K) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-  if (idx >= M * N) return;
-  const int64_t m = idx / N, n = idx % N;
-  float acc = 0.0f;
-  for (int64_t k = 0; k < K; ++k) acc += ld1<ACT>(x, m * K + k) * static_cast<float>(wq[n * K + k]);
-  float val = acc * ld1<ACT>(scales, n);
-  for (int64_t jj = 0; jj < n_out; ++jj) {
-    const int64_t k = oc[jj];
-    if (k >= 0 && k < K) val += ld1<ACT>(x, m * K + k) * ld1<ACT>(w_out, n * n_out + jj);
+    const void* __restrict__ w_out, void* __restrict__ y, int64_t M, int64_t N, int64_t K,
+    int64_t tiles_n) {
+  constexpr int TM = BM / 16;
+  constexpr int TN = kGenBN / 16;
+  constexpr int XL = BM * kGenBK / kGenThreads;        // activation elements per thread per step
+  constexpr int WL = kGenBN * kGenBK / kGenThreads;    // weight codes per thread per step
+  // k-major tiles; rows padded by 4 floats (keeps the float4 reads aligned)
+  __shared__ __align__(16) float xs[2][kGenBK][BM + 4];
+  __shared__ __align__(16) float ws[2][kGenBK][kGenBN + 4];
+  const int tid = threadIdx.x;
+  const int tn = tid % 16, tm = tid / 16;
+  const int64_t bid = blockIdx.x;
+  const int64_t m0 = (bid / tiles_n) * BM, n0 = (bid % tiles_n) * kGenBN;
+
+  float xr[XL], wr[WL];
+  auto load = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      const int e = tid + i * kGenThreads, r = e / kGenBK, kk = e % kGenBK;
+      const int64_t m = m0 + r, k = k0 + kk;
+      xr[i] = (m < M && k < K) ? ld1<ACT>(x, m * K + k) : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < WL; ++i) {
+      const int e = tid + i * kGenThreads, r = e / kGenBK, kk = e % kGenBK;
+      const int64_t n = n0 + r, k = k0 + kk;
+      wr[i] = (n < N && k < K) ? static_cast<float>(wq[n * K + k]) : 0.0f;
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      const int e = tid + i * kGenThreads;
+      xs[buf][e % kGenBK][e / kGenBK] = xr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < WL; ++i) {
+      const int e = tid + i * kGenThreads;
+      ws[buf][e % kGenBK][e / kGenBK] = wr[i];
+    }
+  };
+
+  float acc[TM][TN] = {};
+  const int64_t nt = (K + kGenBK - 1) / kGenBK;
+  if (nt > 0) {
+    load(0);
+    store(0);
+    __syncthreads();
   }
-  if (bias) val += ld1<ACT>(bias, n);
-  if constexpr (ACT == kF32) static_cast<float*>(y)[idx] = val;
-  else static_cast<uint16_t*>(y)[idx] = out1<ACT>(val);
+  for (int64_t t = 0; t < nt; ++t) {
+    const int buf = static_cast<int>(t & 1);
+    if (t + 1 < nt) load((t + 1) * kGenBK);
+#pragma unroll 8
+    for (int kk = 0; kk < kGenBK; ++kk) {
+      float xv[TM], wv[TN];
+      if constexpr (TM == 4) {
+        const float4 v = *reinterpret_cast<const float4*>(&xs[buf][kk][tm * 4]);
+        xv[0] = v.x; xv[1] = v.y; xv[2] = v.z; xv[3] = v.w;
+      } else {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) xv[i] = xs[buf][kk][tm * TM + i];
+      }
+      const float4 w4 = *reinterpret_cast<const float4*>(&ws[buf][kk][tn * 4]);
+      wv[0] = w4.x; wv[1] = w4.y; wv[2] = w4.z; wv[3] = w4.w;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_fmaf(xv[i], wv[j], acc[i][j]);
+    }
+    if (t + 1 < nt) store(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int64_t n = n0 + tn * 4 + j;
+    if (n >= N) continue;
+    const float sc = ld1<ACT>(scales, n);
+    const float bv = bias ? ld1<ACT>(bias, n) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int64_t m = m0 + tm * TM + i;
+      if (m >= M) continue;
+      float val = acc[i][j] * sc;
+      for (int64_t jj = 0; jj < n_out; ++jj) {
+        const int64_t k = oc[jj];
+        if (k >= 0 && k < K) val += ld1<ACT>(x, m * K + k) * ld1<ACT>(w_out, n * n_out + jj);
+      }
+      if (bias) val += bv;
+      if constexpr (ACT == kF32) static_cast<float*>(y)[m * N + n] = val;
+      else static_cast<uint16_t*>(y)[m * N + n] = out1<ACT>(val);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1211,16 +1302,23 @@ void launch_kind(Kind k, const GemmArgs& a, hipStream_t s) {
 }
 
 template <int ACT>
-int w8a16_simple(const void* x, const int8_t* wq, const void* scales, const void* bias,
-                 const int64_t* oc, int64_t n_out, const void* w_out, int64_t M, int64_t N,
-                 int64_t K, void* y, hipStream_t s) {
-  const int64_t blocks = cdiv(M * N, kBlock);
-  if (blocks > 0x7fffffffLL / kBlock) {
+int w8a16_general(const void* x, const int8_t* wq, const void* scales, const void* bias,
+                  const int64_t* oc, int64_t n_out, const void* w_out, int64_t M, int64_t N,
+                  int64_t K, void* y, hipStream_t s) {
+  const int bm = M <= 16 ? 16 : 64;
+  const int64_t tiles_n = cdiv(N, static_cast<int64_t>(kGenBN));
+  const int64_t tiles = cdiv(M, static_cast<int64_t>(bm)) * tiles_n;
+  if (tiles > 0x7fffffffLL) {
     set_error("cbq_w8a16_linear: output too large for the general path");
     return CBQ_EINVAL;
   }
-  k_w8a16_simple<ACT><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s>>>(
-      x, wq, scales, bias, oc, n_out, w_out, y, M, N, K);
+  const dim3 g(static_cast<unsigned>(tiles)), b(kGenThreads);
+  if (bm == 16)
+    k_w8a16_general<ACT, 16><<<g, b, 0, s>>>(x, wq, scales, bias, oc, n_out, w_out, y, M, N, K,
+                                             tiles_n);
+  else
+    k_w8a16_general<ACT, 64><<<g, b, 0, s>>>(x, wq, scales, bias, oc, n_out, w_out, y, M, N, K,
+                                             tiles_n);
   return launch_status("cbq_w8a16_linear");
 }
 
@@ -1236,7 +1334,7 @@ int w8a16_t(const void* x, const int8_t* wq, const void* scales, const void* bia
             const int64_t* oc, int64_t n_out, const void* w_out, int64_t M, int64_t N, int64_t K,
             void* ws, size_t ws_bytes, void* y, hipStream_t s) {
   if (!mfma_path(M, N, K, x, wq, y))
-    return w8a16_simple<ACT>(x, wq, scales, bias, oc, n_out, w_out, M, N, K, y, s);
+    return w8a16_general<ACT>(x, wq, scales, bias, oc, n_out, w_out, M, N, K, y, s);
   GemmArgs a{};
   a.x = static_cast<const uint16_t*>(x);
   a.wq = wq;
@@ -1288,15 +1386,15 @@ extern "C" int cbq_w8a16_linear(const void* x, int act_dtype, const int8_t* wq,
               what);
   if (K == 0) {
     hipStream_t s = as_stream(stream);
-    return act_dtype == kF32 ? w8a16_simple<kF32>(x, wq, scales, bias, nullptr, 0, nullptr, M, N,
+    return act_dtype == kF32 ? w8a16_general<kF32>(x, wq, scales, bias, nullptr, 0, nullptr, M, N,
                                                   K, y, s)
-           : act_dtype == kF16 ? w8a16_simple<kF16>(x, wq, scales, bias, nullptr, 0, nullptr, M,
+           : act_dtype == kF16 ? w8a16_general<kF16>(x, wq, scales, bias, nullptr, 0, nullptr, M,
                                                     N, K, y, s)
-                               : w8a16_simple<kBF16>(x, wq, scales, bias, nullptr, 0, nullptr, M,
+                               : w8a16_general<kBF16>(x, wq, scales, bias, nullptr, 0, nullptr, M,
                                                      N, K, y, s);
   }
   if (act_dtype == kF32)
-    return w8a16_simple<kF32>(x, wq, scales, bias, outlier_cols, n_out, w_out, M, N, K, y,
+    return w8a16_general<kF32>(x, wq, scales, bias, outlier_cols, n_out, w_out, M, N, K, y,
                               as_stream(stream));
   // The split-K partials go after the control block; a workspace that is
   // missing, unaligned or too small selects a path without partials.

@@ -146,6 +146,16 @@ def test_general_path_fp32_and_unaligned():
     run_and_check(40, 256, 72, torch.float16, seed=3, bias=True, x_offset=3)
 
 
+@pytest.mark.parametrize("M,K,N", [(16, 4096, 1024), (300, 1000, 700), (65, 4097, 130),
+                                   (1, 33, 1)])
+def test_general_path_fp32_tiles(M, K, N):
+    """fp32 activations at both tile heights (16 and 64 rows), partial tiles
+    in every dimension and K tails that are not a multiple of the 32-k step."""
+    run_and_check(M, K, N, torch.float32, seed=M + K, bias=True, n_out=3 if K > 3 else 0,
+                  rows=list(range(0, M, max(1, M // 7))))
+    run_and_check(M, K, N, torch.bfloat16, seed=M + K + 1, x_offset=1 if K % 2 else 0)
+
+
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
 def test_empty_contraction(dt):
     """K == 0 (and M == 0 / N == 0): the reference's torch matmul gives
