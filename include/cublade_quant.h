@@ -192,7 +192,9 @@ size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_out);
  *               + sum_j x[m, outlier_cols[j]] * w_out[n,j] + bias[n] )
  * with fp32 accumulation and one final round-to-nearest-even to T.
  * x: [M,K] and y: [M,N] in act_dtype, row-major. CBQ_F16 / CBQ_BF16 run
- * on MFMA; CBQ_F32 (the reference's fp32 Triton path) runs a general kernel.
+ * on MFMA; CBQ_F32 (the reference's fp32 Triton path), K % 16 != 0 and
+ * unaligned operands run a tiled fp32-FMA kernel. K == 0 gives y = bias (or
+ * 0); x and wq may then be null.
  * wq: int8 [N,K] row-major; its outlier columns hold 0.
  * scales, bias (nullable): [N] act_dtype. outlier_cols: n_out int64 indices in
  * [0, K) (nullable when n_out == 0); w_out: [N, n_out] act_dtype.
@@ -224,8 +226,9 @@ size_t cbq_mm_ws_bytes(int64_t M, int64_t N, int64_t K, int in_dtype,
  *   CBQ_I8 -> CBQ_I32, CBQ_U8 -> CBQ_I32 (exact modulo 2^32),
  *   CBQ_F16 -> CBQ_F32 or CBQ_F16, CBQ_BF16 -> CBQ_F32
  * (fp32 accumulation; fp16 output rounded once at the end).
- * M, N, K multiples of 16 (the reference's WMMA constraint); A and B 16-byte
- * aligned; ws: cbq_mm_ws_bytes(...) bytes, 256-byte aligned. */
+ * M, N, K multiples of 16 (the reference's WMMA constraint); A, B and C
+ * 16-byte aligned; ws: cbq_mm_ws_bytes(...) bytes, 256-byte aligned.
+ * K == 0 gives C = 0; A and B may then be null. */
 int cbq_mm(const void* A, const void* B, int in_dtype, int b_layout,
            int64_t M, int64_t N, int64_t K, void* C, int out_dtype, void* ws,
            size_t ws_bytes, cbq_stream_t stream);
