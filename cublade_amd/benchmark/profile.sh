@@ -6,7 +6,10 @@
 # 1. kernel trace of bench.py (BASELINE configs[1] step + W8A16 M=4096)
 # 2. FETCH_SIZE and WRITE_SIZE of bench.py (one counter per run), and of a
 #    256 MiB device copy (copy_calib.py) to calibrate both counters
-# 3. kernel trace of the per-config suite (configs 1-5 and the next rows)
+# 3. the per-config suite (configs 1-5, fp32 W8A16 and the next rows): its
+#    HIP-event timings from a run without the profiler (suite.json; the
+#    tracer's per-launch host cost would otherwise show in host-bound ops),
+#    then a kernel trace
 # 4. rocprof's derived MfmaUtil counter (MFMA busy cycles over active cycles
 #    x SIMDs) for the MFMA kernels: W8A16 (config 5) and the dense GEMM (f4)
 # Summaries: OUTDIR/bench_c2_kernels.txt, OUTDIR/dequant_int8_c2_traffic.json,
@@ -39,9 +42,11 @@ timeout -s KILL 60 rocprofv3 --pmc FETCH_SIZE --kernel-trace -d "$RAW/cal_fetch"
 step "counter WRITE_SIZE: 256 MiB copy"
 timeout -s KILL 60 rocprofv3 --pmc WRITE_SIZE --kernel-trace -d "$RAW/cal_write" -o calib -- \
   $PY -m cublade_amd.benchmark.copy_calib > "$RAW/cal_write.log" 2>&1 || exit $?
+step "suite (HIP-event timing, no profiler attached)"
+timeout -k 10 500 $PY -m cublade_amd.benchmark.suite --json "$OUT/suite.json" > "$RAW/suite_plain.log" 2>&1 || exit $?
 step "kernel trace: suite"
 timeout -k 10 500 rocprofv3 --kernel-trace --stats -d "$RAW/suite" -o suite -- \
-  $PY -m cublade_amd.benchmark.suite --reps 10 --json "$OUT/suite.json" > "$RAW/suite.log" 2>&1 || exit $?
+  $PY -m cublade_amd.benchmark.suite --reps 10 > "$RAW/suite.log" 2>&1 || exit $?
 
 step "counter MfmaUtil: suite configs c5,f4"
 timeout -s KILL 300 rocprofv3 --pmc MfmaUtil --kernel-trace -d "$RAW/mfma" -o suite -- \
@@ -57,7 +62,7 @@ step "summaries"
   echo "# bench.py output line under the profiler:"
   grep '"metric"' "$RAW/trace.log"
 } > "$OUT/bench_c2_kernels.txt" || exit $?
-$R traffic "k_deq_tensor<false, 1>" "$RAW/fetch/bench_results.db" "$RAW/write/bench_results.db" \
+$R traffic "k_deq_tensor<false, 1, 2>" "$RAW/fetch/bench_results.db" "$RAW/write/bench_results.db" \
   "$RAW/cal_fetch/calib_results.db" "$RAW/cal_write/calib_results.db" 262144 \
   | python -c 'import json,sys; d=json.load(sys.stdin); d["command"]="bash cublade_amd/benchmark/profile.sh OUTDIR: rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --kernel-trace -- python -u bench.py --no-cpu --no-w8a16 --steps 3 --warmup 1; calibration: the same counters over python -m cublade_amd.benchmark.copy_calib (256 MiB copy = 262144 KiB)"; d["algorithmic_bytes_per_launch"]=201326596; d["traffic_over_algorithmic"]=round(d["hbm_bytes_per_launch"]/201326596,4); print(json.dumps(d, indent=1))' \
   > "$OUT/dequant_int8_c2_traffic.json" || exit $?

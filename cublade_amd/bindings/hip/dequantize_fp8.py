@@ -33,7 +33,7 @@ def dequantize_per_tensor_fp8(
     if n == 0:
         return y
     L = _abi.lib()
-    with torch.cuda.device(q.device):
+    with _abi.on_device(q.device):
         rc = L.cbq_dequant_fp8_tensor(_abi.ptr(q), _abi.ptr(scale), n, _abi.ptr(y), out,
                                       _abi.stream_handle(q.device))
     _abi.check(rc, "dequantize_per_tensor_fp8")

@@ -30,7 +30,7 @@ def dequantize_per_tensor_int8(
     if n == 0:
         return y
     L = _abi.lib()
-    with torch.cuda.device(q.device):
+    with _abi.on_device(q.device):
         rc = L.cbq_dequant_int8_tensor(_abi.ptr(q), _abi.ptr(scale), n, _abi.ptr(y), out,
                                        _abi.stream_handle(q.device))
     _abi.check(rc, "dequantize_per_tensor_int8")
@@ -62,7 +62,7 @@ def dequantize_per_channel_int8(
     if C == 0 or F == 0:
         return y
     L = _abi.lib()
-    with torch.cuda.device(q.device):
+    with _abi.on_device(q.device):
         rc = L.cbq_dequant_int8_channel(_abi.ptr(q), _abi.ptr(scale), C, F, axis, _abi.ptr(y),
                                         out, _abi.stream_handle(q.device))
     _abi.check(rc, "dequantize_per_channel_int8")
@@ -93,7 +93,7 @@ def dequantize_per_group_int8(
     if G == 0:
         return y
     L = _abi.lib()
-    with torch.cuda.device(q_grouped.device):
+    with _abi.on_device(q_grouped.device):
         rc = L.cbq_dequant_int8_group(_abi.ptr(q_grouped), _abi.ptr(scale), G, int(group_size),
                                       _abi.ptr(y), out, _abi.stream_handle(q_grouped.device))
     _abi.check(rc, "dequantize_per_group_int8")
@@ -124,7 +124,7 @@ def dequantize_per_channel_int8_nd(
     if q.numel() == 0:
         return y
     L = _abi.lib()
-    with torch.cuda.device(q.device):
+    with _abi.on_device(q.device):
         rc = L.cbq_dequant_int8_channel_nd(_abi.ptr(q), _abi.ptr(scale), outer, C, inner,
                                            _abi.ptr(y), out, _abi.stream_handle(q.device))
     _abi.check(rc, "dequantize_per_channel_int8_nd")
@@ -159,7 +159,7 @@ def dequantize_per_group_int8_nd(
     if ng == 0:
         return y
     L = _abi.lib()
-    with torch.cuda.device(q.device):
+    with _abi.on_device(q.device):
         rc = L.cbq_dequant_int8_group_nd(_abi.ptr(q), _abi.ptr(scale), outer, Lq, inner,
                                          group_size, _abi.ptr(y), out,
                                          _abi.stream_handle(q.device))

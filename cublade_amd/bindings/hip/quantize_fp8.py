@@ -36,7 +36,7 @@ def quantize_per_tensor_fp8(
         return q, torch.zeros((), dtype=torch.float32, device=dev)
     scale = torch.empty((), dtype=torch.float32, device=dev)
     L = _abi.lib()
-    with torch.cuda.device(dev):
+    with _abi.on_device(dev):
         ws = _abi.workspace(dev, L.cbq_quant_tensor_ws_bytes())
         rc = L.cbq_quant_fp8_tensor(_abi.ptr(x), code, n, float(eps), _abi.ptr(ws), ws.numel(),
                                     _abi.ptr(q), _abi.ptr(scale), _abi.stream_handle(dev))

@@ -33,7 +33,7 @@ def quantize_per_tensor_int8(
         return q, torch.zeros((), dtype=torch.float32, device=dev)
     scale = torch.empty((), dtype=torch.float32, device=dev)
     L = _abi.lib()
-    with torch.cuda.device(dev):
+    with _abi.on_device(dev):
         ws = _abi.workspace(dev, L.cbq_quant_tensor_ws_bytes())
         rc = L.cbq_quant_int8_tensor(_abi.ptr(x), code, n, float(eps), _abi.ptr(ws), ws.numel(),
                                      _abi.ptr(q), _abi.ptr(scale), _abi.stream_handle(dev))
@@ -70,7 +70,7 @@ def quantize_per_channel_int8(
         return q, torch.zeros((nscale,), dtype=torch.float32, device=dev)
     scale = torch.empty((nscale,), dtype=torch.float32, device=dev)
     L = _abi.lib()
-    with torch.cuda.device(dev):
+    with _abi.on_device(dev):
         ws = _abi.workspace(dev, L.cbq_quant_int8_channel_ws_bytes(C, F, axis))
         rc = L.cbq_quant_int8_channel(_abi.ptr(x), code, C, F, axis, float(eps), _abi.ptr(ws),
                                       ws.numel(), _abi.ptr(q), _abi.ptr(scale),
@@ -101,7 +101,7 @@ def quantize_per_group_int8(
         return q, torch.zeros((0,), dtype=torch.float32, device=dev)
     scale = torch.empty((G,), dtype=torch.float32, device=dev)
     L = _abi.lib()
-    with torch.cuda.device(dev):
+    with _abi.on_device(dev):
         rc = L.cbq_quant_int8_group(_abi.ptr(x_grouped), code, G, int(group_size), float(eps),
                                     _abi.ptr(q), _abi.ptr(scale), _abi.stream_handle(dev))
     _abi.check(rc, "quantize_per_group_int8")
@@ -142,7 +142,7 @@ def quantize_per_channel_int8_nd(
         return q, torch.zeros((C,), dtype=torch.float32, device=dev)
     scale = torch.empty((C,), dtype=torch.float32, device=dev)
     L = _abi.lib()
-    with torch.cuda.device(dev):
+    with _abi.on_device(dev):
         ws = _abi.workspace(dev, L.cbq_quant_int8_channel_nd_ws_bytes(outer, C, inner))
         rc = L.cbq_quant_int8_channel_nd(_abi.ptr(x), code, outer, C, inner, float(eps),
                                          _abi.ptr(ws), ws.numel(), _abi.ptr(q), _abi.ptr(scale),
@@ -178,7 +178,7 @@ def quantize_per_group_int8_nd(
     if ng == 0:
         return q, scale
     L = _abi.lib()
-    with torch.cuda.device(dev):
+    with _abi.on_device(dev):
         rc = L.cbq_quant_int8_group_nd(_abi.ptr(x), code, outer, Lx, inner, group_size,
                                        float(eps), _abi.ptr(q), _abi.ptr(scale),
                                        _abi.stream_handle(dev))

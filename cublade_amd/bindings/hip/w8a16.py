@@ -70,7 +70,7 @@ def w8a16_linear(
     if M == 0 or N == 0:
         return y
     L = _abi.lib()
-    with torch.cuda.device(dev):
+    with _abi.on_device(dev):
         ws = _abi.workspace(dev, L.cbq_w8a16_ws_bytes(M, N, K, n_out))
         rc = L.cbq_w8a16_linear(_abi.ptr(x2d), _abi.DTYPE_CODE[dt], _abi.ptr(wq), _abi.ptr(s),
                                 _abi.ptr(b), _abi.ptr(oc), n_out, _abi.ptr(wo), M, N, K,

@@ -65,7 +65,7 @@ def mm(A: torch.Tensor, B: torch.Tensor, out_dtype: torch.dtype | None = None) -
         return C
     L = _abi.lib()
     code = _abi.MM_DTYPE_CODE[A.dtype]
-    with torch.cuda.device(A.device):
+    with _abi.on_device(A.device):
         ws = _abi.workspace(A.device, L.cbq_mm_ws_bytes(M, N, K, code, layout))
         _abi.check(L.cbq_mm(_abi.ptr(A), _abi.ptr(Bt), code, layout, M, N, K, _abi.ptr(C),
                             _abi.MM_DTYPE_CODE[out], _abi.ptr(ws), ws.numel(),

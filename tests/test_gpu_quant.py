@@ -368,6 +368,19 @@ def test_side_stream():
     assert_bits_equal_16(bits(y), oracle.dequant_fp8_tensor(qo, so, code), code, "stream y")
 
 
+def test_stream_handle_is_torchs_current_stream():
+    """The launch stream the bindings pass is torch's current stream, on the
+    default stream and inside a side stream."""
+    from cublade_amd import _abi
+    dev = torch.device(DEV, torch.cuda.current_device())
+    assert _abi.stream_handle(dev) == torch.cuda.current_stream(dev).cuda_stream
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        assert _abi.stream_handle(dev) == s.cuda_stream
+        assert _abi.stream_handle(torch.device(DEV)) == s.cuda_stream
+    assert _abi.stream_handle(dev) == torch.cuda.current_stream(dev).cuda_stream
+
+
 # ---------------------------------------------------------------------------
 # public API
 # ---------------------------------------------------------------------------
