@@ -1228,7 +1228,7 @@ __global__ __launch_bounds__(kGenThreads) void k_w8a16_general(
 //                 workgroups; else k_skinny (TM = 1)
 //   M <= 64       k_stream<2 or 4> under the same size rules (3 row tiles
 //                 per workgroup); else k_skinny, TM = ceil(M / 16)
-//   64 < M < 1024 k_gemm_dma split over K (2-4 k-ranges, partial tiles in
+//   64 < M < 1024 k_gemm_dma split over K (2-16 k-ranges, partial tiles in
 //                 the workspace, k_splitk_reduce) when the 256 x 256 tiles
 //                 alone would leave at least half of the CUs idle and the
 //                 caller's workspace holds the partials; else k_gemm_dma
@@ -1251,13 +1251,29 @@ bool dma_ok(int64_t M, int64_t N, int64_t K) {
   return K % 64 == 0 && M * K * 2 < kLim && N * K < kLim;
 }
 
-// k-ranges for the split-K tile path (0: not used). More ranges than 4 cost
-// more in partial traffic than they gain in occupancy.
+// k-ranges for the split-K tile path (0: not used). The workgroups
+// (tiles x ranges) must fit one wave of CUs, and each range keeps at least
+// four 64-k steps. Among those counts, the one with the lowest modelled
+// time: 1.28 us per 64-k step of the longest range plus 0.09 us per
+// 256 KiB partial tile written and re-read (fitted on MI355X at M = 128..768,
+// N = 4096 / 11008, K = 4096 / 11008; e.g. 16 tiles at K = 11008: 4 ranges
+// 65.7 us, 8: 44.3, 12: 40.8, 16: 41.2; 43 tiles at K = 4096: 4 ranges
+// 42.1 us, 6 (more workgroups than CUs): 57.1).
 int splitk_count(int64_t M, int64_t N, int64_t K) {
   if (M <= 64 || M >= 1024 || !dma_ok(M, N, K)) return 0;
   const int64_t tiles = cdiv(M, 256) * cdiv(N, 256);
-  const int64_t sp = std::min<int64_t>({4, device_cus() / tiles, K / 64 / 4});
-  return sp >= 2 ? static_cast<int>(sp) : 0;
+  const int64_t nk = K / 64;
+  const int64_t max_sp = std::min<int64_t>({16, device_cus() / tiles, nk / 4});
+  int best = 0;
+  int64_t best_cost = 0;
+  for (int64_t sp = 2; sp <= max_sp; ++sp) {
+    const int64_t cost = 128 * cdiv(nk, sp) + 9 * tiles * sp;
+    if (best == 0 || cost < best_cost) {
+      best = static_cast<int>(sp);
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
 Kind choose(int64_t M, int64_t N, int64_t K, size_t ws_bytes) {

@@ -177,9 +177,10 @@ int cbq_dequant_int8_group_nd(const int8_t* q, const float* scale,
 /* ---- W8A16 linear ------------------------------------------------------- */
 
 /* Workspace bytes for cbq_w8a16_linear at this shape: the control block,
- * plus, for 64 < M < 1024, fp32 partial tiles of a split-K launch (up to
- * 4 x ceil(M/256) x ceil(N/256) x 256 KiB). The reference allocates its
- * temporaries inside the forward (linear.py:105-131). */
+ * plus, for 64 < M < 1024, fp32 partial tiles of a split-K launch
+ * (ranges x ceil(M/256) x ceil(N/256) x 256 KiB with at most 16 ranges and
+ * at most one partial tile per CU, i.e. <= 64 MiB on MI355X). The reference
+ * allocates its temporaries inside the forward (linear.py:105-131). */
 size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_out);
 
 /* Replaces the forward chain of cuBladeW8A16LinearLayer

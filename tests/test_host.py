@@ -94,6 +94,9 @@ def test_workspace_sizes():
     assert L.cbq_w8a16_ws_bytes(256, 11008, 4096, 0) == C + 4 * 43 * 256 * 1024
     assert L.cbq_w8a16_ws_bytes(512, 11008, 4096, 3) == C + 2 * 86 * 256 * 1024
     assert L.cbq_w8a16_ws_bytes(256, 11008, 4000, 0) == C      # K % 64 != 0
+    # few tiles (the MLP down projection): 11 k-ranges x 16 tiles, <= 256 workgroups
+    assert L.cbq_w8a16_ws_bytes(256, 4096, 11008, 0) == C + 11 * 16 * 256 * 1024
+    assert L.cbq_w8a16_ws_bytes(768, 4096, 11008, 0) == C + 5 * 48 * 256 * 1024
 
 
 def test_nd_entry_points_validate_and_size():
