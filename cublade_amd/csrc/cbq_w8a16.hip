@@ -1228,12 +1228,13 @@ __global__ __launch_bounds__(kGenThreads) void k_w8a16_general(
 //                 workgroups; else k_skinny (TM = 1)
 //   M <= 64       k_stream<2 or 4> under the same size rules (3 row tiles
 //                 per workgroup); else k_skinny, TM = ceil(M / 16)
-//   64 < M < 1024 k_gemm_dma split over K (2-16 k-ranges, partial tiles in
+//   M > 64        k_gemm_dma split over K (2-16 k-ranges, partial tiles in
 //                 the workspace, k_splitk_reduce) when the 256 x 256 tiles
-//                 alone would leave at least half of the CUs idle and the
-//                 caller's workspace holds the partials; else k_gemm_dma
-//                 from M = 384 on; else k_gemm 128 x 64 x 64, 2 x 2 waves
-//   M >= 1024     k_gemm_dma (K % 64 == 0 and 32-bit operand offsets),
+//                 alone leave CUs idle and the time model of splitk_count
+//                 prefers it, and the caller's workspace holds the partials;
+//   64 < M < 1024 else k_gemm_dma from M = 384 on; else k_gemm 128 x 64 x 64,
+//                 2 x 2 waves
+//   M >= 1024     else k_gemm_dma (K % 64 == 0 and 32-bit operand offsets),
 //                 else k_gemm 256 x 256 x 64, 4 x 2 waves
 enum Kind { kSkinny1, kSkinny2, kSkinny4, kTileMid, kTileLarge, kTileDma, kStream1, kStream2,
             kStream4, kTileDmaSplit };
@@ -1253,27 +1254,29 @@ bool dma_ok(int64_t M, int64_t N, int64_t K) {
 
 // k-ranges for the split-K tile path (0: not used). The workgroups
 // (tiles x ranges) must fit one wave of CUs, and each range keeps at least
-// four 64-k steps. Among those counts, the one with the lowest modelled
-// time: 1.28 us per 64-k step of the longest range plus 0.09 us per
-// 256 KiB partial tile written and re-read (fitted on MI355X at M = 128..768,
+// four 64-k steps. The count with the lowest modelled time wins, one range
+// (the plain tile kernel) included: 1.28 us per 64-k step of the longest
+// range, plus, when split, 0.09 us per 256 KiB partial tile written and
+// re-read and 5 us for the reduce pass (fitted on MI355X at M = 128..768,
 // N = 4096 / 11008, K = 4096 / 11008; e.g. 16 tiles at K = 11008: 4 ranges
 // 65.7 us, 8: 44.3, 12: 40.8, 16: 41.2; 43 tiles at K = 4096: 4 ranges
-// 42.1 us, 6 (more workgroups than CUs): 57.1).
+// 42.1 us, 6 (more workgroups than CUs): 57.1). Large M splits only while
+// the tiles alone leave CUs idle (e.g. M = 1024, N = 4096: 64 tiles).
 int splitk_count(int64_t M, int64_t N, int64_t K) {
-  if (M <= 64 || M >= 1024 || !dma_ok(M, N, K)) return 0;
+  if (M <= 64 || !dma_ok(M, N, K)) return 0;
   const int64_t tiles = cdiv(M, 256) * cdiv(N, 256);
   const int64_t nk = K / 64;
   const int64_t max_sp = std::min<int64_t>({16, device_cus() / tiles, nk / 4});
-  int best = 0;
-  int64_t best_cost = 0;
+  int best = 1;
+  int64_t best_cost = 128 * nk;
   for (int64_t sp = 2; sp <= max_sp; ++sp) {
-    const int64_t cost = 128 * cdiv(nk, sp) + 9 * tiles * sp;
-    if (best == 0 || cost < best_cost) {
+    const int64_t cost = 128 * cdiv(nk, sp) + 9 * tiles * sp + 500;
+    if (cost < best_cost) {
       best = static_cast<int>(sp);
       best_cost = cost;
     }
   }
-  return best;
+  return best >= 2 ? best : 0;
 }
 
 Kind choose(int64_t M, int64_t N, int64_t K, size_t ws_bytes) {
@@ -1284,12 +1287,10 @@ Kind choose(int64_t M, int64_t N, int64_t K, size_t ws_bytes) {
   const bool tiles_fit = cdiv(N, 16) <= kStreamMaxTiles * cus;
   if (M <= 32) return (stream && tiles_fit) ? kStream2 : kSkinny2;
   if (M <= 64) return (stream && tiles_fit) ? kStream4 : kSkinny4;
-  if (M < 1024) {
-    const int sp = splitk_count(M, N, K);
-    if (sp && ws_bytes >= static_cast<size_t>(CBQ_WS_CTRL_BYTES + splitk_bytes(M, N, sp)))
-      return kTileDmaSplit;
-    return (M >= 384 && dma_ok(M, N, K)) ? kTileDma : kTileMid;
-  }
+  const int sp = splitk_count(M, N, K);
+  if (sp && ws_bytes >= static_cast<size_t>(CBQ_WS_CTRL_BYTES + splitk_bytes(M, N, sp)))
+    return kTileDmaSplit;
+  if (M < 1024) return (M >= 384 && dma_ok(M, N, K)) ? kTileDma : kTileMid;
   return dma_ok(M, N, K) ? kTileDma : kTileLarge;
 }
 

@@ -177,7 +177,8 @@ int cbq_dequant_int8_group_nd(const int8_t* q, const float* scale,
 /* ---- W8A16 linear ------------------------------------------------------- */
 
 /* Workspace bytes for cbq_w8a16_linear at this shape: the control block,
- * plus, for 64 < M < 1024, fp32 partial tiles of a split-K launch
+ * plus, for M > 64 with fewer 256 x 256 output tiles than CUs, fp32 partial
+ * tiles of a split-K launch
  * (ranges x ceil(M/256) x ceil(N/256) x 256 KiB with at most 16 ranges and
  * at most one partial tile per CU, i.e. <= 64 MiB on MI355X). The reference
  * allocates its temporaries inside the forward (linear.py:105-131). */
@@ -201,7 +202,7 @@ size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_out);
  * [0, K) (nullable when n_out == 0); w_out: [N, n_out] act_dtype.
  * ws: cbq_w8a16_ws_bytes(...) bytes, 256-byte aligned, control block zeroed;
  * a smaller or missing workspace selects a kernel without split-K (same
- * results within fp32 accumulation order, slower for 64 < M < 1024). */
+ * results within fp32 accumulation order, slower at those shapes). */
 int cbq_w8a16_linear(const void* x, int act_dtype, const int8_t* wq,
                      const void* scales, const void* bias,
                      const int64_t* outlier_cols, int64_t n_out,

@@ -195,6 +195,28 @@ def test_splitk_workspace_fallback():
     np.testing.assert_allclose(y_split.float().cpu().numpy()[[0, 99, 255]], ref, **TOL)
 
 
+@pytest.mark.parametrize("M,K,N", [(1024, 2048, 1100), (1500, 1024, 700)])
+def test_splitk_large_m_few_tiles(M, K, N):
+    """M >= 1024 with fewer tiles than CUs takes the split-K path; rows
+    against the oracle and the no-split kernel (control-block workspace)."""
+    from cublade_amd import _abi
+    L = _abi.lib()
+    assert L.cbq_w8a16_ws_bytes(M, N, K, 0) > _abi.WS_CTRL_BYTES
+    x, wq, s, b, _, _ = make_case(M, K, N, torch.bfloat16, M + N, bias=True)
+    xd, wd, sd, bd = x.to(DEV), wq.to(DEV), s.to(DEV), b.to(DEV)
+    y_split = w8a16(xd, wd, sd, bd)
+    rows = np.array([0, 257, M // 2, M - 1])
+    ref = oracle_y(bits(x), oracle.BF16, wq.numpy(), bits(s), bits(b), rows=rows)
+    np.testing.assert_allclose(y_split.float().cpu().numpy()[rows], ref, **TOL)
+    y_one = torch.empty_like(y_split)
+    ws = torch.zeros(_abi.WS_CTRL_BYTES, dtype=torch.uint8, device=DEV)
+    rc = L.cbq_w8a16_linear(_abi.ptr(xd), CODE_OF[torch.bfloat16], _abi.ptr(wd), _abi.ptr(sd),
+                            _abi.ptr(bd), None, 0, None, M, N, K, _abi.ptr(ws), ws.numel(),
+                            _abi.ptr(y_one), _abi.stream_handle(xd.device))
+    assert rc == 0
+    torch.testing.assert_close(y_split.float(), y_one.float(), **TOL)
+
+
 def test_mfma_bit_stability_across_calls():
     """Same inputs, same outputs, bit for bit (fixed accumulation order)."""
     x, wq, s, b, _, _ = make_case(256, 1024, 512, torch.float16, 8, bias=True)
