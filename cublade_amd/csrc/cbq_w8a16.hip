@@ -1107,85 +1107,117 @@ void launch_stream(GemmArgs a, hipStream_t s) {
 }
 
 // Any shape or activation dtype (fp32 activations, K not a multiple of 16,
-// unaligned pointers): k_w8a16_general<ACT, BM>. Output tile BM (m) x 64 (n)
-// per 256-thread workgroup, each thread TM = BM / 16 rows x 4 consecutive n.
-// Per 32-k step the workgroup loads the activation tile (BM x 32, element
-// loads along k, coalesced) and the int8 weight tile (64 x 32) into
-// registers, converts both to fp32 and stores them k-major in LDS; the next
-// step's loads are in flight while the current one is multiplied (two LDS
-// buffers, one barrier per step). fp32 FMA accumulation on the VALU (no
-// MFMA: fp32 operands are the point of this path), then the same epilogue
-// as the MFMA kernels: scale, outlier side-GEMM, bias, one rounding.
-constexpr int kGenBN = 64;
+// unaligned pointers): k_w8a16_general<ACT, BM, BN, SPLIT>. Output tile
+// BM (m) x BN (n) per 256-thread workgroup, 64 x 64 or, for M <= 16,
+// 16 x 256; each thread owns 4 rows x 4 consecutive n. Per 32-k step the
+// workgroup loads the activation tile (BM x 32, element loads along k,
+// coalesced) and the int8 weight tile (BN x 32) into registers, converts
+// both to fp32 and stores them k-major in LDS; the next step's loads are in
+// flight while the current one is multiplied (two LDS buffers, one barrier
+// per step). fp32 FMA accumulation on the VALU (no MFMA: fp32 operands are
+// the point of this path), then the same epilogue as the MFMA kernels:
+// scale, outlier side-GEMM, bias, one rounding. When the tiles alone leave
+// the GPU under-occupied (small M) the host splits K into `splits` ranges:
+// workgroup (split, tile) writes its fp32 sums to the workspace and
+// k_general_reduce adds the ranges in order (deterministic) before the
+// epilogue.
 constexpr int kGenBK = 32;
 constexpr int kGenThreads = 256;
 
-template <int ACT, int BM>
-__global__ __launch_bounds__(kGenThreads) void k_w8a16_general(
-    const void* __restrict__ x, const int8_t* __restrict__ wq, const void* __restrict__ scales,
-    const void* __restrict__ bias, const int64_t* __restrict__ oc, int64_t n_out,
-    const void* __restrict__ w_out, void* __restrict__ y, int64_t M, int64_t N, int64_t K,
-    int64_t tiles_n) {
-  constexpr int TM = BM / 16;
-  constexpr int TN = kGenBN / 16;
-  constexpr int XL = BM * kGenBK / kGenThreads;        // activation elements per thread per step
-  constexpr int WL = kGenBN * kGenBK / kGenThreads;    // weight codes per thread per step
+struct GenArgs {
+  const void* x;           // [M, K] act
+  const int8_t* wq;        // [N, K]
+  const void* scales;      // [N] act
+  const void* bias;        // [N] act or null
+  const int64_t* oc;       // [n_out]
+  const void* w_out;       // [N, n_out] act
+  void* y;                 // [M, N] act
+  float* part;             // [splits, M, N] fp32 (split mode)
+  int64_t n_out, M, N, K;
+  int64_t tiles_n, tiles;  // output tiles along n, in total
+  int64_t kper;            // k per split (a multiple of kGenBK, hence of every k step)
+  int splits;
+};
+
+// Epilogue of one output: scale, outlier side-GEMM, bias, one rounding.
+template <int ACT>
+__device__ __forceinline__ void general_out(const GenArgs& a, int64_t m, int64_t n, float acc) {
+  float val = acc * ld1<ACT>(a.scales, n);
+  for (int64_t jj = 0; jj < a.n_out; ++jj) {
+    const int64_t k = a.oc[jj];
+    if (k >= 0 && k < a.K)
+      val += ld1<ACT>(a.x, m * a.K + k) * ld1<ACT>(a.w_out, n * a.n_out + jj);
+  }
+  if (a.bias) val += ld1<ACT>(a.bias, n);
+  if constexpr (ACT == kF32) static_cast<float*>(a.y)[m * a.N + n] = val;
+  else static_cast<uint16_t*>(a.y)[m * a.N + n] = out1<ACT>(val);
+}
+
+template <int ACT, int BM, int BN, bool SPLIT>
+__global__ __launch_bounds__(kGenThreads) void k_w8a16_general(GenArgs a) {
+  constexpr int TM = 4, TN = 4;
+  // 32-k steps; 16 for the 256-wide tile (32 weight codes per thread per
+  // step would cost more address registers than the loads are worth)
+  constexpr int BK = BN > 64 ? 16 : kGenBK;
+  static_assert((BM / TM) * (BN / TN) == kGenThreads, "one 4 x 4 output block per thread");
+  constexpr int XL = BM * BK / kGenThreads;        // activation elements per thread per step
+  constexpr int WL = BN * BK / kGenThreads;        // weight codes per thread per step
   // k-major tiles; rows padded by 4 floats (keeps the float4 reads aligned)
-  __shared__ __align__(16) float xs[2][kGenBK][BM + 4];
-  __shared__ __align__(16) float ws[2][kGenBK][kGenBN + 4];
+  __shared__ __align__(16) float xs[2][BK][BM + 4];
+  __shared__ __align__(16) float ws[2][BK][BN + 4];
   const int tid = threadIdx.x;
-  const int tn = tid % 16, tm = tid / 16;
+  const int tn = tid % (BN / TN), tm = tid / (BN / TN);
   const int64_t bid = blockIdx.x;
-  const int64_t m0 = (bid / tiles_n) * BM, n0 = (bid % tiles_n) * kGenBN;
+  const int64_t split = SPLIT ? bid / a.tiles : 0;
+  const int64_t tile = SPLIT ? bid % a.tiles : bid;
+  const int64_t m0 = (tile / a.tiles_n) * BM, n0 = (tile % a.tiles_n) * BN;
+  const int64_t kb = SPLIT ? split * a.kper : 0;
+  const int64_t ke = SPLIT ? min(a.K, kb + a.kper) : a.K;
+  const int64_t M = a.M, N = a.N, K = a.K;
 
   float xr[XL], wr[WL];
   auto load = [&](int64_t k0) {
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
-      const int e = tid + i * kGenThreads, r = e / kGenBK, kk = e % kGenBK;
+      const int e = tid + i * kGenThreads, r = e / BK, kk = e % BK;
       const int64_t m = m0 + r, k = k0 + kk;
-      xr[i] = (m < M && k < K) ? ld1<ACT>(x, m * K + k) : 0.0f;
+      xr[i] = (m < M && k < ke) ? ld1<ACT>(a.x, m * K + k) : 0.0f;
     }
 #pragma unroll
     for (int i = 0; i < WL; ++i) {
-      const int e = tid + i * kGenThreads, r = e / kGenBK, kk = e % kGenBK;
+      const int e = tid + i * kGenThreads, r = e / BK, kk = e % BK;
       const int64_t n = n0 + r, k = k0 + kk;
-      wr[i] = (n < N && k < K) ? static_cast<float>(wq[n * K + k]) : 0.0f;
+      wr[i] = (n < N && k < ke) ? static_cast<float>(a.wq[n * K + k]) : 0.0f;
     }
   };
   auto store = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
       const int e = tid + i * kGenThreads;
-      xs[buf][e % kGenBK][e / kGenBK] = xr[i];
+      xs[buf][e % BK][e / BK] = xr[i];
     }
 #pragma unroll
     for (int i = 0; i < WL; ++i) {
       const int e = tid + i * kGenThreads;
-      ws[buf][e % kGenBK][e / kGenBK] = wr[i];
+      ws[buf][e % BK][e / BK] = wr[i];
     }
   };
 
   float acc[TM][TN] = {};
-  const int64_t nt = (K + kGenBK - 1) / kGenBK;
+  const int64_t nt = ke > kb ? (ke - kb + BK - 1) / BK : 0;
   if (nt > 0) {
-    load(0);
+    load(kb);
     store(0);
     __syncthreads();
   }
   for (int64_t t = 0; t < nt; ++t) {
     const int buf = static_cast<int>(t & 1);
-    if (t + 1 < nt) load((t + 1) * kGenBK);
+    if (t + 1 < nt) load(kb + (t + 1) * BK);
 #pragma unroll 8
-    for (int kk = 0; kk < kGenBK; ++kk) {
+    for (int kk = 0; kk < BK; ++kk) {
       float xv[TM], wv[TN];
-      if constexpr (TM == 4) {
-        const float4 v = *reinterpret_cast<const float4*>(&xs[buf][kk][tm * 4]);
-        xv[0] = v.x; xv[1] = v.y; xv[2] = v.z; xv[3] = v.w;
-      } else {
-#pragma unroll
-        for (int i = 0; i < TM; ++i) xv[i] = xs[buf][kk][tm * TM + i];
-      }
+      const float4 v = *reinterpret_cast<const float4*>(&xs[buf][kk][tm * 4]);
+      xv[0] = v.x; xv[1] = v.y; xv[2] = v.z; xv[3] = v.w;
       const float4 w4 = *reinterpret_cast<const float4*>(&ws[buf][kk][tn * 4]);
       wv[0] = w4.x; wv[1] = w4.y; wv[2] = w4.z; wv[3] = w4.w;
 #pragma unroll
@@ -1201,22 +1233,26 @@ __global__ __launch_bounds__(kGenThreads) void k_w8a16_general(
   for (int j = 0; j < TN; ++j) {
     const int64_t n = n0 + tn * 4 + j;
     if (n >= N) continue;
-    const float sc = ld1<ACT>(scales, n);
-    const float bv = bias ? ld1<ACT>(bias, n) : 0.0f;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int64_t m = m0 + tm * TM + i;
       if (m >= M) continue;
-      float val = acc[i][j] * sc;
-      for (int64_t jj = 0; jj < n_out; ++jj) {
-        const int64_t k = oc[jj];
-        if (k >= 0 && k < K) val += ld1<ACT>(x, m * K + k) * ld1<ACT>(w_out, n * n_out + jj);
-      }
-      if (bias) val += bv;
-      if constexpr (ACT == kF32) static_cast<float*>(y)[m * N + n] = val;
-      else static_cast<uint16_t*>(y)[m * N + n] = out1<ACT>(val);
+      if constexpr (SPLIT) a.part[(split * M + m) * N + n] = acc[i][j];
+      else general_out<ACT>(a, m, n, acc[i][j]);
     }
   }
+}
+
+// Split-K finish of the general path: one thread per output, the ranges
+// summed in order, then the epilogue.
+template <int ACT>
+__global__ __launch_bounds__(kBlock) void k_general_reduce(GenArgs a) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  const int64_t mn = a.M * a.N;
+  if (idx >= mn) return;
+  float sum = a.part[idx];
+  for (int sp = 1; sp < a.splits; ++sp) sum += a.part[sp * mn + idx];
+  general_out<ACT>(a, idx / a.N, idx % a.N, sum);
 }
 
 // ---------------------------------------------------------------------------
@@ -1318,24 +1354,64 @@ void launch_kind(Kind k, const GemmArgs& a, hipStream_t s) {
   }
 }
 
+// Tile of the general path: 16 x 256 for M <= 16, else 64 x 64.
+int general_bm(int64_t M) { return M <= 16 ? 16 : 64; }
+int general_bn(int64_t M) { return M <= 16 ? 256 : 64; }
+
+// k-ranges of the general path (1: no split): enough workgroups for about
+// four per CU when the tiles alone are fewer than two per CU, each range at
+// least four 32-k steps, at most 16 ranges (measured on MI355X, M = 16,
+// N = 11008, K = 4096, fp32: 289 us in one range).
+int general_splits(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = cdiv(M, general_bm(M)) * cdiv(N, general_bn(M));
+  const int64_t cus = device_cus();
+  if (tiles >= 2 * cus) return 1;
+  const int64_t sp = std::min<int64_t>({16, cdiv(4 * cus, tiles), K / (4 * kGenBK)});
+  return sp >= 2 ? static_cast<int>(sp) : 1;
+}
+
+int64_t general_split_bytes(int64_t M, int64_t N, int64_t K) {
+  const int sp = general_splits(M, N, K);
+  return sp > 1 ? static_cast<int64_t>(sp) * M * N * 4 : 0;
+}
+
 template <int ACT>
 int w8a16_general(const void* x, const int8_t* wq, const void* scales, const void* bias,
                   const int64_t* oc, int64_t n_out, const void* w_out, int64_t M, int64_t N,
-                  int64_t K, void* y, hipStream_t s) {
-  const int bm = M <= 16 ? 16 : 64;
-  const int64_t tiles_n = cdiv(N, static_cast<int64_t>(kGenBN));
-  const int64_t tiles = cdiv(M, static_cast<int64_t>(bm)) * tiles_n;
-  if (tiles > 0x7fffffffLL) {
+                  int64_t K, void* ws, size_t ws_bytes, void* y, hipStream_t s) {
+  const int bm = general_bm(M), bn = general_bn(M);
+  GenArgs a{};
+  a.x = x; a.wq = wq; a.scales = scales; a.bias = bias; a.oc = oc; a.w_out = w_out; a.y = y;
+  a.n_out = n_out; a.M = M; a.N = N; a.K = K;
+  a.tiles_n = cdiv(N, static_cast<int64_t>(bn));
+  a.tiles = cdiv(M, static_cast<int64_t>(bm)) * a.tiles_n;
+  int sp = general_splits(M, N, K);
+  if (sp > 1 && (!ws || ws_bytes < static_cast<size_t>(CBQ_WS_CTRL_BYTES + general_split_bytes(M, N, K))))
+    sp = 1;   // no room for the partial sums: one range
+  if (sp > 1) {
+    a.kper = cdiv(cdiv(K, static_cast<int64_t>(kGenBK)), sp) * kGenBK;
+    a.splits = static_cast<int>(cdiv(K, a.kper));   // no empty ranges
+    a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + CBQ_WS_CTRL_BYTES);
+  } else {
+    a.kper = K;
+    a.splits = 1;
+  }
+  const int64_t blocks = a.tiles * a.splits;
+  if (blocks > 0x7fffffffLL || cdiv(M * N, static_cast<int64_t>(kBlock)) > 0x7fffffffLL) {
     set_error("cbq_w8a16_linear: output too large for the general path");
     return CBQ_EINVAL;
   }
-  const dim3 g(static_cast<unsigned>(tiles)), b(kGenThreads);
-  if (bm == 16)
-    k_w8a16_general<ACT, 16><<<g, b, 0, s>>>(x, wq, scales, bias, oc, n_out, w_out, y, M, N, K,
-                                             tiles_n);
-  else
-    k_w8a16_general<ACT, 64><<<g, b, 0, s>>>(x, wq, scales, bias, oc, n_out, w_out, y, M, N, K,
-                                             tiles_n);
+  const dim3 g(static_cast<unsigned>(blocks)), b(kGenThreads);
+  if (a.splits > 1) {
+    if (bm == 16) k_w8a16_general<ACT, 16, 256, true><<<g, b, 0, s>>>(a);
+    else k_w8a16_general<ACT, 64, 64, true><<<g, b, 0, s>>>(a);
+    k_general_reduce<ACT><<<dim3(static_cast<unsigned>(cdiv(M * N, static_cast<int64_t>(kBlock)))),
+                            dim3(kBlock), 0, s>>>(a);
+  } else if (bm == 16) {
+    k_w8a16_general<ACT, 16, 256, false><<<g, b, 0, s>>>(a);
+  } else {
+    k_w8a16_general<ACT, 64, 64, false><<<g, b, 0, s>>>(a);
+  }
   return launch_status("cbq_w8a16_linear");
 }
 
@@ -1351,7 +1427,7 @@ int w8a16_t(const void* x, const int8_t* wq, const void* scales, const void* bia
             const int64_t* oc, int64_t n_out, const void* w_out, int64_t M, int64_t N, int64_t K,
             void* ws, size_t ws_bytes, void* y, hipStream_t s) {
   if (!mfma_path(M, N, K, x, wq, y))
-    return w8a16_general<ACT>(x, wq, scales, bias, oc, n_out, w_out, M, N, K, y, s);
+    return w8a16_general<ACT>(x, wq, scales, bias, oc, n_out, w_out, M, N, K, ws, ws_bytes, y, s);
   GemmArgs a{};
   a.x = static_cast<const uint16_t*>(x);
   a.wq = wq;
@@ -1381,8 +1457,11 @@ using namespace cbq;
 extern "C" size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_out) {
   (void)n_out;
   if (M <= 0 || N <= 0 || K <= 0) return CBQ_WS_CTRL_BYTES;
+  // The larger of the MFMA split-K partials and the general path's partial
+  // sums (the dtype and alignment that choose between them are not known here).
   const int sp = splitk_count(M, N, K);
-  return CBQ_WS_CTRL_BYTES + (sp ? static_cast<size_t>(splitk_bytes(M, N, sp)) : 0);
+  const int64_t mfma = sp ? splitk_bytes(M, N, sp) : 0;
+  return CBQ_WS_CTRL_BYTES + static_cast<size_t>(std::max(mfma, general_split_bytes(M, N, K)));
 }
 
 extern "C" int cbq_w8a16_linear(const void* x, int act_dtype, const int8_t* wq,
@@ -1401,21 +1480,21 @@ extern "C" int cbq_w8a16_linear(const void* x, int act_dtype, const int8_t* wq,
   CBQ_REQUIRE(scales && y && (K == 0 || (x && wq)), "%s: null pointer", what);
   CBQ_REQUIRE(n_out == 0 || (outlier_cols && w_out), "%s: outlier columns need indices and weights",
               what);
-  if (K == 0) {
-    hipStream_t s = as_stream(stream);
-    return act_dtype == kF32 ? w8a16_general<kF32>(x, wq, scales, bias, nullptr, 0, nullptr, M, N,
-                                                  K, y, s)
-           : act_dtype == kF16 ? w8a16_general<kF16>(x, wq, scales, bias, nullptr, 0, nullptr, M,
-                                                    N, K, y, s)
-                               : w8a16_general<kBF16>(x, wq, scales, bias, nullptr, 0, nullptr, M,
-                                                     N, K, y, s);
-  }
-  if (act_dtype == kF32)
-    return w8a16_general<kF32>(x, wq, scales, bias, outlier_cols, n_out, w_out, M, N, K, y,
-                              as_stream(stream));
   // The split-K partials go after the control block; a workspace that is
   // missing, unaligned or too small selects a path without partials.
   if (ws && !aligned(ws, 256)) ws = nullptr;
+  if (K == 0) {
+    hipStream_t s = as_stream(stream);
+    return act_dtype == kF32 ? w8a16_general<kF32>(x, wq, scales, bias, nullptr, 0, nullptr, M, N,
+                                                  K, nullptr, 0, y, s)
+           : act_dtype == kF16 ? w8a16_general<kF16>(x, wq, scales, bias, nullptr, 0, nullptr, M,
+                                                    N, K, nullptr, 0, y, s)
+                               : w8a16_general<kBF16>(x, wq, scales, bias, nullptr, 0, nullptr, M,
+                                                     N, K, nullptr, 0, y, s);
+  }
+  if (act_dtype == kF32)
+    return w8a16_general<kF32>(x, wq, scales, bias, outlier_cols, n_out, w_out, M, N, K, ws,
+                              ws_bytes, y, as_stream(stream));
   return act_dtype == kF16
              ? w8a16_t<kF16>(x, wq, scales, bias, outlier_cols, n_out, w_out, M, N, K, ws,
                              ws_bytes, y, as_stream(stream))

@@ -87,7 +87,9 @@ def test_workspace_sizes():
     assert L.cbq_quant_tensor_ws_bytes() == C + 4 * 2048
     big = L.cbq_quant_int8_channel_ws_bytes(28672, 8192, 1)
     assert big >= C + 8192 * 4 * 2 and big < 64 << 20
-    assert L.cbq_w8a16_ws_bytes(16, 11008, 4096, 0) == C
+    # M <= 16: room for the general path's k-split partial sums (16 ranges of
+    # [16, 11008] fp32 over 43 tiles of 16 x 256)
+    assert L.cbq_w8a16_ws_bytes(16, 11008, 4096, 0) == C + 16 * 16 * 11008 * 4
     assert L.cbq_w8a16_ws_bytes(4096, 11008, 4096, 0) == C
     # split-K tile path (64 < M < 1024): 4 k-ranges x 43 tiles of 256 KiB
     # fp32 partials (256 CUs, also the CPU-only fallback count)
