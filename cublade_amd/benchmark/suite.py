@@ -222,6 +222,25 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
             out.append(r)
             print(json.dumps(r), flush=True)
         del ah, wh
+        # The reference's own WMMA benchmark shapes (examples/kernels/
+        # wmma_simple.py:137-150) up to 4096^3: few 256 x 256 tiles, K split.
+        for n in (512, 1024, 2048, 4096):
+            fl = 2.0 * n ** 3
+            a8 = torch.randint(-128, 128, (n, n), generator=g, dtype=torch.int16).to(torch.int8).to(dev)
+            b8 = torch.randint(-128, 128, (n, n), generator=g, dtype=torch.int16).to(torch.int8).to(dev)
+            ah = torch.randn(n, n, generator=g).half().to(dev)
+            bh = torch.randn(n, n, generator=g).half().to(dev)
+            for name, fn, i8 in [(f"mm_i8_kn_{n}", lambda: wmma_gemm(a8, b8), True),
+                                 (f"torch_int_mm_i8_{n}", lambda: torch._int_mm(a8, b8), True),
+                                 (f"mm_f16_f32_kn_{n}", lambda: wmma_gemm(ah, bh), False),
+                                 (f"torch_matmul_f16_{n}", lambda: torch.matmul(ah, bh), False)]:
+                r = _rec("f4", name, time_op(fn, reps, warmup, flush), None, fl)
+                if i8:
+                    r["tops"] = r.pop("tflops")
+                    r["mfma_frac"] = round(r["tops"] * 1e12 / I8_MFMA_PEAK_OP_S, 4)
+                out.append(r)
+                print(json.dumps(r), flush=True)
+            del a8, b8, ah, bh
     torch.cuda.synchronize()
     return out
 

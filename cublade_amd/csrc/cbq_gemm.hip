@@ -14,7 +14,7 @@
 // Integer results are exact modulo 2^32 (int32 wrap-around, as the int32
 // accumulators of the reference).
 //
-// k_mm_dma<IN, OUT>: 256 x 256 output tiles, 8 waves (two per SIMD) of
+// k_mm_dma<IN, OUT, SPLIT>: 256 x 256 output tiles, 8 waves (two per SIMD) of
 // 128 (m) x 64 (n) (4 x 2 tiles of 32 x 32), k-steps of 64 bytes per row (64
 // int8 or 32 fp16 k), four LDS stages of 32 KiB filled by LDS DMA
 // (global_load_lds_dwordx4), three k-steps in flight, one barrier per k-step
@@ -22,6 +22,10 @@
 // reads overlap the second substep's MFMAs. Measured on MI355X at 8192^3
 // (random data): two waves per SIMD raise rocprof's MfmaUtil from ~47% to
 // 58% (int8) / 65% (fp16); the int8 kernel then runs level with hipBLASLt.
+// When the 256 x 256 tiles alone leave CUs idle (small M x N), the host
+// splits K into ranges (mm_splits): k_mm_dma<IN, OUT, true> writes each
+// range's raw int32 / fp32 sums to the workspace and k_mm_reduce adds the
+// ranges in order (int32 wrap-around: bit-exact; fp32: deterministic).
 // Both operands are K-contiguous rows: A [M, K] as given
 // and B as B^T [N, K]. A B that is stored [N, K] (B = W^T, the usual weight
 // layout) is read in place; a [K, N] B is transposed into the workspace
@@ -87,6 +91,10 @@ struct MmArgs {
   int nk;                // 64-byte k-steps
   int K;                 // true K (the uint8 correction's 16384 K term)
   int tiles_m, tiles_n;
+  // split-K: `splits` k-ranges of `split_steps` 64-byte steps; range s writes
+  // its raw sums (int32 or fp32) to part[s][M][N] and k_mm_reduce adds them
+  void* part;
+  int splits, split_steps;
 };
 
 // Workgroup -> (tile m, tile n): XCD b % 8 gets a contiguous run of logical
@@ -111,7 +119,7 @@ constexpr int kMmSB = 2 * kMmHalf;       // stage bytes (32 KiB)
 constexpr int kMmThreads = 512;          // 8 waves, two per SIMD
 constexpr int kMmL = kMmHalf / (kMmThreads * 16);   // DMA instructions per operand per thread (2)
 
-template <int IN, int OUT>
+template <int IN, int OUT, bool SPLIT>
 __global__ __launch_bounds__(kMmThreads) void k_mm_dma(MmArgs a) {
   typedef typename AccOf<IN>::type Acc;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kMmNS * kMmSB];
@@ -120,10 +128,17 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_dma(MmArgs a) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;   // 128-row half of m, 64-column quarter of n
-  int tm, tn;
-  mm_tile(blockIdx.x, a, tm, tn);
+  int tm, tn, split = 0;
+  if constexpr (SPLIT) {
+    const int tiles = a.tiles_m * a.tiles_n;
+    split = blockIdx.x / tiles;
+    mm_tile(blockIdx.x % tiles, a, tm, tn);
+  } else {
+    mm_tile(blockIdx.x, a, tm, tn);
+  }
   const int m0 = tm * 256, n0 = tn * 256;
-  const int nk = a.nk;
+  const int kb = SPLIT ? split * a.split_steps : 0;   // first 64-byte k-step of this range
+  const int nk = SPLIT ? min(a.split_steps, a.nk - kb) : a.nk;
   const uint32_t sbase = __builtin_amdgcn_readfirstlane(lds_addr(smem));
 
   // DMA sources: instruction u of an operand fills rows (u * 8 + wave) * 16
@@ -140,8 +155,8 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_dma(MmArgs a) {
   }
   auto issue = [&](int t, int stage) {
     const uint32_t dst = sbase + stage * kMmSB + wave * 1024;
-    const uint8_t* pa = uniform_ptr(a.a + t * 64);
-    const uint8_t* pb = uniform_ptr(a.bt + t * 64);
+    const uint8_t* pa = uniform_ptr(a.a + (kb + t) * 64);
+    const uint8_t* pb = uniform_ptr(a.bt + (kb + t) * 64);
 #pragma unroll
     for (int u = 0; u < kMmL; ++u) lds_dma16(ao[u], pa, dst + u * 8192);
 #pragma unroll
@@ -235,9 +250,13 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_dma(MmArgs a) {
   }
 
   // Epilogue: C[m][n], n = 32 i + r32, m = 32 j + 8 (v / 4) + 4 h + v % 4;
-  // 32-bit offsets from the wave's corner (128 rows of N elements).
-  constexpr int ES_OUT = OUT == kOutF16 ? 2 : 4;
-  uint8_t* cw = static_cast<uint8_t*>(a.c) + (static_cast<int64_t>(mw) * a.N + nw) * ES_OUT;
+  // 32-bit offsets from the wave's corner (128 rows of N elements). A split
+  // range stores its raw 4-byte sums to its plane of the partial buffer.
+  typedef typename std::conditional<IN == kInI8, int, float>::type PartT;
+  constexpr int ES_OUT = (OUT == kOutF16 && !SPLIT) ? 2 : 4;
+  uint8_t* cw = SPLIT ? static_cast<uint8_t*>(a.part) +
+                            ((static_cast<int64_t>(split) * a.M + mw) * a.N + nw) * ES_OUT
+                      : static_cast<uint8_t*>(a.c) + (static_cast<int64_t>(mw) * a.N + nw) * ES_OUT;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -249,7 +268,9 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_dma(MmArgs a) {
           const int ml = 32 * j + 8 * (v >> 2) + 4 * h + (v & 3);
           if (mw + ml < a.M) {
             const uint32_t off = (static_cast<uint32_t>(ml) * static_cast<uint32_t>(a.N) + nl) * ES_OUT;
-            if constexpr (OUT == kOutI32)
+            if constexpr (SPLIT)
+              *reinterpret_cast<PartT*>(cw + off) = acc[j][i][v];
+            else if constexpr (OUT == kOutI32)
               *reinterpret_cast<int*>(cw + off) = acc[j][i][v];
             else if constexpr (OUT == kOutF32)
               *reinterpret_cast<float*>(cw + off) = acc[j][i][v];
@@ -260,6 +281,28 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_dma(MmArgs a) {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+  }
+}
+
+// Split-K finish: C = the sum of the ranges' partial planes, in range order
+// (int32 wrap-around for integer inputs, fp32 for float inputs, then one
+// rounding for fp16 outputs). One thread per output.
+template <int IN, int OUT>
+__global__ __launch_bounds__(kBlock) void k_mm_reduce(MmArgs a) {
+  const int64_t mn = static_cast<int64_t>(a.M) * a.N;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (idx >= mn) return;
+  if constexpr (IN == kInI8) {
+    const uint32_t* p = static_cast<const uint32_t*>(a.part) + idx;
+    uint32_t sum = p[0];
+    for (int s = 1; s < a.splits; ++s) sum += p[s * mn];
+    static_cast<uint32_t*>(a.c)[idx] = sum;
+  } else {
+    const float* p = static_cast<const float*>(a.part) + idx;
+    float sum = p[0];
+    for (int s = 1; s < a.splits; ++s) sum += p[s * mn];
+    if constexpr (OUT == kOutF16) static_cast<_Float16*>(a.c)[idx] = static_cast<_Float16>(sum);
+    else static_cast<float*>(a.c)[idx] = sum;
   }
 }
 
@@ -400,8 +443,30 @@ struct MmPlan {
   bool u8;
   int64_t kb, ldk;     // row bytes, padded row bytes
   bool stage_a, stage_b;
-  size_t a_off, b_off, rs_off, cs_off, bytes;
+  int splits;          // k-ranges (1: no split-K)
+  size_t a_off, b_off, rs_off, cs_off, part_off, bytes;
 };
+
+// k-ranges for C = A . B when the 256 x 256 tiles alone leave CUs idle: the
+// count with the lowest modelled time, one range included: 1.0 us per
+// 64-byte k-step of the longest range (k_mm_dma at 8192^3, int8 and fp16),
+// plus, when split, 0.09 us per 256 KiB of 4-byte partial sums written and
+// re-read and 5 us for the reduce pass. At most 16 ranges, at most one
+// workgroup per CU, at least four k-steps per range.
+int mm_splits(int64_t M, int64_t N, int64_t nk) {
+  const int64_t tiles = cdiv(M, 256) * cdiv(N, 256);
+  const int64_t max_sp = std::min<int64_t>({16, device_cus() / tiles, nk / 4});
+  int best = 1;
+  int64_t best_cost = 100 * nk;
+  for (int64_t sp = 2; sp <= max_sp; ++sp) {
+    const int64_t cost = 100 * cdiv(nk, sp) + 9 * cdiv(sp * M * N * 4, 262144) + 500;
+    if (cost < best_cost) {
+      best = static_cast<int>(sp);
+      best_cost = cost;
+    }
+  }
+  return best;
+}
 
 size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
@@ -427,13 +492,23 @@ bool mm_plan(int64_t M, int64_t N, int64_t K, int in_dtype, int b_layout, MmPlan
   if (p.u8) off = align256(off + static_cast<size_t>(M) * 4);
   p.cs_off = off;
   if (p.u8) off = align256(off + static_cast<size_t>(N) * 4);
+  p.splits = (M > 0 && N > 0 && K > 0) ? mm_splits(M, N, p.ldk / 64) : 1;
+  p.part_off = off;
+  if (p.splits > 1) off = align256(off + static_cast<size_t>(p.splits) * M * N * 4);
   p.bytes = off;
   return true;
 }
 
 template <int IN, int OUT>
 void launch_mm(const MmArgs& a, hipStream_t s) {
-  k_mm_dma<IN, OUT><<<dim3(static_cast<unsigned>(a.tiles_m * a.tiles_n)), dim3(kMmThreads), 0, s>>>(a);
+  const unsigned tiles = static_cast<unsigned>(a.tiles_m * a.tiles_n);
+  if (a.splits > 1) {
+    k_mm_dma<IN, OUT, true><<<dim3(tiles * a.splits), dim3(kMmThreads), 0, s>>>(a);
+    const int64_t mn = static_cast<int64_t>(a.M) * a.N;
+    k_mm_reduce<IN, OUT><<<dim3(static_cast<unsigned>(cdiv(mn, kBlock))), dim3(kBlock), 0, s>>>(a);
+  } else {
+    k_mm_dma<IN, OUT, false><<<dim3(tiles), dim3(kMmThreads), 0, s>>>(a);
+  }
 }
 
 unsigned grid_for(int64_t work, int64_t per_block) {
@@ -510,6 +585,14 @@ extern "C" int cbq_mm(const void* A, const void* B, int in_dtype, int b_layout, 
   a.K = static_cast<int>(K);
   a.tiles_m = static_cast<int>(cdiv(M, 256));
   a.tiles_n = static_cast<int>(cdiv(N, 256));
+  a.part = nullptr;
+  a.splits = 1;
+  a.split_steps = a.nk;
+  if (p.splits > 1) {
+    a.split_steps = static_cast<int>(cdiv(a.nk, p.splits));
+    a.splits = static_cast<int>(cdiv(a.nk, a.split_steps));   // no empty ranges
+    a.part = w + p.part_off;
+  }
   if (p.stage_a && K > 0) {
     uint8_t* da = w + p.a_off;
     const unsigned g = grid_for(M * (p.ldk / 16), kBlock);

@@ -221,7 +221,8 @@ enum { CBQ_MM_B_KN = 0, CBQ_MM_B_NK = 1 };
 /* Workspace bytes for cbq_mm at this shape: the control block, plus staging
  * buffers when B is [K, N] (transposed copy), the inputs are uint8 (offset
  * copies and row sums) or K * element bytes is not a multiple of 64 (padded
- * copies). */
+ * copies), plus, when the 256 x 256 output tiles are fewer than the CUs,
+ * the 4-byte partial sums of a split over K (up to 16 x M x N x 4 bytes). */
 size_t cbq_mm_ws_bytes(int64_t M, int64_t N, int64_t K, int in_dtype,
                        int b_layout);
 

@@ -160,6 +160,8 @@ def test_mm_entry_point_validates_and_sizes():
     # fp16: 2-byte elements, K = 48 -> 96 bytes -> 128-byte rows
     assert L.cbq_mm_ws_bytes(16, 16, 48, F16, NK) == a256(a256(C + 16 * 128) + 16 * 128)
     assert L.cbq_mm_ws_bytes(16, 16, 64, BF16, NK) == C
+    # few tiles: K split into 16 ranges, int32 partial planes [16, M, N]
+    assert L.cbq_mm_ws_bytes(64, 1024, 4096, I8, NK) == C + 16 * 64 * 1024 * 4
     P = ctypes.c_void_p
     f = P(0x10000)
     ws = P(0x100000)
