@@ -147,6 +147,28 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
             rq["speedup_vs_fp16"] = round(statistics.median(us_f) / statistics.median(us_q), 3)
             out += [rq, rf]
             print(json.dumps(rq), json.dumps(rf), sep="\n", flush=True)
+        # The M = 16 decode step captured in a HIP graph (torch.cuda.graph):
+        # replays carry no per-call host work.
+        x16 = torch.randn(16, 4096, generator=g).half().to(dev)
+        flops = 3 * 2.0 * 16 * 4096 * 11008
+        graph_us = {}
+        for tag, blk in (("w8a16", qblock), ("fp16", block)):
+            st = torch.cuda.Stream()
+            with torch.no_grad(), torch.cuda.stream(st):
+                for _ in range(3):
+                    blk(x16)
+            torch.cuda.synchronize()
+            cg = torch.cuda.CUDAGraph()
+            with torch.no_grad(), torch.cuda.graph(cg, stream=st):
+                blk(x16)
+            graph_us[tag] = time_op(cg.replay, reps, warmup, flush)
+            del cg
+        rq = _rec("f1", "mlp_w8a16_m16_graph", graph_us["w8a16"], 3 * 4096 * 11008, flops)
+        rf = _rec("f1", "mlp_fp16_m16_graph", graph_us["fp16"], 3 * 2 * 4096 * 11008, flops)
+        rq["speedup_vs_fp16"] = round(statistics.median(graph_us["fp16"]) /
+                                      statistics.median(graph_us["w8a16"]), 3)
+        out += [rq, rf]
+        print(json.dumps(rq), json.dumps(rf), sep="\n", flush=True)
         del block, qblock
     if "f3" in selected:
         # Non-default axes in place: groups along axis 0 of config 4's tensor
