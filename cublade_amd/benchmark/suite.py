@@ -10,7 +10,7 @@ passes); dequant N + 2N + 4 * scales. W8A16 and the dense GEMM: 2 * M * N * K
 FLOPs (int8 GEMMs against the 5.0 POP/s dense int8 peak, the fp32-activation
 W8A16 against the 157.3 TFLOP/s fp32 peak).
 
-    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5,c5f32,f1,f3,f4 [--json out.json]
+    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5,c5f32,f1,f3,f4,f4s [--json out.json]
 """
 from __future__ import annotations
 
@@ -244,8 +244,11 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
             out.append(r)
             print(json.dumps(r), flush=True)
         del ah, wh
+    if "f4s" in selected:
         # The reference's own WMMA benchmark shapes (examples/kernels/
         # wmma_simple.py:137-150) up to 4096^3: few 256 x 256 tiles, K split.
+        from cublade_amd.bindings.hip.wmma import wmma_gemm
+        g = torch.Generator().manual_seed(7)
         for n in (512, 1024, 2048, 4096):
             fl = 2.0 * n ** 3
             a8 = torch.randint(-128, 128, (n, n), generator=g, dtype=torch.int16).to(torch.int8).to(dev)
@@ -256,7 +259,7 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
                                  (f"torch_int_mm_i8_{n}", lambda: torch._int_mm(a8, b8), True),
                                  (f"mm_f16_f32_kn_{n}", lambda: wmma_gemm(ah, bh), False),
                                  (f"torch_matmul_f16_{n}", lambda: torch.matmul(ah, bh), False)]:
-                r = _rec("f4", name, time_op(fn, reps, warmup, flush), None, fl)
+                r = _rec("f4s", name, time_op(fn, reps, warmup, flush), None, fl)
                 if i8:
                     r["tops"] = r.pop("tflops")
                     r["mfma_frac"] = round(r["tops"] * 1e12 / I8_MFMA_PEAK_OP_S, 4)
@@ -269,7 +272,7 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,c5f32,f1,f3,f4")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,c5f32,f1,f3,f4,f4s")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--json", default=None)
