@@ -14,7 +14,7 @@
 // Integer results are exact modulo 2^32 (int32 wrap-around, as the int32
 // accumulators of the reference).
 //
-// k_mm_dma<IN, OUT, SPLIT>: 256 x 256 output tiles, 8 waves (two per SIMD) of
+// k_mm_dma<IN, OUT, SPLIT, T>: T x T output tiles; T = 256: 8 waves (two per SIMD) of
 // 128 (m) x 64 (n) (4 x 2 tiles of 32 x 32), k-steps of 64 bytes per row (64
 // int8 or 32 fp16 k), four LDS stages of 32 KiB filled by LDS DMA
 // (global_load_lds_dwordx4), three k-steps in flight, one barrier per k-step
@@ -22,10 +22,12 @@
 // reads overlap the second substep's MFMAs. Measured on MI355X at 8192^3
 // (random data): two waves per SIMD raise rocprof's MfmaUtil from ~47% to
 // 58% (int8) / 65% (fp16); the int8 kernel then runs level with hipBLASLt.
-// When the 256 x 256 tiles alone leave CUs idle (small M x N), the host
-// splits K into ranges (mm_splits): k_mm_dma<IN, OUT, true> writes each
-// range's raw int32 / fp32 sums to the workspace and k_mm_reduce adds the
-// ranges in order (int32 wrap-around: bit-exact; fp32: deterministic).
+// T = 128 (4 waves of 64 x 64, two workgroups per CU) serves shapes whose
+// 256 x 256 tiles would leave CUs idle, and the host may also split K into
+// ranges (mm_choose picks both from a time model): k_mm_dma<IN, OUT, true, T>
+// writes each range's raw int32 / fp32 sums to the workspace and k_mm_reduce
+// adds the ranges in order (int32 wrap-around: bit-exact; fp32:
+// deterministic).
 // Both operands are K-contiguous rows: A [M, K] as given
 // and B as B^T [N, K]. A B that is stored [N, K] (B = W^T, the usual weight
 // layout) is read in place; a [K, N] B is transposed into the workspace
@@ -97,9 +99,9 @@ struct MmArgs {
   int splits, split_steps;
 };
 
-// Workgroup -> (tile m, tile n): XCD b % 8 gets a contiguous run of logical
-// tiles, which run in groups of 8 m-tiles so that the workgroups resident on
-// one XCD share A and B^T k-slices in its L2.
+// Workgroup -> (tile m, tile n) of the tiles_m x tiles_n grid: XCD b % 8
+// gets a contiguous run of logical tiles, which run in groups of 8 m-tiles so
+// that the workgroups resident on one XCD share A and B^T k-slices in its L2.
 __device__ __forceinline__ void mm_tile(int b, const MmArgs& a, int& tm, int& tn) {
   const int total = a.tiles_m * a.tiles_n;
   const int per = total >> 3;
@@ -114,20 +116,32 @@ __device__ __forceinline__ void mm_tile(int b, const MmArgs& a, int& tm, int& tn
 }
 
 constexpr int kMmNS = 4;                 // LDS stages
-constexpr int kMmHalf = 256 * 64;        // bytes of one operand per stage
-constexpr int kMmSB = 2 * kMmHalf;       // stage bytes (32 KiB)
-constexpr int kMmThreads = 512;          // 8 waves, two per SIMD
-constexpr int kMmL = kMmHalf / (kMmThreads * 16);   // DMA instructions per operand per thread (2)
 
-template <int IN, int OUT, bool SPLIT>
-__global__ __launch_bounds__(kMmThreads) void k_mm_dma(MmArgs a) {
+// Geometry of a T x T output tile (T = 256: 8 waves of 128 x 64, two per
+// SIMD, one workgroup per CU; T = 128: 4 waves of 64 x 64, two workgroups
+// per CU). Each wave computes J x 2 tiles of 32 x 32.
+template <int T> struct MmGeom {
+  static constexpr int kThreads = T == 256 ? 512 : 256;
+  static constexpr int kWaves = kThreads / 64;
+  static constexpr int kHalf = T * 64;                     // bytes of one operand per stage
+  static constexpr int kSB = 2 * kHalf;                    // stage bytes
+  static constexpr int kL = kHalf / (kThreads * 16);       // DMA instructions per operand per thread
+  static constexpr int kWM = T / 2;                        // rows of a wave tile
+  static constexpr int kJ = kWM / 32;                      // 32-row tiles per wave
+  static_assert(kL == 2 && T / (kWaves / 2) == 64, "two DMA rows per thread, 64-column wave tiles");
+};
+
+template <int IN, int OUT, bool SPLIT, int T>
+__global__ __launch_bounds__(MmGeom<T>::kThreads) void k_mm_dma(MmArgs a) {
   typedef typename AccOf<IN>::type Acc;
+  typedef MmGeom<T> G;
+  constexpr int kMmHalf = G::kHalf, kMmSB = G::kSB, kMmL = G::kL, J = G::kJ;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kMmNS * kMmSB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 1, wn = wave >> 1;   // 128-row half of m, 64-column quarter of n
+  const int wm = wave & 1, wn = wave >> 1;   // T/2-row half of m, 64-column slice of n
   int tm, tn, split = 0;
   if constexpr (SPLIT) {
     const int tiles = a.tiles_m * a.tiles_n;
@@ -136,19 +150,19 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_dma(MmArgs a) {
   } else {
     mm_tile(blockIdx.x, a, tm, tn);
   }
-  const int m0 = tm * 256, n0 = tn * 256;
+  const int m0 = tm * T, n0 = tn * T;
   const int kb = SPLIT ? split * a.split_steps : 0;   // first 64-byte k-step of this range
   const int nk = SPLIT ? min(a.split_steps, a.nk - kb) : a.nk;
   const uint32_t sbase = __builtin_amdgcn_readfirstlane(lds_addr(smem));
 
-  // DMA sources: instruction u of an operand fills rows (u * 8 + wave) * 16
-  // + lane / 4, chunk slot lane % 4, which holds source chunk slot ^ swizzle.
+  // DMA sources: instruction u of an operand fills rows (u * waves + wave) *
+  // 16 + lane / 4, chunk slot lane % 4, which holds source chunk slot ^ swizzle.
   // Rows past M or N are clamped to the last row; their products land in
   // outputs that are never stored.
   uint32_t ao[kMmL], bo[kMmL];
 #pragma unroll
   for (int u = 0; u < kMmL; ++u) {
-    const int row = (u * 8 + wave) * 16 + (lane >> 2);
+    const int row = (u * G::kWaves + wave) * 16 + (lane >> 2);
     const int c = (lane & 3) ^ ((row >> 2) & 3);
     ao[u] = static_cast<uint32_t>(min(m0 + row, a.M - 1)) * static_cast<uint32_t>(a.ldk) + c * 16u;
     bo[u] = static_cast<uint32_t>(min(n0 + row, a.N - 1)) * static_cast<uint32_t>(a.ldk) + c * 16u;
@@ -158,9 +172,9 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_dma(MmArgs a) {
     const uint8_t* pa = uniform_ptr(a.a + (kb + t) * 64);
     const uint8_t* pb = uniform_ptr(a.bt + (kb + t) * 64);
 #pragma unroll
-    for (int u = 0; u < kMmL; ++u) lds_dma16(ao[u], pa, dst + u * 8192);
+    for (int u = 0; u < kMmL; ++u) lds_dma16(ao[u], pa, dst + u * G::kWaves * 1024);
 #pragma unroll
-    for (int u = 0; u < kMmL; ++u) lds_dma16(bo[u], pb, dst + kMmHalf + u * 8192);
+    for (int u = 0; u < kMmL; ++u) lds_dma16(bo[u], pb, dst + kMmHalf + u * G::kWaves * 1024);
   };
 
   // Fragment read offsets: row r32 of 32-row tile j (A) / i (B^T), chunk
@@ -170,33 +184,34 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_dma(MmArgs a) {
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     const uint32_t slot = static_cast<uint32_t>((2 * h + s) ^ ((r32 >> 2) & 3)) << 4;
-    ar[s] = (wm * 128 + r32) * 64 + slot;
+    ar[s] = (wm * G::kWM + r32) * 64 + slot;
     br[s] = kMmHalf + (wn * 64 + r32) * 64 + slot;
   }
 
-  const int mw = m0 + wm * 128, nw = n0 + wn * 64;
-  Acc acc[4][2];   // [j: m-tile][i: n-tile]
+  const int mw = m0 + wm * G::kWM, nw = n0 + wn * 64;
+  Acc acc[J][2];   // [j: m-tile][i: n-tile]
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int j = 0; j < J; ++j)
 #pragma unroll
     for (int i = 0; i < 2; ++i) acc[j][i] = Acc{};
 
-  // Fragments of one k-substep: 4 A tiles, 2 B^T tiles (6 reads, 8 MFMAs).
+  // Fragments of one k-substep: J A tiles, 2 B^T tiles (J + 2 reads, 2 J
+  // MFMAs).
   struct Frags {
-    u32x4 x[4];
+    u32x4 x[J];
     u32x4 w[2];
   };
   auto read_one = [&](int stage, int s, Frags& f, int r) {
     const uint8_t* st = smem + stage * kMmSB;
-    if (r < 4) f.x[r] = *reinterpret_cast<const u32x4*>(st + ar[s] + r * 2048);
-    else f.w[r - 4] = *reinterpret_cast<const u32x4*>(st + br[s] + (r - 4) * 2048);
+    if (r < J) f.x[r] = *reinterpret_cast<const u32x4*>(st + ar[s] + r * 2048);
+    else f.w[r - J] = *reinterpret_cast<const u32x4*>(st + br[s] + (r - J) * 2048);
   };
   auto read = [&](int stage, int s, Frags& f) {
 #pragma unroll
-    for (int r = 0; r < 6; ++r) read_one(stage, s, f, r);
+    for (int r = 0; r < J + 2; ++r) read_one(stage, s, f, r);
   };
-  // MFMA q (0..7) of a substep: tile (j, i) = (q / 2, q % 2); an accumulator
-  // is reused every 8th MFMA.
+  // MFMA q (0 .. 2 J - 1) of a substep: tile (j, i) = (q / 2, q % 2); an
+  // accumulator is reused every (2 J)th MFMA.
   auto mma_one = [&](const Frags& f, int q) {
     acc[q >> 1][q & 1] = mfma32<IN>(f.x[q >> 1], f.w[q & 1], acc[q >> 1][q & 1]);
   };
@@ -212,7 +227,7 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_dma(MmArgs a) {
   // tile in flight (wait for everything).
   auto step = [&](int t, auto dma, auto all) {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) mma_one(f0, q);
+    for (int q = 0; q < 2 * J; ++q) mma_one(f0, q);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (decltype(all)::value) dma_wait_barrier<0>();
     else dma_wait_barrier<2 * kMmL>();
@@ -220,9 +235,9 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_dma(MmArgs a) {
     if constexpr (decltype(dma)::value) issue(t + kMmNS - 1, (t + kMmNS - 1) % kMmNS);
     const int next = (t + 1) % kMmNS;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < 2 * J; ++q) {
       mma_one(f1, q);
-      if (q < 6) read_one(next, 0, f0, q);
+      if (q < J + 2) read_one(next, 0, f0, q);
       __builtin_amdgcn_sched_barrier(0);
     }
     read(next, 1, f1);
@@ -244,13 +259,13 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_dma(MmArgs a) {
     if (t + 2 < nk) step(t++, no{}, no{});                  // tile t + 2 still in flight
     if (t + 1 < nk) step(t++, no{}, yes{});
 #pragma unroll
-    for (int q = 0; q < 8; ++q) mma_one(f0, q);
+    for (int q = 0; q < 2 * J; ++q) mma_one(f0, q);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) mma_one(f1, q);
+    for (int q = 0; q < 2 * J; ++q) mma_one(f1, q);
   }
 
   // Epilogue: C[m][n], n = 32 i + r32, m = 32 j + 8 (v / 4) + 4 h + v % 4;
-  // 32-bit offsets from the wave's corner (128 rows of N elements). A split
+  // 32-bit offsets from the wave's corner (T/2 rows of N elements). A split
   // range stores its raw 4-byte sums to its plane of the partial buffer.
   typedef typename std::conditional<IN == kInI8, int, float>::type PartT;
   constexpr int ES_OUT = (OUT == kOutF16 && !SPLIT) ? 2 : 4;
@@ -258,7 +273,7 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_dma(MmArgs a) {
                             ((static_cast<int64_t>(split) * a.M + mw) * a.N + nw) * ES_OUT
                       : static_cast<uint8_t*>(a.c) + (static_cast<int64_t>(mw) * a.N + nw) * ES_OUT;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < J; ++j) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int nl = 32 * i + r32;
@@ -443,29 +458,41 @@ struct MmPlan {
   bool u8;
   int64_t kb, ldk;     // row bytes, padded row bytes
   bool stage_a, stage_b;
+  int tile;            // output tile edge (256 or 128)
   int splits;          // k-ranges (1: no split-K)
   size_t a_off, b_off, rs_off, cs_off, part_off, bytes;
 };
 
-// k-ranges for C = A . B when the 256 x 256 tiles alone leave CUs idle: the
-// count with the lowest modelled time, one range included: 1.0 us per
-// 64-byte k-step of the longest range (k_mm_dma at 8192^3, int8 and fp16),
-// plus, when split, 0.09 us per 256 KiB of 4-byte partial sums written and
-// re-read and 5 us for the reduce pass. At most 16 ranges, at most one
-// workgroup per CU, at least four k-steps per range.
-int mm_splits(int64_t M, int64_t N, int64_t nk) {
-  const int64_t tiles = cdiv(M, 256) * cdiv(N, 256);
-  const int64_t max_sp = std::min<int64_t>({16, device_cus() / tiles, nk / 4});
-  int best = 1;
-  int64_t best_cost = 100 * nk;
-  for (int64_t sp = 2; sp <= max_sp; ++sp) {
-    const int64_t cost = 100 * cdiv(nk, sp) + 9 * cdiv(sp * M * N * 4, 262144) + 500;
-    if (cost < best_cost) {
-      best = static_cast<int>(sp);
-      best_cost = cost;
+// Tile and k-ranges for C = A . B: the pair with the lowest modelled time
+// (0.01 us units, fitted on MI355X at 512^3 .. 8192^3 and M = 16 .. 2048 x
+// N = 4096 / 11008, int8 and fp16). Per 64-byte k-step of the longest range
+// and per round of workgroups over the CUs: 1.0 us for a 256 x 256 tile,
+// 0.4 us for a 128 x 128 tile (its workgroups are a quarter of the work but
+// less efficient: 1024^3 int8 12.4 us against 21.2, 2048^3 fp16 32.5 against
+// 59.4; 8192^3 stays on 256 tiles). A split of K into 2-16 ranges adds
+// 0.09 us per 256 KiB of 4-byte partial sums written and re-read and 5 us
+// for the reduce pass; ranges keep at least four k-steps, and the split
+// workgroups must fit one round (256 tiles) or two (128 tiles, two per CU).
+void mm_choose(int64_t M, int64_t N, int64_t nk, int& tile, int& splits) {
+  const int64_t cus = device_cus();
+  tile = 256;
+  splits = 1;
+  int64_t best = -1;
+  for (int t : {256, 128}) {
+    const int64_t tiles = cdiv(M, t) * cdiv(N, t);
+    const int64_t step = t == 256 ? 100 : 40;
+    const int64_t max_wg = t == 256 ? cus : 2 * cus;
+    for (int64_t sp = 1; sp <= 16; ++sp) {
+      if (sp > 1 && (tiles * sp > max_wg || nk / sp < 4)) break;
+      int64_t cost = step * cdiv(nk, sp) * cdiv(tiles * sp, cus);
+      if (sp > 1) cost += 9 * cdiv(sp * M * N * 4, 262144) + 500;
+      if (best < 0 || cost < best) {
+        best = cost;
+        tile = t;
+        splits = static_cast<int>(sp);
+      }
     }
   }
-  return best;
 }
 
 size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
@@ -492,23 +519,33 @@ bool mm_plan(int64_t M, int64_t N, int64_t K, int in_dtype, int b_layout, MmPlan
   if (p.u8) off = align256(off + static_cast<size_t>(M) * 4);
   p.cs_off = off;
   if (p.u8) off = align256(off + static_cast<size_t>(N) * 4);
-  p.splits = (M > 0 && N > 0 && K > 0) ? mm_splits(M, N, p.ldk / 64) : 1;
+  p.tile = 256;
+  p.splits = 1;
+  if (M > 0 && N > 0 && K > 0) mm_choose(M, N, p.ldk / 64, p.tile, p.splits);
   p.part_off = off;
   if (p.splits > 1) off = align256(off + static_cast<size_t>(p.splits) * M * N * 4);
   p.bytes = off;
   return true;
 }
 
-template <int IN, int OUT>
-void launch_mm(const MmArgs& a, hipStream_t s) {
+template <int IN, int OUT, int T>
+void launch_mm_t(const MmArgs& a, hipStream_t s) {
   const unsigned tiles = static_cast<unsigned>(a.tiles_m * a.tiles_n);
+  const dim3 b(MmGeom<T>::kThreads);
   if (a.splits > 1) {
-    k_mm_dma<IN, OUT, true><<<dim3(tiles * a.splits), dim3(kMmThreads), 0, s>>>(a);
+    k_mm_dma<IN, OUT, true, T><<<dim3(tiles * a.splits), b, 0, s>>>(a);
     const int64_t mn = static_cast<int64_t>(a.M) * a.N;
     k_mm_reduce<IN, OUT><<<dim3(static_cast<unsigned>(cdiv(mn, kBlock))), dim3(kBlock), 0, s>>>(a);
   } else {
-    k_mm_dma<IN, OUT, false><<<dim3(tiles), dim3(kMmThreads), 0, s>>>(a);
+    k_mm_dma<IN, OUT, false, T><<<dim3(tiles), b, 0, s>>>(a);
   }
+}
+
+// a.tiles_m / a.tiles_n must be counted in tiles of `tile`.
+template <int IN, int OUT>
+void launch_mm(const MmArgs& a, int tile, hipStream_t s) {
+  if (tile == 128) launch_mm_t<IN, OUT, 128>(a, s);
+  else launch_mm_t<IN, OUT, 256>(a, s);
 }
 
 unsigned grid_for(int64_t work, int64_t per_block) {
@@ -583,8 +620,8 @@ extern "C" int cbq_mm(const void* A, const void* B, int in_dtype, int b_layout, 
   a.ldk = static_cast<int>(p.ldk);
   a.nk = static_cast<int>(p.ldk / 64);
   a.K = static_cast<int>(K);
-  a.tiles_m = static_cast<int>(cdiv(M, 256));
-  a.tiles_n = static_cast<int>(cdiv(N, 256));
+  a.tiles_m = static_cast<int>(cdiv(M, p.tile));
+  a.tiles_n = static_cast<int>(cdiv(N, p.tile));
   a.part = nullptr;
   a.splits = 1;
   a.split_steps = a.nk;
@@ -623,13 +660,13 @@ extern "C" int cbq_mm(const void* A, const void* B, int in_dtype, int b_layout, 
     a.col_sum = cs;
   }
   if (p.in == kInI8) {
-    launch_mm<kInI8, kOutI32>(a, s);
+    launch_mm<kInI8, kOutI32>(a, p.tile, s);
     if (a.col_sum)
       k_u8_fix<<<grid_for(M * (N / 4), kBlock), kBlock, 0, s>>>(static_cast<int*>(C), M, N,
                                                                a.row_sum, a.col_sum, K);
   }
-  else if (p.in == kInF16 && out_dtype == CBQ_F16) launch_mm<kInF16, kOutF16>(a, s);
-  else if (p.in == kInF16) launch_mm<kInF16, kOutF32>(a, s);
-  else launch_mm<kInBF16, kOutF32>(a, s);
+  else if (p.in == kInF16 && out_dtype == CBQ_F16) launch_mm<kInF16, kOutF16>(a, p.tile, s);
+  else if (p.in == kInF16) launch_mm<kInF16, kOutF32>(a, p.tile, s);
+  else launch_mm<kInBF16, kOutF32>(a, p.tile, s);
   return launch_status(what);
 }

@@ -8,7 +8,8 @@ bf16 within the fp32-accumulation error bound
 2^-11 |ref| + 2^-24, for fp16 outputs), with ref the oracle's double sum.
 Covers both storages of B ([K, N] and the [N, K] weight layout read in
 place), K that is not a multiple of 64 bytes (padded staging), partial
-256 x 256 tiles, and the reference's argument errors.
+tiles, both tile sizes (256 and 128) with and without a K split, and the
+reference's argument errors.
 """
 from __future__ import annotations
 
@@ -164,6 +165,40 @@ def test_mm_empty_contraction(dt, out):
     C = H().wmma_gemm(torch.empty(0, 16, dtype=dt, device=DEV),
                       torch.zeros(16, 48, dtype=dt, device=DEV), out)
     assert tuple(C.shape) == (0, 48)
+
+
+@pytest.mark.parametrize("M,N,K,dt,path", [
+    (4096, 4096, 128, torch.int8, "256 tiles"),
+    (256, 8192, 16384, torch.int8, "256 tiles, K in 8 ranges"),
+    (1024, 1024, 1024, torch.int8, "128 tiles"),
+    (16, 11008, 4096, torch.int8, "128 tiles, K in 5 ranges"),
+    (64, 1024, 4096, torch.uint8, "128 tiles, K in 16 ranges"),
+    (2048, 4096, 4096, torch.float16, "256 tiles, K in 2 ranges"),
+    (1024, 4096, 4096, torch.float16, "128 tiles"),
+])
+def test_mm_tile_and_split_paths(M, N, K, dt, path):
+    """Each tile size with and without a K split (the host's time model picks
+    them per shape), B in the weight layout; sampled rows against an exact
+    numpy product: int64 reduced modulo 2^32 for integers, the fp32
+    accumulation bound for fp16."""
+    print(f"[mm] {dt} M={M} N={N} K={K} ({path})", flush=True)
+    if dt == torch.float16:
+        g = torch.Generator().manual_seed(M + N)
+        A, W = torch.randn(M, K, generator=g).half(), torch.randn(N, K, generator=g).half()
+    else:
+        A, W = rand_int((M, K), dt, seed=M + K), rand_int((N, K), dt, seed=N + K)
+    C = H().wmma_gemm(A.to(DEV), W.to(DEV).t())
+    rows = np.unique(np.array([0, 1, M // 3, M // 2, M - 1]))
+    if dt == torch.float16:
+        a64 = A.numpy()[rows].astype(np.float64)
+        b64 = W.numpy().astype(np.float64).T
+        ref = a64 @ b64
+        err = np.abs(np_of(C)[rows].astype(np.float64) - ref)
+        assert (err <= float_bound(a64, b64, K, False, ref)).all()
+    else:
+        ref = (np_of(A)[rows].astype(np.int64) @ np_of(W).astype(np.int64).T) % (1 << 32)
+        got = np_of(C)[rows].astype(np.int64) % (1 << 32)
+        np.testing.assert_array_equal(got, ref)
 
 
 def test_mm_repeated_calls_share_workspace():
