@@ -104,18 +104,23 @@ struct GemmArgs {
   const int64_t* oc;        // [n_out]
   const uint16_t* w_out;    // [N, n_out]
   uint16_t* y;              // [M, N]
-  float* part;              // split-K partial tiles (k_gemm_dma<ACT, true>)
+  float* part;              // split-K partial tiles (k_gemm_dma<ACT, true, TM>)
   int M, N, K, n_out;
   int tiles_m, tiles_n;
   int splits, split_steps;  // split-K: number of k-ranges, 64-k steps per range
+  int full_tiles;           // split-K: tiles [0, full_tiles) run whole, the rest split
 };
 
-// Workgroup -> (tile m, tile n); see the file comment.
-__device__ __forceinline__ void decode_tile(int b, const GemmArgs& a, int& tm, int& tn) {
-  const int total = a.tiles_m * a.tiles_n;
-  const int per = total >> 3;
-  if (b < per * 8) b = (b & 7) * per + (b >> 3);
-  const int t = b;
+// Workgroup b of n goes to XCD b % 8; renumbered so that each XCD takes a
+// contiguous run of [0, n) (neighbouring tiles share operand rows in its L2).
+__device__ __forceinline__ int xcd_renumber(int b, int n) {
+  const int per = n >> 3;
+  return b < per * 8 ? (b & 7) * per + (b >> 3) : b;
+}
+
+// Linear tile t -> (tile m, tile n): groups of 8 tile rows, column-major
+// inside a group.
+__device__ __forceinline__ void group_tile(int t, const GemmArgs& a, int& tm, int& tn) {
   constexpr int G = 8;
   const int group = t / (G * a.tiles_n);
   const int first_m = group * G;
@@ -123,6 +128,11 @@ __device__ __forceinline__ void decode_tile(int b, const GemmArgs& a, int& tm, i
   const int r = t % (G * a.tiles_n);
   tm = first_m + r % gsize;
   tn = r / gsize;
+}
+
+// Workgroup -> (tile m, tile n); see the file comment.
+__device__ __forceinline__ void decode_tile(int b, const GemmArgs& a, int& tm, int& tn) {
+  group_tile(xcd_renumber(b, a.tiles_m * a.tiles_n), a, tm, tn);
 }
 
 // Outlier side-GEMM for 4 consecutive outputs y[m, nb .. nb+3]:
@@ -367,41 +377,51 @@ __device__ __forceinline__ f16x mfma32x32x16(const u32x4& a, const u32x4& b, f16
 }
 
 constexpr int kDmaThreads = 512;   // 8 waves, two per SIMD
-constexpr int kDmaTM = 4, kDmaTN = 2;   // 32 x 32 tiles per wave: x (m) x weight (n)
+constexpr int kDmaTN = 2;          // 32-row weight tiles per wave
 
-template <int ACT, bool SPLIT>
+// TM: 32-row x tiles per wave; the workgroup tile is 64 TM x 256 (TM = 4:
+// 256 x 256, TM = 2: 128 x 256 for small M and tile counts that leave the
+// last wave of workgroups short).
+// SPLIT: workgroups [0, full_tiles) take whole tiles 0 .. full_tiles - 1;
+// the others split the remaining tiles over `splits` k-ranges, workgroup
+// full_tiles + b covering tail tile b % rest of k-range b / rest (after the
+// XCD renumbering, so the workgroups of one XCD share a k-range of x).
+template <int ACT, bool SPLIT, int TM>
 __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
-  constexpr int BM = 256, BN = 256, BK = 64, NS = 3;
-  constexpr int XB = BM * BK * 2;          // x stage bytes (32 KiB)
+  constexpr int BM = 64 * TM, BN = 256, BK = 64, NS = 3;
+  constexpr int XB = BM * BK * 2;          // x stage bytes (32 / 16 KiB)
   constexpr int WB = BN * BK;              // weight stage bytes (16 KiB)
   constexpr int SB = XB + WB;
-  constexpr int XL = XB / (kDmaThreads * 16);   // DMA instructions per thread: 4
+  constexpr int XL = XB / (kDmaThreads * 16);   // DMA instructions per thread: TM
   constexpr int WL = WB / (kDmaThreads * 16);   // 2
-  constexpr int TM = kDmaTM, TN = kDmaTN;
+  constexpr int TN = kDmaTN;
+  static_assert(TM == 2 || TM == 4, "x tile of 128 or 256 rows");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * SB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 1, wn = wave >> 1;   // 128 x rows, 64 weight rows
-  // Split-K: workgroup b covers tile b % tiles of k-range b / tiles (after
-  // the XCD renumbering, so the workgroups of one XCD share a k-range of x).
-  int tm, tn, split = 0;
+  const int wm = wave & 1, wn = wave >> 1;   // 32 TM x rows, 64 weight rows
+  int tm, tn, split = 0, ptile = 0;
+  bool partial = false;
   if constexpr (SPLIT) {
-    const int tiles = a.tiles_m * a.tiles_n;
-    const int total = tiles * a.splits;
-    const int per = total >> 3;
-    int b = blockIdx.x;
-    if (b < per * 8) b = (b & 7) * per + (b >> 3);
-    split = b / tiles;
-    tm = (b % tiles) % a.tiles_m;
-    tn = (b % tiles) / a.tiles_m;
+    const int b = blockIdx.x;
+    if (b < a.full_tiles) {
+      group_tile(xcd_renumber(b, a.full_tiles), a, tm, tn);
+    } else {
+      partial = true;
+      const int rest = a.tiles_m * a.tiles_n - a.full_tiles;
+      const int r = xcd_renumber(b - a.full_tiles, rest * a.splits);
+      split = r / rest;
+      ptile = r % rest;
+      group_tile(a.full_tiles + ptile, a, tm, tn);
+    }
   } else {
     decode_tile(blockIdx.x, a, tm, tn);
   }
   const int m0 = tm * BM, n0 = tn * BN;
-  const int kb = SPLIT ? split * a.split_steps : 0;          // first 64-k step
-  const int nk = SPLIT ? min(a.split_steps, a.K / BK - kb) : a.K / BK;
+  const int kb = partial ? split * a.split_steps : 0;          // first 64-k step
+  const int nk = partial ? min(a.split_steps, a.K / BK - kb) : a.K / BK;
   const uint32_t sbase = __builtin_amdgcn_readfirstlane(lds_addr(smem));
 
   // Per-lane DMA source offsets (bytes from the k0 column of the tile). x
@@ -445,7 +465,7 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
   for (int e = 0; e < 2; ++e) {
 #pragma unroll
     for (int q = 0; q < 2; ++q)
-      xr[e][q] = (wm * 128 + r32) * 128 + (((4 * h + 2 * e + q) ^ ((r32 >> 1) & 7)) << 4);
+      xr[e][q] = (wm * TM * 32 + r32) * 128 + (((4 * h + 2 * e + q) ^ ((r32 >> 1) & 7)) << 4);
     wr[e] = XB + (wn * 64 + r32) * 64 + (((2 * h + e) ^ ((r32 >> 2) & 3)) << 4);
   }
 
@@ -529,7 +549,7 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
     const int stage_cur = t % NS, stage_next = (t + 1) % NS;
     half(fr[1], &fr[0], [&](int i, int p) {
       if constexpr (decltype(dma)::value) {
-        if (i == 0 && p < 3) {
+        if (i == 0 && 2 * p < XL + WL) {
           issue_one(t + NS, stage_cur, 2 * p);
           issue_one(t + NS, stage_cur, 2 * p + 1);
         }
@@ -561,13 +581,13 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
     half(fr[1], nullptr, [&](int, int) {});
   }
 
-  const int mw = m0 + wm * 128, nw = n0 + wn * 64;
-  if constexpr (SPLIT) {
-    // Partial tile in lane order: f4 (split, tile, wave, i, j, q, lane), one
-    // contiguous 1 KiB store per (i, j, q); k_splitk_reduce finishes it.
+  const int mw = m0 + wm * TM * 32, nw = n0 + wn * 64;
+  if (SPLIT && partial) {
+    // Partial tile in lane order: f4 (split, tail tile, wave, i, j, q, lane),
+    // one contiguous 1 KiB store per (i, j, q); k_splitk_reduce finishes it.
+    const int rest = a.tiles_m * a.tiles_n - a.full_tiles;
     f4* dst = reinterpret_cast<f4*>(a.part) +
-              ((static_cast<int64_t>(split) * a.tiles_m * a.tiles_n + tn * a.tiles_m + tm) * 8 + wave) *
-                  (TN * TM * 4 * 64) + lane;
+              ((static_cast<int64_t>(split) * rest + ptile) * 8 + wave) * (TN * TM * 4 * 64) + lane;
 #pragma unroll
     for (int i = 0; i < TN; ++i)
 #pragma unroll
@@ -581,13 +601,13 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
   // Epilogue. Accumulator values 4q .. 4q+3 of tile (i, j) are the wave's
   // outputs (m, n .. n+3) with m = 32 j + r32, n = 32 i + 8 q + 4 h. Each is
   // finished in fp32 (scale, outlier sum, bias, in that order), rounded once,
-  // and written to an LDS copy of the wave's 128 x 64 output tile; the tile
-  // is then stored with 16-byte row-contiguous stores. The per-lane scales
-  // are loaded once, before any output store.
+  // and written to an LDS copy of the wave's 32 TM x 64 output tile; the
+  // tile is then stored with 16-byte row-contiguous stores. The per-lane
+  // scales are loaded once, before any output store.
   constexpr int EPS = 72;    // LDS row stride of the output tile (halfs)
-  static_assert(8 * 128 * EPS * 2 <= NS * SB, "epilogue tile fits in LDS");
+  static_assert(8 * TM * 32 * EPS * 2 <= NS * SB, "epilogue tile fits in LDS");
   dma_wait_barrier<0>();     // every wave is done with the operand stages
-  uint16_t* ep = reinterpret_cast<uint16_t*>(smem) + wave * (128 * EPS);
+  uint16_t* ep = reinterpret_cast<uint16_t*>(smem) + wave * (TM * 32 * EPS);
 #pragma unroll
   for (int i = 0; i < TN; ++i) {
 #pragma unroll
@@ -619,7 +639,7 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
   // Row-contiguous stores: 8 lanes cover one 64-wide row (8 outputs each).
   const bool vec16 = (a.N % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
 #pragma unroll 4
-  for (int u = 0; u < 16; ++u) {
+  for (int u = 0; u < 4 * TM; ++u) {
     const int row = u * 8 + (lane >> 3), c8 = (lane & 7) * 8;
     const int m = mw + row, n = nw + c8;
     if (m >= a.M || n >= a.N) continue;
@@ -636,53 +656,67 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
   }
 }
 
-template <int ACT>
+template <int ACT, int TM>
 void launch_gemm_dma(GemmArgs a, hipStream_t s) {
-  a.tiles_m = static_cast<int>(cdiv(a.M, 256));
+  a.tiles_m = static_cast<int>(cdiv(a.M, 64 * TM));
   a.tiles_n = static_cast<int>(cdiv(a.N, 256));
   const unsigned grid = static_cast<unsigned>(a.tiles_m) * a.tiles_n;
-  k_gemm_dma<ACT, false><<<dim3(grid), dim3(kDmaThreads), 0, s>>>(a);
+  k_gemm_dma<ACT, false, TM><<<dim3(grid), dim3(kDmaThreads), 0, s>>>(a);
 }
 
-// Split-K finish: one thread per partial f4 (4 outputs y[m, n .. n+3]); sums
-// the splits in order (deterministic), then scale, outliers, bias and one
-// rounding, as in the tile kernels' epilogue. Partial index bits, low to
-// high: lane (6), q (2), j (2), i (1), wave (3), tile.
-template <int ACT>
+// Split-K finish: one thread per partial f4 (4 outputs y[m, n .. n+3]) of a
+// tail tile; sums the splits in order (deterministic), then scale, outliers,
+// bias and one rounding, as in the tile kernels' epilogue. Partial index
+// bits, low to high: lane (6), q (2), j (log2 TM), i (1), wave (3), tail tile.
+template <int ACT, int TM>
 __global__ __launch_bounds__(kBlock) void k_splitk_reduce(GemmArgs a) {
-  const int64_t per_split = static_cast<int64_t>(a.tiles_m) * a.tiles_n * 16384;
+  constexpr int LJ = TM == 4 ? 2 : 1;
+  constexpr int kTileF4 = 8 * kDmaTN * TM * 4 * 64;
+  const int rest = a.tiles_m * a.tiles_n - a.full_tiles;
+  const int64_t per_split = static_cast<int64_t>(rest) * kTileF4;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
   if (idx >= per_split) return;
   const f4* src = reinterpret_cast<const f4*>(a.part) + idx;
   f4 sum = src[0];
   for (int sp = 1; sp < a.splits; ++sp) sum += src[sp * per_split];
   const int lane = static_cast<int>(idx & 63), q = static_cast<int>((idx >> 6) & 3);
-  const int j = static_cast<int>((idx >> 8) & 3), i = static_cast<int>((idx >> 10) & 1);
-  const int wave = static_cast<int>((idx >> 11) & 7);
-  const int tile = static_cast<int>(idx >> 14);
-  const int tm = tile % a.tiles_m, tn = tile / a.tiles_m;
-  const int m = tm * 256 + (wave & 1) * 128 + j * 32 + (lane & 31);
+  const int j = static_cast<int>((idx >> 8) & (TM - 1)), i = static_cast<int>((idx >> (8 + LJ)) & 1);
+  const int wave = static_cast<int>((idx >> (9 + LJ)) & 7);
+  int tm, tn;
+  group_tile(a.full_tiles + static_cast<int>(idx / kTileF4), a, tm, tn);
+  const int m = tm * 64 * TM + (wave & 1) * 32 * TM + j * 32 + (lane & 31);
   const int nb = tn * 256 + (wave >> 1) * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
   if (m >= a.M || nb >= a.N) return;
   store_quad<ACT>(a, sum, m, nb, (a.N % 4) == 0);
 }
 
-// Bytes of split-K partials for `splits` k-ranges.
-int64_t splitk_bytes(int64_t M, int64_t N, int splits) {
-  return cdiv(M, 256) * cdiv(N, 256) * splits * 16384 * 16;
+// Launch plan of the k_gemm_dma path: x tile of 64 tm rows; tiles
+// [0, full) whole, the rest split over `splits` k-ranges (splits == 1:
+// every tile whole, no partials).
+struct DmaPlan {
+  int tm, full, splits;
+};
+
+// Bytes of split-K partials of a plan: one fp32 tile per tail tile and range.
+int64_t splitk_bytes(int64_t M, int64_t N, const DmaPlan& p) {
+  if (p.splits <= 1) return 0;
+  const int64_t tiles = cdiv(M, 64 * p.tm) * cdiv(N, 256);
+  return (tiles - p.full) * p.splits * (p.tm * 64) * 256 * 4;
 }
 
-template <int ACT>
-void launch_gemm_dma_splitk(GemmArgs a, int splits, hipStream_t s) {
-  a.tiles_m = static_cast<int>(cdiv(a.M, 256));
+template <int ACT, int TM>
+void launch_gemm_dma_splitk(GemmArgs a, const DmaPlan& p, hipStream_t s) {
+  a.tiles_m = static_cast<int>(cdiv(a.M, 64 * TM));
   a.tiles_n = static_cast<int>(cdiv(a.N, 256));
+  a.full_tiles = p.full;
   const int nk = a.K / 64;
-  a.split_steps = static_cast<int>(cdiv(nk, splits));
+  a.split_steps = static_cast<int>(cdiv(nk, p.splits));
   a.splits = static_cast<int>(cdiv(nk, a.split_steps));   // no empty ranges
-  const unsigned grid = static_cast<unsigned>(a.tiles_m) * a.tiles_n * a.splits;
-  k_gemm_dma<ACT, true><<<dim3(grid), dim3(kDmaThreads), 0, s>>>(a);
-  const int64_t n4 = static_cast<int64_t>(a.tiles_m) * a.tiles_n * 16384;
-  k_splitk_reduce<ACT><<<dim3(static_cast<unsigned>(cdiv(n4, kBlock))), dim3(kBlock), 0, s>>>(a);
+  const int rest = a.tiles_m * a.tiles_n - a.full_tiles;
+  const unsigned grid = static_cast<unsigned>(a.full_tiles + rest * a.splits);
+  k_gemm_dma<ACT, true, TM><<<dim3(grid), dim3(kDmaThreads), 0, s>>>(a);
+  const int64_t n4 = static_cast<int64_t>(rest) * 8 * kDmaTN * TM * 4 * 64;
+  k_splitk_reduce<ACT, TM><<<dim3(static_cast<unsigned>(cdiv(n4, kBlock))), dim3(kBlock), 0, s>>>(a);
 }
 
 // Small M (M <= 16 * TM): weight streaming. A workgroup owns 16 * TN weight
@@ -1264,14 +1298,16 @@ __global__ __launch_bounds__(kBlock) void k_general_reduce(GenArgs a) {
 //                 workgroups; else k_skinny (TM = 1)
 //   M <= 64       k_stream<2 or 4> under the same size rules (3 row tiles
 //                 per workgroup); else k_skinny, TM = ceil(M / 16)
-//   M > 64        k_gemm_dma split over K (2-16 k-ranges, partial tiles in
-//                 the workspace, k_splitk_reduce) when the 256 x 256 tiles
-//                 alone leave CUs idle and the time model of splitk_count
-//                 prefers it, and the caller's workspace holds the partials;
-//   64 < M < 1024 else k_gemm_dma from M = 384 on; else k_gemm 128 x 64 x 64,
+//   M > 64        k_gemm_dma (K % 64 == 0 and 32-bit operand offsets) with
+//                 the x tile (256 or 128 rows) and split-K plan of dma_plan:
+//                 the last, short wave of tiles split over K (2-16 k-ranges,
+//                 partial tiles in the workspace, k_splitk_reduce) when the
+//                 time model prefers it and the caller's workspace holds the
+//                 partials;
+//   64 < M < 384  else (no workspace, or no k_gemm_dma) k_gemm 128 x 64 x 64,
 //                 2 x 2 waves
-//   M >= 1024     else k_gemm_dma (K % 64 == 0 and 32-bit operand offsets),
-//                 else k_gemm 256 x 256 x 64, 4 x 2 waves
+//   M >= 384      else k_gemm_dma without a split; else k_gemm 256 x 256 x
+//                 64, 4 x 2 waves
 enum Kind { kSkinny1, kSkinny2, kSkinny4, kTileMid, kTileLarge, kTileDma, kStream1, kStream2,
             kStream4, kTileDmaSplit };
 
@@ -1288,34 +1324,57 @@ bool dma_ok(int64_t M, int64_t N, int64_t K) {
   return K % 64 == 0 && M * K * 2 < kLim && N * K < kLim;
 }
 
-// k-ranges for the split-K tile path (0: not used). The workgroups
-// (tiles x ranges) must fit one wave of CUs, and each range keeps at least
-// four 64-k steps. The count with the lowest modelled time wins, one range
-// (the plain tile kernel) included: 1.28 us per 64-k step of the longest
-// range, plus, when split, 0.09 us per 256 KiB partial tile written and
-// re-read and 5 us for the reduce pass (fitted on MI355X at M = 128..768,
-// N = 4096 / 11008, K = 4096 / 11008; e.g. 16 tiles at K = 11008: 4 ranges
-// 65.7 us, 8: 44.3, 12: 40.8, 16: 41.2; 43 tiles at K = 4096: 4 ranges
-// 42.1 us, 6 (more workgroups than CUs): 57.1). Large M splits only while
-// the tiles alone leave CUs idle (e.g. M = 1024, N = 4096: 64 tiles).
-int splitk_count(int64_t M, int64_t N, int64_t K) {
-  if (M <= 64 || !dma_ok(M, N, K)) return 0;
-  const int64_t tiles = cdiv(M, 256) * cdiv(N, 256);
-  const int64_t nk = K / 64;
-  const int64_t max_sp = std::min<int64_t>({16, device_cus() / tiles, nk / 4});
-  int best = 1;
-  int64_t best_cost = 128 * nk;
-  for (int64_t sp = 2; sp <= max_sp; ++sp) {
-    const int64_t cost = 128 * cdiv(nk, sp) + 9 * tiles * sp + 500;
-    if (cost < best_cost) {
-      best = static_cast<int>(sp);
-      best_cost = cost;
-    }
-  }
-  return best >= 2 ? best : 0;
+// Plan of the k_gemm_dma path with the lowest modelled time (0.01 us): the
+// 64-k steps of the longest chain of workgroups on one CU times the cost of
+// a step, which grows with the share of CUs busy (clock and bandwidth under
+// load): 1.30 + 0.55 occ us for 256 x 256 tiles, 0.78 + 0.27 occ us for
+// 128 x 256; plus, when split, 5 us for the reduce pass and 0.12 us per
+// 256 KiB of partial tiles written and re-read. With `rest` tiles in the
+// last, short wave, a split runs the full waves whole and the rest over sp
+// k-ranges (rest x sp workgroups fit one wave of CUs, each range keeps at
+// least four 64-k steps). Fitted on MI355X over M = 96..4096 at N = 11008,
+// K = 4096 and N = 4096, K = 11008 (fp16, e.g. M = 1536, N = 11008: whole
+// 256 x 256 tiles 208 us, the 2 tail tiles over 16 ranges 141 us; M = 128:
+// 256 x 256 over 5 ranges 46.8 us, 128 x 256 over 5 ranges 30.8 us).
+int64_t dma_step_cost(int tm, int64_t wgs, int64_t cus) {
+  const int64_t busy = std::min(wgs, cus);
+  return tm == 4 ? 130 + 55 * busy / cus : 78 + 27 * busy / cus;
 }
 
-Kind choose(int64_t M, int64_t N, int64_t K, size_t ws_bytes) {
+DmaPlan dma_plan(int64_t M, int64_t N, int64_t K, bool allow_split) {
+  const int64_t cus = device_cus(), nk = K / 64;
+  DmaPlan best{4, 0, 1};
+  int64_t best_cost = INT64_MAX;
+  for (const int tm : {4, 2}) {
+    const int64_t tiles = cdiv(M, 64 * tm) * cdiv(N, 256);
+    const int64_t rounds = tiles / cus, rest = tiles % cus;
+    const int64_t whole = nk * cdiv(tiles, cus) * dma_step_cost(tm, tiles, cus);
+    if (whole < best_cost) {
+      best = {tm, static_cast<int>(tiles), 1};
+      best_cost = whole;
+    }
+    if (!allow_split || rest == 0) continue;
+    const int64_t max_sp = std::min<int64_t>({16, cus / rest, nk / 4});
+    for (int64_t sp = 2; sp <= max_sp; ++sp) {
+      const int64_t wgs = rounds * cus + rest * sp;
+      const int64_t cost = (rounds * nk + cdiv(nk, sp)) * dma_step_cost(tm, wgs, cus) + 500 +
+                           3 * tm * rest * sp;
+      if (cost < best_cost) {
+        best = {tm, static_cast<int>(rounds * cus), static_cast<int>(sp)};
+        best_cost = cost;
+      }
+    }
+  }
+  return best;
+}
+
+// The split plan when it applies (M > 64, k_gemm_dma usable), else none.
+DmaPlan split_plan(int64_t M, int64_t N, int64_t K) {
+  if (M <= 64 || !dma_ok(M, N, K)) return DmaPlan{4, 0, 1};
+  return dma_plan(M, N, K, true);
+}
+
+Kind choose(int64_t M, int64_t N, int64_t K, size_t ws_bytes, DmaPlan& plan) {
   const int64_t cus = device_cus();
   const bool stream = stream_ok(M, N, K);
   if (M <= 16)
@@ -1323,11 +1382,14 @@ Kind choose(int64_t M, int64_t N, int64_t K, size_t ws_bytes) {
   const bool tiles_fit = cdiv(N, 16) <= kStreamMaxTiles * cus;
   if (M <= 32) return (stream && tiles_fit) ? kStream2 : kSkinny2;
   if (M <= 64) return (stream && tiles_fit) ? kStream4 : kSkinny4;
-  const int sp = splitk_count(M, N, K);
-  if (sp && ws_bytes >= static_cast<size_t>(CBQ_WS_CTRL_BYTES + splitk_bytes(M, N, sp)))
+  if (!dma_ok(M, N, K)) return M < 1024 ? kTileMid : kTileLarge;
+  plan = dma_plan(M, N, K, true);
+  if (plan.splits > 1 &&
+      ws_bytes >= static_cast<size_t>(CBQ_WS_CTRL_BYTES + splitk_bytes(M, N, plan)))
     return kTileDmaSplit;
-  if (M < 1024) return (M >= 384 && dma_ok(M, N, K)) ? kTileDma : kTileMid;
-  return dma_ok(M, N, K) ? kTileDma : kTileLarge;
+  if (M < 384) return kTileMid;
+  plan = dma_plan(M, N, K, false);
+  return kTileDma;
 }
 
 template <int ACT, int BM, int BN, int BK, int WGM, int WGN, int PD>
@@ -1339,7 +1401,7 @@ void launch_gemm(GemmArgs a, hipStream_t s) {
 }
 
 template <int ACT>
-void launch_kind(Kind k, const GemmArgs& a, hipStream_t s) {
+void launch_kind(Kind k, const GemmArgs& a, const DmaPlan& p, hipStream_t s) {
   switch (k) {
     case kSkinny1: launch_skinny<ACT, 1, 1, 4>(a, s); break;
     case kSkinny2: launch_skinny<ACT, 2, 1, 4>(a, s); break;
@@ -1348,8 +1410,14 @@ void launch_kind(Kind k, const GemmArgs& a, hipStream_t s) {
     case kStream2: launch_stream<ACT, 2>(a, s); break;
     case kStream4: launch_stream<ACT, 4>(a, s); break;
     case kTileMid: launch_gemm<ACT, 128, 64, 64, 2, 2, 1>(a, s); break;
-    case kTileDma: launch_gemm_dma<ACT>(a, s); break;
-    case kTileDmaSplit: launch_gemm_dma_splitk<ACT>(a, a.splits, s); break;
+    case kTileDma:
+      if (p.tm == 2) launch_gemm_dma<ACT, 2>(a, s);
+      else launch_gemm_dma<ACT, 4>(a, s);
+      break;
+    case kTileDmaSplit:
+      if (p.tm == 2) launch_gemm_dma_splitk<ACT, 2>(a, p, s);
+      else launch_gemm_dma_splitk<ACT, 4>(a, p, s);
+      break;
     default: launch_gemm<ACT, 256, 256, 64, 4, 2, 1>(a, s); break;
   }
 }
@@ -1440,12 +1508,11 @@ int w8a16_t(const void* x, const int8_t* wq, const void* scales, const void* bia
   a.N = static_cast<int>(N);
   a.K = static_cast<int>(K);
   a.n_out = static_cast<int>(n_out);
-  const Kind kind = choose(M, N, K, ws ? ws_bytes : 0);
-  if (kind == kTileDmaSplit) {
+  DmaPlan plan{4, 0, 1};
+  const Kind kind = choose(M, N, K, ws ? ws_bytes : 0, plan);
+  if (kind == kTileDmaSplit)
     a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + CBQ_WS_CTRL_BYTES);
-    a.splits = splitk_count(M, N, K);
-  }
-  launch_kind<ACT>(kind, a, s);
+  launch_kind<ACT>(kind, a, plan, s);
   return launch_status("cbq_w8a16_linear");
 }
 
@@ -1459,8 +1526,7 @@ extern "C" size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_
   if (M <= 0 || N <= 0 || K <= 0) return CBQ_WS_CTRL_BYTES;
   // The larger of the MFMA split-K partials and the general path's partial
   // sums (the dtype and alignment that choose between them are not known here).
-  const int sp = splitk_count(M, N, K);
-  const int64_t mfma = sp ? splitk_bytes(M, N, sp) : 0;
+  const int64_t mfma = splitk_bytes(M, N, split_plan(M, N, K));
   return CBQ_WS_CTRL_BYTES + static_cast<size_t>(std::max(mfma, general_split_bytes(M, N, K)));
 }
 

@@ -217,6 +217,37 @@ def test_splitk_large_m_few_tiles(M, K, N):
     torch.testing.assert_close(y_split.float(), y_one.float(), **TOL)
 
 
+@pytest.mark.parametrize("M,K,N,dt,n_out,path", [
+    (128, 4096, 11008, torch.float16, 3, "128-row tiles, K in 4 ranges"),
+    (512, 4096, 11008, torch.bfloat16, 0, "128-row tiles, whole"),
+    (768, 4096, 11008, torch.float16, 2, "128-row tiles, 256 whole + 2 over 16 ranges"),
+    (1536, 4096, 11008, torch.bfloat16, 2, "256-row tiles, 256 whole + 2 over 16 ranges"),
+    (3000, 1024, 5500, torch.float16, 0, "256-row tiles, 256 whole + 8 over 4 ranges, M and N tails"),
+])
+def test_dma_plans(M, K, N, dt, n_out, path):
+    """Each x-tile height and split plan of the MFMA tile path (the host's
+    time model picks them per shape): rows that fall in whole and in split
+    tail tiles (the last tile column) against the oracle, and the full
+    output against the same call with a control-block workspace (no split)."""
+    from cublade_amd import _abi
+    print(f"[w8a16] {dt} M={M} K={K} N={N} outliers={n_out} ({path})", flush=True)
+    rows = [0, M // 2 + 3, 2 * M // 3, M - 1]
+    y = run_and_check(M, K, N, dt, seed=M + N, bias=True, n_out=n_out, rows=rows)
+    x, wq, s, b, oc, w_out = make_case(M, K, N, dt, M + N, True, n_out)
+    xd, wd, sd, bd = x.to(DEV), wq.to(DEV), s.to(DEV), b.to(DEV)
+    ocd = torch.tensor(oc, dtype=torch.int64, device=DEV) if oc else None
+    wod = w_out.to(DEV) if oc else None
+    L = _abi.lib()
+    y_one = torch.empty_like(y)
+    ws = torch.zeros(_abi.WS_CTRL_BYTES, dtype=torch.uint8, device=DEV)
+    rc = L.cbq_w8a16_linear(_abi.ptr(xd), CODE_OF[dt], _abi.ptr(wd), _abi.ptr(sd), _abi.ptr(bd),
+                            None if ocd is None else _abi.ptr(ocd), n_out,
+                            None if wod is None else _abi.ptr(wod), M, N, K, _abi.ptr(ws),
+                            ws.numel(), _abi.ptr(y_one), _abi.stream_handle(xd.device))
+    assert rc == 0
+    torch.testing.assert_close(y.float(), y_one.float(), **TOL)
+
+
 def test_mfma_bit_stability_across_calls():
     """Same inputs, same outputs, bit for bit (fixed accumulation order)."""
     x, wq, s, b, _, _ = make_case(256, 1024, 512, torch.float16, 8, bias=True)

@@ -91,14 +91,17 @@ def test_workspace_sizes():
     # [16, 11008] fp32 over 43 tiles of 16 x 256)
     assert L.cbq_w8a16_ws_bytes(16, 11008, 4096, 0) == C + 16 * 16 * 11008 * 4
     assert L.cbq_w8a16_ws_bytes(4096, 11008, 4096, 0) == C
-    # split-K tile path (64 < M < 1024): 4 k-ranges x 43 tiles of 256 KiB
-    # fp32 partials (256 CUs, also the CPU-only fallback count)
-    assert L.cbq_w8a16_ws_bytes(256, 11008, 4096, 0) == C + 4 * 43 * 256 * 1024
-    assert L.cbq_w8a16_ws_bytes(512, 11008, 4096, 3) == C + 2 * 86 * 256 * 1024
+    # split-K tile path, 256 CUs (also the CPU-only fallback count): 2 k-ranges
+    # x 86 tiles of 128 x 256 (128 KiB of fp32 partials each)
+    assert L.cbq_w8a16_ws_bytes(256, 11008, 4096, 0) == C + 2 * 86 * 128 * 1024
+    assert L.cbq_w8a16_ws_bytes(512, 11008, 4096, 3) == C      # 172 whole 128-row tiles
     assert L.cbq_w8a16_ws_bytes(256, 11008, 4000, 0) == C      # K % 64 != 0
-    # few tiles (the MLP down projection): 11 k-ranges x 16 tiles, <= 256 workgroups
-    assert L.cbq_w8a16_ws_bytes(256, 4096, 11008, 0) == C + 11 * 16 * 256 * 1024
+    # few tiles (the MLP down projection): 8 k-ranges x 32 tiles of 128 x 256,
+    # 5 k-ranges x 48 tiles of 256 x 256; <= 256 workgroups
+    assert L.cbq_w8a16_ws_bytes(256, 4096, 11008, 0) == C + 8 * 32 * 128 * 1024
     assert L.cbq_w8a16_ws_bytes(768, 4096, 11008, 0) == C + 5 * 48 * 256 * 1024
+    # 258 tiles of 256 x 256: one full wave whole, the 2 left over split 16 ways
+    assert L.cbq_w8a16_ws_bytes(1536, 11008, 4096, 0) == C + 16 * 2 * 256 * 1024
 
 
 def test_nd_entry_points_validate_and_size():
