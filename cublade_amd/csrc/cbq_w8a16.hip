@@ -1297,7 +1297,8 @@ __global__ __launch_bounds__(kBlock) void k_general_reduce(GenArgs a) {
 //                 K <= 4096 and the 48-row groups fit one wave of
 //                 workgroups; else k_skinny (TM = 1)
 //   M <= 64       k_stream<2 or 4> under the same size rules (3 row tiles
-//                 per workgroup); else k_skinny, TM = ceil(M / 16)
+//                 per workgroup); else k_skinny, TM = ceil(M / 16); for
+//                 M > 32 and K > 8192 the split k_gemm_dma plan below first
 //   M > 64        k_gemm_dma (K % 64 == 0 and 32-bit operand offsets) with
 //                 the x tile (256 or 128 rows) and split-K plan of dma_plan:
 //                 the last, short wave of tiles split over K (2-16 k-ranges,
@@ -1368,9 +1369,18 @@ DmaPlan dma_plan(int64_t M, int64_t N, int64_t K, bool allow_split) {
   return best;
 }
 
-// The split plan when it applies (M > 64, k_gemm_dma usable), else none.
+// Whether k_gemm_dma is a candidate: M > 64, or 32 < M <= 64 with K above
+// 8 x-chunks of k_stream<4> (from 8 chunks on its per-chunk staging and
+// barriers cost more than the empty rows of a 128-row MFMA tile: N = 4096,
+// K = 11008, M = 64: k_stream 52.2 us, 128 x 256 tiles over 11 k-ranges
+// about 31 us; at K = 4096 k_stream is ahead, 29.8 us).
+bool dma_candidate(int64_t M, int64_t N, int64_t K) {
+  return (M > 64 || (M > 32 && K > 8 * stream_kc<4>())) && dma_ok(M, N, K);
+}
+
+// The split plan when it applies, else none.
 DmaPlan split_plan(int64_t M, int64_t N, int64_t K) {
-  if (M <= 64 || !dma_ok(M, N, K)) return DmaPlan{4, 0, 1};
+  if (!dma_candidate(M, N, K)) return DmaPlan{4, 0, 1};
   return dma_plan(M, N, K, true);
 }
 
@@ -1381,12 +1391,14 @@ Kind choose(int64_t M, int64_t N, int64_t K, size_t ws_bytes, DmaPlan& plan) {
     return (stream && K <= 4096 && cdiv(N, kStream1Rows) <= cus) ? kStream1 : kSkinny1;
   const bool tiles_fit = cdiv(N, 16) <= kStreamMaxTiles * cus;
   if (M <= 32) return (stream && tiles_fit) ? kStream2 : kSkinny2;
-  if (M <= 64) return (stream && tiles_fit) ? kStream4 : kSkinny4;
+  const Kind narrow = (stream && tiles_fit) ? kStream4 : kSkinny4;
+  if (M <= 64 && !dma_candidate(M, N, K)) return narrow;
   if (!dma_ok(M, N, K)) return M < 1024 ? kTileMid : kTileLarge;
   plan = dma_plan(M, N, K, true);
   if (plan.splits > 1 &&
       ws_bytes >= static_cast<size_t>(CBQ_WS_CTRL_BYTES + splitk_bytes(M, N, plan)))
     return kTileDmaSplit;
+  if (M <= 64) return narrow;
   if (M < 384) return kTileMid;
   plan = dma_plan(M, N, K, false);
   return kTileDma;

@@ -100,6 +100,8 @@ def test_workspace_sizes():
     # 5 k-ranges x 48 tiles of 256 x 256; <= 256 workgroups
     assert L.cbq_w8a16_ws_bytes(256, 4096, 11008, 0) == C + 8 * 32 * 128 * 1024
     assert L.cbq_w8a16_ws_bytes(768, 4096, 11008, 0) == C + 5 * 48 * 256 * 1024
+    # 32 < M <= 64 with K > 8192: the split MFMA path (11 ranges x 16 tiles of 128 x 256)
+    assert L.cbq_w8a16_ws_bytes(64, 4096, 11008, 0) == C + 11 * 16 * 128 * 1024
     # 258 tiles of 256 x 256: one full wave whole, the 2 left over split 16 ways
     assert L.cbq_w8a16_ws_bytes(1536, 11008, 4096, 0) == C + 16 * 2 * 256 * 1024
 
