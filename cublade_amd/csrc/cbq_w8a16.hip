@@ -55,7 +55,6 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef __bf16 b8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f16x __attribute__((ext_vector_type(16)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 // Operands and staging registers use native vector types: HIP's uint4 is a
 // struct around a union, and arrays of it are kept on the stack (scratch or
@@ -74,14 +73,17 @@ __device__ __forceinline__ f4 mfma16x16x32(const u32x4& a, const u32x4& b, f4 c)
 template <int ACT>
 __device__ __forceinline__ void i8x4_to_act(uint32_t w, uint32_t& lo, uint32_t& hi) {
   if constexpr (ACT == kF16) {
-    // fp16 0x6400 | b is 1024 + b for a byte b; b = q + 128, minus 1152 -> q.
-    // v_perm_b32 selector bytes 0-3 pick bytes of u, 4 picks 0x64.
-    const uint32_t u = w ^ 0x80808080u;
-    const uint32_t l = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
-    const uint32_t h = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
-    const h2 bias = {static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
-    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, l) - bias);
-    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, h) - bias);
+    // One v_cvt_f16_i16 per code: the SDWA source select takes byte b of w
+    // sign-extended, the destination select writes one half of lo / hi and
+    // keeps the other (exact: every int8 is an fp16). The compiler does not
+    // form these selects from shifts and casts itself (it shifts each byte
+    // first and packs the halves: 5 instructions per word instead of 4).
+    asm("v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
+        "v_cvt_f16_i16_sdwa %1, sext(%2) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+        "v_cvt_f16_i16_sdwa %1, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3"
+        : "=&v"(lo), "=&v"(hi)
+        : "v"(w));
   } else {
     float f[4];
     int8x4_to_f32(w, f);
@@ -532,32 +534,34 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
       }
     }
   };
-  // Step t: set 0 holds half 0 of tile t, set 1 half 1, wa weight tile 0 of
-  // set 0 widened; tiles t + 1 and t + 2 are in flight. Half 0 (its last
-  // tile widens tile 0 of set 1); the wait for tile t + 1 and the barrier,
-  // after which every wave is done with tile t's stage (its fragments were
-  // read during step t - 1), so the DMA of tile t + 3 goes there; half 1 with
-  // the DMA spread over its first tile and the reads of tile t + 1's half 0
-  // over its first two tiles; then the reads of half 1 into set 1. The other
-  // wave of the SIMD keeps the MFMA pipe busy while a wave waits.
+  // Step t: set 0 holds half 0 of tile t, wa weight tile 0 of set 0
+  // widened; tiles t + 1 and t + 2 are in flight. Half 0, with the reads of
+  // tile t's half 1 into set 1 spread over its first MFMAs (tile t landed
+  // before the previous step's barrier; the last tile of half 0 widens tile
+  // 0 of set 1); the wait for tile t + 1 and the barrier, after which every
+  // wave is done with tile t's stage, so the DMA of tile t + 3 goes there;
+  // half 1 with one DMA instruction and one read of tile t + 1's half 0 into
+  // set 0 after each of its first MFMAs. Spreading the DMA and the reads
+  // (rather than issuing them in bursts) took 4-5% off the step at M = 4096,
+  // N = 11008 / 4096 on MI355X. The other wave of the SIMD keeps the MFMA
+  // pipe busy while a wave waits.
   auto step = [&](int t, auto dma, int nwait) {
-    half(fr[0], &fr[1], [&](int, int) {});
+    half(fr[0], &fr[1], [&](int i, int p) {
+      const int r = i * 2 * TM + p;
+      if (r < 2 * TM + TN) read_one(t % NS, 1, fr[1], r);
+    });
     __builtin_amdgcn_sched_barrier(0);
     if (nwait >= 1) dma_wait_barrier<XL + WL>();
     else dma_wait_barrier<0>();
     __builtin_amdgcn_sched_barrier(0);
     const int stage_cur = t % NS, stage_next = (t + 1) % NS;
     half(fr[1], &fr[0], [&](int i, int p) {
-      if constexpr (decltype(dma)::value) {
-        if (i == 0 && 2 * p < XL + WL) {
-          issue_one(t + NS, stage_cur, 2 * p);
-          issue_one(t + NS, stage_cur, 2 * p + 1);
-        }
-      }
       const int r = i * 2 * TM + p;
+      if constexpr (decltype(dma)::value) {
+        if (r < XL + WL) issue_one(t + NS, stage_cur, r);
+      }
       if (r < 2 * TM + TN) read_one(stage_next, 0, fr[0], r);
     });
-    read_half(stage_next, 1, fr[1]);
     __builtin_amdgcn_sched_barrier(0);
   };
   using yes = std::true_type;
@@ -571,13 +575,15 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
     else if (nk > 1) dma_wait_barrier<XL + WL>();
     else dma_wait_barrier<0>();
     read_half(0, 0, fr[0]);
-    read_half(0, 1, fr[1]);
 #pragma unroll
     for (int c = 0; c < 4; ++c) cvt_word(fr[0], 0, c, wa);
     int t = 0;
     for (; t + NS < nk; ++t) step(t, yes{}, 1);     // tile t + 2 in flight, DMA of t + 3
     for (; t + 1 < nk; ++t) step(t, no{}, nk - 2 - t);
-    half(fr[0], &fr[1], [&](int, int) {});
+    half(fr[0], &fr[1], [&](int i, int p) {
+      const int r = i * 2 * TM + p;
+      if (r < 2 * TM + TN) read_one((nk - 1) % NS, 1, fr[1], r);
+    });
     half(fr[1], nullptr, [&](int, int) {});
   }
 
