@@ -100,9 +100,14 @@ def main(argv=None):
         for k, n, avg, mn, mx, _ in kernel_stats(argv[1]):
             print(f"{k:110s} {n:6d} {avg:10.2f} {mn:10.2f} {mx:10.2f}")
     else:
+        # Per kernel: mean, median and the values in dispatch order (the first
+        # dispatch of a kernel can be an outlier: warm-up, first scratch use).
         for (k, c), vals in sorted(counter_stats(argv[1]).items()):
             avg = sum(vals) / len(vals)
-            print(f"{k:110s} {c:12s} n={len(vals):4d} avg={avg:14.1f}")
+            med = sorted(vals)[len(vals) // 2] if len(vals) % 2 else \
+                sum(sorted(vals)[len(vals) // 2 - 1:len(vals) // 2 + 1]) / 2
+            each = " ".join(f"{v:.1f}" for v in vals[:8]) + (" ..." if len(vals) > 8 else "")
+            print(f"{k:110s} {c:12s} n={len(vals):4d} avg={avg:14.1f} median={med:14.1f}  [{each}]")
     return 0
 
 
