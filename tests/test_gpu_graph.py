@@ -45,10 +45,12 @@ def _check_replays(static_in, make_input, fn, g, out, n=3):
                                w.view(torch.uint8) if w.dtype.itemsize == 1 else w), f"replay {seed}"
 
 
-@pytest.mark.parametrize("M", [16, 256])
+@pytest.mark.parametrize("M", [16, 256, 4096])
 def test_graph_w8a16_layer(M):
-    """The W8A16 layer at a decode shape (weight streaming) and at M = 256
-    (split-K: fp32 partials in the workspace, reused by every replay)."""
+    """The W8A16 layer at a decode shape (weight streaming), at M = 256
+    (split-K: fp32 partials in the workspace, reused by every replay) and at
+    M = 4096 (256-row MFMA tiles, whose kernel keeps a few spilled registers
+    in scratch memory)."""
     from cublade_amd.quantization import cuBladeW8A16LinearLayer
     N, K = 4096, 2048
     g0 = torch.Generator().manual_seed(M)
