@@ -382,8 +382,8 @@ constexpr int kDmaThreads = 512;   // 8 waves, two per SIMD
 constexpr int kDmaTN = 2;          // 32-row weight tiles per wave
 
 // TM: 32-row x tiles per wave; the workgroup tile is 64 TM x 256 (TM = 4:
-// 256 x 256, TM = 2: 128 x 256 for small M and tile counts that leave the
-// last wave of workgroups short).
+// 256 x 256; TM = 3 or 2: 192 or 128 x 256 for small M and for tile counts
+// that leave the last wave of workgroups short).
 // SPLIT: workgroups [0, full_tiles) take whole tiles 0 .. full_tiles - 1;
 // the others split the remaining tiles over `splits` k-ranges, workgroup
 // full_tiles + b covering tail tile b % rest of k-range b / rest (after the
@@ -391,13 +391,13 @@ constexpr int kDmaTN = 2;          // 32-row weight tiles per wave
 template <int ACT, bool SPLIT, int TM>
 __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
   constexpr int BM = 64 * TM, BN = 256, BK = 64, NS = 3;
-  constexpr int XB = BM * BK * 2;          // x stage bytes (32 / 16 KiB)
+  constexpr int XB = BM * BK * 2;          // x stage bytes (32 / 24 / 16 KiB)
   constexpr int WB = BN * BK;              // weight stage bytes (16 KiB)
   constexpr int SB = XB + WB;
   constexpr int XL = XB / (kDmaThreads * 16);   // DMA instructions per thread: TM
   constexpr int WL = WB / (kDmaThreads * 16);   // 2
   constexpr int TN = kDmaTN;
-  static_assert(TM == 2 || TM == 4, "x tile of 128 or 256 rows");
+  static_assert(TM >= 2 && TM <= 4, "x tile of 128, 192 or 256 rows");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * SB];
 
   const int tid = threadIdx.x;
@@ -689,12 +689,12 @@ void launch_gemm_dma(GemmArgs a, hipStream_t s) {
 
 // Split-K finish: one thread per partial f4 (4 outputs y[m, n .. n+3]) of a
 // tail tile; sums the splits in order (deterministic), then scale, outliers,
-// bias and one rounding, as in the tile kernels' epilogue. Partial index
-// bits, low to high: lane (6), q (2), j (log2 TM), i (1), wave (3), tail tile.
+// bias and one rounding, as in the tile kernels' epilogue. Partial index,
+// fastest first: lane (64), q (4), j (TM), i (2), wave (8), tail tile.
 template <int ACT, int TM>
 __global__ __launch_bounds__(kBlock) void k_splitk_reduce(GemmArgs a) {
-  constexpr int LJ = TM == 4 ? 2 : 1;
-  constexpr int kTileF4 = 8 * kDmaTN * TM * 4 * 64;
+  constexpr int kWaveF4 = kDmaTN * TM * 4 * 64;
+  constexpr int kTileF4 = 8 * kWaveF4;
   const int rest = a.tiles_m * a.tiles_n - a.full_tiles;
   const int64_t per_split = static_cast<int64_t>(rest) * kTileF4;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
@@ -702,9 +702,9 @@ __global__ __launch_bounds__(kBlock) void k_splitk_reduce(GemmArgs a) {
   const f4* src = reinterpret_cast<const f4*>(a.part) + idx;
   f4 sum = src[0];
   for (int sp = 1; sp < a.splits; ++sp) sum += src[sp * per_split];
-  const int lane = static_cast<int>(idx & 63), q = static_cast<int>((idx >> 6) & 3);
-  const int j = static_cast<int>((idx >> 8) & (TM - 1)), i = static_cast<int>((idx >> (8 + LJ)) & 1);
-  const int wave = static_cast<int>((idx >> (9 + LJ)) & 7);
+  const int w = static_cast<int>(idx % kWaveF4);
+  const int lane = w & 63, q = (w >> 6) & 3, j = (w >> 8) % TM, i = (w >> 8) / TM;
+  const int wave = static_cast<int>((idx / kWaveF4) & 7);
   int tm, tn;
   group_tile(a.full_tiles + static_cast<int>(idx / kTileF4), a, tm, tn);
   const int m = tm * 64 * TM + (wave & 1) * 32 * TM + j * 32 + (lane & 31);
@@ -1351,25 +1351,30 @@ bool dma_ok(int64_t M, int64_t N, int64_t K) {
 // Plan of the k_gemm_dma path with the lowest modelled time (0.01 us): the
 // 64-k steps of the longest chain of workgroups on one CU times the cost of
 // a step, which grows with the share of CUs busy (clock and bandwidth under
-// load): 1.30 + 0.55 occ us for 256 x 256 tiles, 0.78 + 0.27 occ us for
-// 128 x 256; plus, when split, 5 us for the reduce pass and 0.12 us per
+// load): 1.30 + 0.55 occ us for 256 x 256 tiles, 0.96 + 0.50 occ us for
+// 192 x 256, 0.84 + 0.28 occ us for 128 x 256; plus, when split, 5 us for the reduce pass and 0.12 us per
 // 256 KiB of partial tiles written and re-read. With `rest` tiles in the
 // last, short wave, a split runs the full waves whole and the rest over sp
 // k-ranges (rest x sp workgroups fit one wave of CUs, each range keeps at
 // least four 64-k steps). Fitted on MI355X over M = 96..4096 at N = 11008,
-// K = 4096 and N = 4096, K = 11008 (fp16, e.g. M = 1536, N = 11008: whole
-// 256 x 256 tiles 208 us, the 2 tail tiles over 16 ranges 141 us; M = 128:
-// 256 x 256 over 5 ranges 46.8 us, 128 x 256 over 5 ranges 30.8 us).
+// K = 4096 and N = 4096, K = 11008 (fp16; over those 20 shapes the plan
+// picked is 0.6% slower than the best one measured on average, 3.4% at
+// worst). E.g. M = 1536, N = 11008: whole 256 x 256 tiles 208 us, the 2
+// tail tiles over 16 ranges 133 us; M = 768: 172 tiles of 192 x 256 in one
+// wave 74.9 us, 258 of 128 x 256 with the tail split 79.6 us; M = 128:
+// 256 x 256 over 5 ranges 46.8 us, 128 x 256 over 4 ranges 29.8 us.
 int64_t dma_step_cost(int tm, int64_t wgs, int64_t cus) {
   const int64_t busy = std::min(wgs, cus);
-  return tm == 4 ? 130 + 55 * busy / cus : 78 + 27 * busy / cus;
+  if (tm == 4) return 130 + 55 * busy / cus;
+  if (tm == 3) return 96 + 50 * busy / cus;
+  return 84 + 28 * busy / cus;
 }
 
 DmaPlan dma_plan(int64_t M, int64_t N, int64_t K, bool allow_split) {
   const int64_t cus = device_cus(), nk = K / 64;
   DmaPlan best{4, 0, 1};
   int64_t best_cost = INT64_MAX;
-  for (const int tm : {4, 2}) {
+  for (const int tm : {4, 2, 3}) {
     const int64_t tiles = cdiv(M, 64 * tm) * cdiv(N, 256);
     const int64_t rounds = tiles / cus, rest = tiles % cus;
     const int64_t whole = nk * cdiv(tiles, cus) * dma_step_cost(tm, tiles, cus);
@@ -1447,10 +1452,12 @@ void launch_kind(Kind k, const GemmArgs& a, const DmaPlan& p, hipStream_t s) {
     case kTileMid: launch_gemm<ACT, 128, 64, 64, 2, 2, 1>(a, s); break;
     case kTileDma:
       if (p.tm == 2) launch_gemm_dma<ACT, 2>(a, s);
+      else if (p.tm == 3) launch_gemm_dma<ACT, 3>(a, s);
       else launch_gemm_dma<ACT, 4>(a, s);
       break;
     case kTileDmaSplit:
       if (p.tm == 2) launch_gemm_dma_splitk<ACT, 2>(a, p, s);
+      else if (p.tm == 3) launch_gemm_dma_splitk<ACT, 3>(a, p, s);
       else launch_gemm_dma_splitk<ACT, 4>(a, p, s);
       break;
     default: launch_gemm<ACT, 256, 256, 64, 4, 2, 1>(a, s); break;

@@ -220,17 +220,21 @@ def test_splitk_large_m_few_tiles(M, K, N):
 @pytest.mark.parametrize("M,K,N,dt,n_out,path", [
     (128, 4096, 11008, torch.float16, 3, "128-row tiles, K in 4 ranges"),
     (512, 4096, 11008, torch.bfloat16, 0, "128-row tiles, whole"),
-    (768, 4096, 11008, torch.float16, 2, "128-row tiles, 256 whole + 2 over 16 ranges"),
+    (2137, 2048, 8192, torch.bfloat16, 2, "128-row tiles, 512 whole + the rest over 4 ranges"),
+    (768, 4096, 11008, torch.float16, 2, "192-row tiles, whole (172 tiles in one wave)"),
+    (139, 4096, 11008, torch.bfloat16, 1, "192-row tiles, K in 4 ranges, M tail"),
+    (2211, 1024, 11008, torch.float16, 0, "192-row tiles, 512 whole + the rest over 4 ranges"),
     (1536, 4096, 11008, torch.bfloat16, 2, "256-row tiles, 256 whole + 2 over 16 ranges"),
     (3000, 1024, 5500, torch.float16, 0, "256-row tiles, 256 whole + 8 over 4 ranges, M and N tails"),
     (64, 11008, 4096, torch.float16, 2, "M <= 64 with long K: 128-row tiles over 11 ranges"),
     (40, 16384, 1000, torch.bfloat16, 0, "M <= 64 with long K, N tail"),
 ])
 def test_dma_plans(M, K, N, dt, n_out, path):
-    """Each x-tile height and split plan of the MFMA tile path (the host's
-    time model picks them per shape): rows that fall in whole and in split
-    tail tiles (the last tile column) against the oracle, and the full
-    output against the same call with a control-block workspace (no split)."""
+    """Each x-tile height (128, 192, 256 rows) and split plan of the MFMA tile
+    path (whole tiles, all tiles over k-ranges, full waves whole plus a split
+    tail; the host's time model picks them per shape): sampled rows against
+    the oracle, and the full output against the same call with a
+    control-block workspace (no split)."""
     from cublade_amd import _abi
     print(f"[w8a16] {dt} M={M} K={K} N={N} outliers={n_out} ({path})", flush=True)
     rows = [0, M // 2 + 3, 2 * M // 3, M - 1]

@@ -97,9 +97,9 @@ def test_workspace_sizes():
     assert L.cbq_w8a16_ws_bytes(512, 11008, 4096, 3) == C      # 172 whole 128-row tiles
     assert L.cbq_w8a16_ws_bytes(256, 11008, 4000, 0) == C      # K % 64 != 0
     # few tiles (the MLP down projection): 8 k-ranges x 32 tiles of 128 x 256,
-    # 5 k-ranges x 48 tiles of 256 x 256; <= 256 workgroups
+    # 4 k-ranges x 64 tiles of 192 x 256 (192 KiB each); <= 256 workgroups
     assert L.cbq_w8a16_ws_bytes(256, 4096, 11008, 0) == C + 8 * 32 * 128 * 1024
-    assert L.cbq_w8a16_ws_bytes(768, 4096, 11008, 0) == C + 5 * 48 * 256 * 1024
+    assert L.cbq_w8a16_ws_bytes(768, 4096, 11008, 0) == C + 4 * 64 * 192 * 1024
     # 32 < M <= 64 with K > 8192: the split MFMA path (11 ranges x 16 tiles of 128 x 256)
     assert L.cbq_w8a16_ws_bytes(64, 4096, 11008, 0) == C + 11 * 16 * 128 * 1024
     # 258 tiles of 256 x 256: one full wave whole, the 2 left over split 16 ways
