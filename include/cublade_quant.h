@@ -181,8 +181,8 @@ int cbq_dequant_int8_group_nd(const int8_t* q, const float* scale,
  * (fp32 / unaligned) path's fp32 partial sums, up to 16 x M x N x 4 bytes
  * when its tiles give fewer than two workgroups per CU, and, for M > 64 when
  * the last wave of output tiles is short, the MFMA path's fp32 partial
- * tiles of that wave (ranges x tail tiles x 256 KiB for 256 x 256 tiles or
- * 128 KiB for 128 x 256; at most 16 ranges and at most one partial tile per
+ * tiles of that wave (ranges x tail tiles x 256 / 192 / 128 KiB for tiles of
+ * 256 / 192 / 128 x 256; at most 16 ranges and at most one partial tile per
  * CU, i.e. <= 64 MiB on MI355X). The reference allocates its temporaries
  * inside the forward (linear.py:105-131). */
 size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_out);
