@@ -29,18 +29,22 @@
 // contiguous run of tiles, and tiles run in groups of 8 m-tiles, so the
 // workgroups resident on one XCD share activation and weight k-slices in L2.
 //
-// k_gemm_dma<ACT> (M >= 1024, K % 64 == 0): 256 x 256 tiles of
-// v_mfma_f32_32x32x16 fed by LDS DMA, 8 waves (two per SIMD), int8 weights
-// widened after the fragment read, explicitly scheduled k-steps (see the
-// kernel's comment).
+// k_gemm_dma<ACT, SPLIT, TM> (M > 64, K % 64 == 0): 64 TM x 256 tiles (TM =
+// 4, 3, 2) of v_mfma_f32_32x32x16 fed by LDS DMA, 8 waves (two per SIMD),
+// int8 weights widened after the fragment read, explicitly scheduled k-steps
+// (see the kernel's comment). With SPLIT, the tiles of a short last wave run
+// over several k-ranges into fp32 partial tiles in the caller's workspace and
+// k_splitk_reduce sums them in a fixed order (no cross-workgroup fences);
+// dma_plan picks the tile height and the split with a fitted time model.
 //
 // k_stream1<ACT> (M <= 16) and k_stream<ACT, TM> (M <= 64): persistent
 // weight streaming for large weights (see the kernels' comments).
 //
 // k_skinny<ACT, TM, TN, U> (M <= 64): weight streaming with the K split across
 // the waves of a workgroup and reduced through LDS (see below). A split of K
-// across workgroups was measured slower on MI355X: publishing partial tiles
-// needs agent-scope release fences, which write back the whole L2.
+// across workgroups that publishes partial tiles for a last-arriving
+// workgroup was measured slower on MI355X: it needs agent-scope release
+// fences, which write back the whole L2.
 #include <algorithm>
 #include <type_traits>
 
