@@ -1325,7 +1325,7 @@ __global__ __launch_bounds__(kBlock) void k_general_reduce(GenArgs a) {
 //                 workgroups; else k_skinny (TM = 1)
 //   M <= 64       k_stream<2 or 4> under the same size rules (3 row tiles
 //                 per workgroup); else k_skinny, TM = ceil(M / 16); for
-//                 M > 32 and K > 8192 the split k_gemm_dma plan below first
+//                 M > 24 and K > 8192 the split k_gemm_dma plan below first
 //   M > 64        k_gemm_dma (K % 64 == 0 and 32-bit operand offsets) with
 //                 the x tile (256 or 128 rows) and split-K plan of dma_plan:
 //                 the last, short wave of tiles split over K (2-16 k-ranges,
@@ -1401,13 +1401,14 @@ DmaPlan dma_plan(int64_t M, int64_t N, int64_t K, bool allow_split) {
   return best;
 }
 
-// Whether k_gemm_dma is a candidate: M > 64, or 32 < M <= 64 with K above
+// Whether k_gemm_dma is a candidate: M > 64, or 24 < M <= 64 with K above
 // 8 x-chunks of k_stream<4> (from 8 chunks on its per-chunk staging and
 // barriers cost more than the empty rows of a 128-row MFMA tile: N = 4096,
 // K = 11008, M = 64: k_stream 52.2 us, 128 x 256 tiles over 11 k-ranges
-// about 31 us; at K = 4096 k_stream is ahead, 29.8 us).
+// about 31 us; M = 32: k_stream<2> 32.4 us; at M = 24 the two are level, and
+// at K = 4096 k_stream is ahead, 29.8 us at M = 64).
 bool dma_candidate(int64_t M, int64_t N, int64_t K) {
-  return (M > 64 || (M > 32 && K > 8 * stream_kc<4>())) && dma_ok(M, N, K);
+  return (M > 64 || (M > 24 && K > 8 * stream_kc<4>())) && dma_ok(M, N, K);
 }
 
 // The split plan when it applies, else none.
@@ -1422,8 +1423,8 @@ Kind choose(int64_t M, int64_t N, int64_t K, size_t ws_bytes, DmaPlan& plan) {
   if (M <= 16)
     return (stream && K <= 4096 && cdiv(N, kStream1Rows) <= cus) ? kStream1 : kSkinny1;
   const bool tiles_fit = cdiv(N, 16) <= kStreamMaxTiles * cus;
-  if (M <= 32) return (stream && tiles_fit) ? kStream2 : kSkinny2;
-  const Kind narrow = (stream && tiles_fit) ? kStream4 : kSkinny4;
+  const Kind narrow = M <= 32 ? ((stream && tiles_fit) ? kStream2 : kSkinny2)
+                              : ((stream && tiles_fit) ? kStream4 : kSkinny4);
   if (M <= 64 && !dma_candidate(M, N, K)) return narrow;
   if (!dma_ok(M, N, K)) return M < 1024 ? kTileMid : kTileLarge;
   plan = dma_plan(M, N, K, true);

@@ -227,6 +227,7 @@ def test_splitk_large_m_few_tiles(M, K, N):
     (1536, 4096, 11008, torch.bfloat16, 2, "256-row tiles, 256 whole + 2 over 16 ranges"),
     (3000, 1024, 5500, torch.float16, 0, "256-row tiles, 256 whole + 8 over 4 ranges, M and N tails"),
     (64, 11008, 4096, torch.float16, 2, "M <= 64 with long K: 128-row tiles over 11 ranges"),
+    (32, 11008, 4096, torch.bfloat16, 1, "M = 32 with long K: 128-row tiles over 11 ranges"),
     (40, 16384, 1000, torch.bfloat16, 0, "M <= 64 with long K, N tail"),
 ])
 def test_dma_plans(M, K, N, dt, n_out, path):

@@ -100,8 +100,11 @@ def test_workspace_sizes():
     # 4 k-ranges x 64 tiles of 192 x 256 (192 KiB each); <= 256 workgroups
     assert L.cbq_w8a16_ws_bytes(256, 4096, 11008, 0) == C + 8 * 32 * 128 * 1024
     assert L.cbq_w8a16_ws_bytes(768, 4096, 11008, 0) == C + 4 * 64 * 192 * 1024
-    # 32 < M <= 64 with K > 8192: the split MFMA path (11 ranges x 16 tiles of 128 x 256)
+    # 24 < M <= 64 with K > 8192: the split MFMA path (11 ranges x 16 tiles of 128 x 256)
     assert L.cbq_w8a16_ws_bytes(64, 4096, 11008, 0) == C + 11 * 16 * 128 * 1024
+    assert L.cbq_w8a16_ws_bytes(32, 4096, 11008, 0) == C + 11 * 16 * 128 * 1024
+    # M = 24: k_stream<2>, no MFMA partials; only the general path's 16 ranges of [24, 4096] fp32
+    assert L.cbq_w8a16_ws_bytes(24, 4096, 11008, 0) == C + 16 * 24 * 4096 * 4
     # 258 tiles of 256 x 256: one full wave whole, the 2 left over split 16 ways
     assert L.cbq_w8a16_ws_bytes(1536, 11008, 4096, 0) == C + 16 * 2 * 256 * 1024
 
