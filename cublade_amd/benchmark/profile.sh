@@ -75,7 +75,7 @@ $R traffic "k_deq_tensor<false, 1, 2>" "$RAW/fetch/bench_results.db" "$RAW/write
 {
   echo "# rocprof derived counter MfmaUtil = sum(SQ_VALU_MFMA_BUSY_CYCLES) / (max(GRBM_GUI_ACTIVE) * SIMDs) * 100,"
   echo "# per kernel: mean and median over dispatches, then the values in dispatch order (the first is the"
-  echo "# suite's warm-up call): W8A16 (suite config c5, M = 16 / 256 / 4096) and the dense GEMM (f4, 8192^3)"
+  echo "# suite's warm-up call): W8A16 (suite config c5, M = 16 / 256 / 768 / 1536 / 4096) and the dense GEMM (f4, 8192^3)"
   echo "# command: rocprofv3 --pmc MfmaUtil --kernel-trace -d RAW/mfma -o suite -- python -u -m cublade_amd.benchmark.suite --configs c5,f4 --reps 3 --warmup 1"
   $R counters "$RAW/mfma/suite_results.db" | grep -E "k_gemm_dma|k_stream|k_skinny|k_gemm<|k_mm_dma|Cijk"
 } > "$OUT/mfma_util.txt" || exit $?

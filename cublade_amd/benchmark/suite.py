@@ -83,7 +83,9 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
                  2 * n + n + 4 * G, n + 2 * n + 4 * G)
         del x
     if "c5" in selected:
-        for M in (16, 256, 4096):
+        # BASELINE config 5's M = 16 / 256 / 4096, plus M = 768 and 1536 (the
+        # 192-row tiles in one wave, and 256-row tiles with a split last wave)
+        for M in (16, 256, 768, 1536, 4096):
             x, w = configs.c5_w8a16(M)
             N, K = w.shape
             layer = cuBladeW8A16LinearLayer(K, N, bias=False, dtype=torch.float16)
