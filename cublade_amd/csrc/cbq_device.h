@@ -204,23 +204,33 @@ __device__ __forceinline__ uint4 pack8_out(const float (&f)[8]) {
 // ---------------------------------------------------------------------------
 // INT8 encoder: round half to even, clamp to [-127, 127], NaN -> 0.
 // ---------------------------------------------------------------------------
+// Three VALU operations: v_rndne_f32 (ties to even), v_cvt_i32_f32 (the
+// hardware conversion saturates out-of-range values and turns NaN into 0),
+// and v_med3_i32 for the clamp. Same results as clamping in fp32 first.
 __device__ __forceinline__ int q_int8(float v) {
-  float r = __builtin_rintf(v);              // v_rndne_f32: ties to even
-  r = r > 127.0f ? 127.0f : r;               // comparisons keep NaN as NaN
-  r = r < -127.0f ? -127.0f : r;
-  return (r == r) ? static_cast<int>(r) : 0;
+  const float r = __builtin_rintf(v);
+  int i;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(i) : "v"(r));
+  return i < -127 ? -127 : (i > 127 ? 127 : i);
+}
+
+// Low bytes of four integers as one word, a in byte 0 (two v_perm_b32 and
+// an or: selector nibbles 0-3 pick the second operand's bytes, 4-7 the
+// first's, 0xc a zero byte).
+__device__ __forceinline__ uint32_t pack4_low_bytes(int a, int b, int c, int d) {
+  const uint32_t ab = __builtin_amdgcn_perm(static_cast<uint32_t>(b), static_cast<uint32_t>(a),
+                                            0x0c0c0400u);
+  const uint32_t cd = __builtin_amdgcn_perm(static_cast<uint32_t>(d), static_cast<uint32_t>(c),
+                                            0x04000c0cu);
+  return ab | cd;
 }
 
 __device__ __forceinline__ uint2 pack8_int8(const float (&f)[8], float inv) {
   uint32_t w[2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const uint32_t b0 = static_cast<uint32_t>(q_int8(f[4 * h + 0] * inv)) & 0xffu;
-    const uint32_t b1 = static_cast<uint32_t>(q_int8(f[4 * h + 1] * inv)) & 0xffu;
-    const uint32_t b2 = static_cast<uint32_t>(q_int8(f[4 * h + 2] * inv)) & 0xffu;
-    const uint32_t b3 = static_cast<uint32_t>(q_int8(f[4 * h + 3] * inv)) & 0xffu;
-    w[h] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-  }
+  for (int h = 0; h < 2; ++h)
+    w[h] = pack4_low_bytes(q_int8(f[4 * h + 0] * inv), q_int8(f[4 * h + 1] * inv),
+                           q_int8(f[4 * h + 2] * inv), q_int8(f[4 * h + 3] * inv));
   return make_uint2(w[0], w[1]);
 }
 

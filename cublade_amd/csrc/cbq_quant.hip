@@ -2,12 +2,20 @@
 // and their C-ABI entry points.
 //
 // Kernels (reference kernels they replace, kernels/cuda/quantization/...):
+//   k_quant_tensor_1pass
+//                   per-tensor quant in one launch (x of 2^20 elements and
+//                   more): one resident workgroup per CU reads x once,
+//                   holds up to 96 MiB of it in registers, exchanges
+//                   workgroup maxima through tagged slots in the workspace,
+//                   then casts from registers (quantize_per_tensor_fp8.cu:38-132,
+//                   quantize_int8.cu:47-166: both passes in one)
 //   k_amax_tensor   per-tensor |x| max over a persistent grid: 16-byte loads,
 //                   wave64 DPP reduce, one partial maximum per workgroup
 //                   written to the workspace (no atomics: measured on MI355X,
 //                   ~4k same-address device atomics cost ~100 us)
 //                   (quantize_per_tensor_fp8.cu:38-86, quantize_int8.cu:47-101)
-//   k_cast_tensor   per-tensor cast on the same persistent grid: each workgroup
+//   k_cast_tensor   per-tensor cast on the same persistent grid (the two-pass
+//                   path for smaller or unaligned x): each workgroup
 //                   issues its first 16-byte loads, reduces the partial maxima
 //                   (L2-resident) to inv meanwhile, then 8-byte packed stores;
 //                   workgroup 0 writes the scale
@@ -38,6 +46,8 @@
 //
 // Numerics: see cbq_device.h. Every kernel guards its indices against the
 // sizes it is given; the entry points check shapes, dtypes and alignment.
+#include <cstdlib>
+
 #include "cbq_device.h"
 #include "cbq_host.h"
 
@@ -157,6 +167,242 @@ __global__ __launch_bounds__(kBlock) void k_cast_tensor(
       const float v = ld1<DT>(x, i) * inv;
       q[i] = FP8 ? q_fp8_1(v) : static_cast<uint8_t>(q_int8(v));
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Per tensor in one launch. A resident grid of one 1024-thread workgroup per
+// CU reads x once in grid-stride steps (4 chunks of 16 bytes per thread and
+// step: measured on MI355X, deeper load pipelines read 15-25% slower),
+// keeping the last HOLD_STEPS steps of each thread in registers; the
+// workgroups exchange their maxima through the workspace's control block;
+// then each casts its held chunks from registers and re-reads only the steps
+// that did not fit (x beyond 96 MiB of 2-byte elements, 48 MiB of fp32).
+// HBM traffic: 2N + N bytes up to that size, against 2N + 2N + N for the
+// amax + cast passes above.
+//
+// Step i of workgroup b covers the 4096 consecutive chunks starting at chunk
+// (i * gridDim.x + b) * 4096, lane t of the workgroup taking chunks + t,
+// + 1024 + t, + 2048 + t, + 3072 + t (one 64-byte-per-lane stretch of 16 KiB
+// per workgroup and step, the whole grid covering 16 MiB of x per step).
+//
+// Exchange (no atomics: same-address device atomics serialize at ~25 ns each
+// on MI355X, 6 us for one per workgroup). Control block layout, bytes:
+//   0      gen     64-bit call count of this workspace
+//   512    status  sticky; 1 when a workgroup's wait timed out
+//   1024   slot[b] 64-bit per workgroup: (low 32 bits of gen + 1) << 32 |
+//                  the workgroup's |x| maximum (float bits)
+// Every workgroup reads gen when it starts, publishes its slot with the tag
+// gen + 1, and polls all slots until every tag is gen + 1; workgroup 0 then
+// stores gen + 1 (every workgroup has read gen by then: its slot carries it).
+// Each call rewrites every slot, so no word needs resetting, and a stale tag
+// is always the previous call's. A wait gives up after spin_limit polls;
+// the workgroup then sets status and writes NaN codes (INT8: 0) and a NaN
+// scale instead of quietly wrong ones.
+// ---------------------------------------------------------------------------
+constexpr int kFusedBlock = 1024;                // 16 waves: four per SIMD
+constexpr int kFusedU = 4;                       // chunks per thread and step
+constexpr int64_t kFusedMinElems = int64_t(1) << 20;
+constexpr uint32_t kFusedSpinLimit = 1u << 20;   // polls (each >= one memory round trip)
+constexpr int kCtlGen = 0, kCtlStatus = 512, kCtlSlots = 1024;
+constexpr int kMaxFusedGrid = (CBQ_WS_CTRL_BYTES - kCtlSlots) / 8;
+
+// Steps held in registers: 24 chunks (96 VGPRs) of 2-byte input, 12 of fp32.
+template <int DT> constexpr int fused_hold_steps() { return DT == kF32 ? 3 : 6; }
+
+// Chunk loads and code stores addressed as a wave-uniform base plus a 32-bit
+// per-thread offset (keeps one offset register per thread instead of one
+// address pair per held chunk).
+template <int DT>
+__device__ __forceinline__ Raw8<DT> ld8_at(const char* base, uint32_t off) {
+  Raw8<DT> r;
+  r.a = ldg16(base + off);
+  if constexpr (DT == kF32) r.b = ldg16(base + off + 16);
+  return r;
+}
+
+template <int DT, bool FP8>
+__device__ __forceinline__ void cast_store8(const Raw8<DT>& r, float inv, uint8_t* base,
+                                            uint32_t off) {
+  float f[8];
+  cvt8<DT>(r, f);
+  stg8(base + off, FP8 ? pack8_fp8(f, inv) : pack8_int8(f, inv));
+}
+
+// Buffer resources for the held steps: num_records bounds each access, so a
+// chunk past the end of x reads as zeros and its code store is dropped by the
+// hardware, without branches (a guarded load would make the compiler wait
+// for every outstanding load where the branch rejoins).
+constexpr int kBufDword3 = 0x00020000;           // gfx9 raw buffer: 32-bit dword data format
+constexpr int kAuxNT = 2;                        // cache policy bit: non-temporal
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
+  const int nr = bytes <= 0 ? 0 : static_cast<int>(bytes);   // callers pass <= 128 KiB
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nr, kBufDword3);
+}
+
+template <int DT>
+__device__ __forceinline__ Raw8<DT> ld8_buf(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  Raw8<DT> r;
+  const u32x4 a = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rs, off, 0, CBQ_NT_LOADS ? kAuxNT : 0));
+  r.a = make_uint4(a.x, a.y, a.z, a.w);
+  if constexpr (DT == kF32) {
+    const u32x4 b = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                rs, off + 16, 0, CBQ_NT_LOADS ? kAuxNT : 0));
+    r.b = make_uint4(b.x, b.y, b.z, b.w);
+  }
+  return r;
+}
+
+template <int DT, bool FP8>
+__device__ __forceinline__ void cast_store8_buf(const Raw8<DT>& r, float inv,
+                                                __amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  float f[8];
+  cvt8<DT>(r, f);
+  const uint2 c = FP8 ? pack8_fp8(f, inv) : pack8_int8(f, inv);
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, u32x2{c.x, c.y}), rs, off, 0,
+                                        CBQ_NT_STORES_NARROW ? kAuxNT : 0);
+}
+
+// Grid-wide maximum of the workgroups' m (see the exchange above); returns
+// NaN if the wait timed out. Every thread of the workgroup gets the result.
+__device__ float grid_max_exchange(float m, char* ctl, uint32_t spin_limit, float* red) {
+  __shared__ unsigned long long s_gen;
+  auto* gen_w = reinterpret_cast<unsigned long long*>(ctl + kCtlGen);
+  auto* status = reinterpret_cast<unsigned int*>(ctl + kCtlStatus);
+  auto* slots = reinterpret_cast<unsigned long long*>(ctl + kCtlSlots);
+  if (threadIdx.x == 0) {
+    const unsigned long long gen = __hip_atomic_load(gen_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_gen = gen;
+    __hip_atomic_store(slots + blockIdx.x,
+                       (static_cast<unsigned long long>(static_cast<uint32_t>(gen + 1)) << 32) |
+                           __float_as_uint(m),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  const uint32_t tag = static_cast<uint32_t>(s_gen + 1);
+  const int G = static_cast<int>(gridDim.x);
+  uint32_t spins = 0;
+  float mx;
+  int ok;
+  for (;;) {
+    ok = 1;
+    mx = 0.0f;
+    for (int i = threadIdx.x; i < G; i += blockDim.x) {
+      const unsigned long long v = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ok &= static_cast<uint32_t>(v >> 32) == tag;
+      mx = fmaxf(mx, __uint_as_float(static_cast<uint32_t>(v)));
+    }
+    ok = __syncthreads_and(ok);
+    if (ok || spins >= spin_limit) break;
+    ++spins;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  mx = block_max(mx, red);
+  if (threadIdx.x == 0) {
+    if (!ok) __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (blockIdx.x == 0)
+      __hip_atomic_store(gen_w, s_gen + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return ok ? mx : __builtin_nanf("");
+}
+
+template <int DT, bool FP8>
+__global__ __launch_bounds__(kFusedBlock) void k_quant_tensor_1pass(
+    const void* __restrict__ x, int64_t n, float eps, uint8_t* __restrict__ q,
+    float* __restrict__ scale_out, char* __restrict__ ctl, uint32_t spin_limit) {
+  constexpr int U = kFusedU;
+  constexpr int HS = fused_hold_steps<DT>();
+  constexpr int EB = 8 * elem_bytes<DT>();            // bytes of x per chunk
+  constexpr float kQ = FP8 ? kQmaxFp8 : kQmaxInt8;
+  __shared__ float red[kFusedBlock / kWave];
+
+  const int64_t SB = static_cast<int64_t>(kFusedBlock) * U;   // chunks per workgroup and step
+  const int64_t GS = static_cast<int64_t>(gridDim.x) * SB;    // chunks per grid step
+  const int64_t n8 = n >> 3;
+  const int64_t I = (n8 + GS - 1) / GS;               // steps
+  const int64_t held0 = I > HS ? I - HS : 0;          // first held step; earlier steps are full
+  // chunk (i, u) = i * GS + b * SB + u * kFusedBlock + t: a wave-uniform part
+  // (the bases below plus i * GS + u * kFusedBlock) and the lane's t.
+  const char* xw = static_cast<const char*>(x) + static_cast<int64_t>(blockIdx.x) * SB * EB;
+  uint8_t* qw = q + static_cast<int64_t>(blockIdx.x) * SB * 8;
+  const uint32_t xo = threadIdx.x * EB, qo = threadIdx.x * 8;
+
+  // Pass 1: |x| max; streamed steps first, then the held steps into r[].
+  float m = 0.0f;
+  for (int64_t i = 0; i < held0; ++i) {
+    Raw8<DT> v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = ld8_at<DT>(xw + (i * GS + u * kFusedBlock) * EB, xo);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float f[8];
+      cvt8<DT>(v[u], f);
+      m = absmax8(f, m);
+    }
+  }
+  // Held steps through buffer resources bounded at the end of x (the
+  // workgroup's part of a step: SB chunks from chunk c0 + b * SB).
+  // Steps wholly past the end (the workgroup's part starts at or after chunk
+  // n8) are skipped with a workgroup-uniform branch.
+  const int64_t cb = static_cast<int64_t>(blockIdx.x) * SB;
+  Raw8<DT> r[HS * U];
+#pragma unroll
+  for (int k = 0; k < HS; ++k) {
+    const int64_t c0 = (held0 + k) * GS + cb;
+    const int64_t left = n8 - c0;                     // chunks of x from the step's base
+    // one step's loads in flight at a time (the scheduler would otherwise
+    // hoist the loads of every held step)
+    __builtin_amdgcn_sched_barrier(0);
+    if (left > 0) {
+      const auto rs = rsrc(static_cast<const char*>(x) + c0 * EB, (left < SB ? left : SB) * EB);
+#pragma unroll
+      for (int u = 0; u < U; ++u) r[k * U + u] = ld8_buf<DT>(rs, u * kFusedBlock * EB + xo);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float f[8];
+        cvt8<DT>(r[k * U + u], f);
+        m = absmax8(f, m);
+      }
+    }
+  }
+  float tail = 0.0f;                                  // the < 8 trailing elements
+  if (blockIdx.x == 0 && threadIdx.x < 8 && n8 * 8 + threadIdx.x < n) {
+    tail = ld1<DT>(x, n8 * 8 + threadIdx.x);
+    m = fmaxf(m, __builtin_fabsf(tail));
+  }
+  // Pass 2 converts the held chunks again from their raw words (keeping the
+  // first conversion live would take 8 registers per chunk instead of 4).
+#pragma unroll
+  for (int j = 0; j < HS * U; ++j) reload_barrier<DT>(r[j]);
+  const float amax = grid_max_exchange(block_max(m, red), ctl, spin_limit, red);
+  const float inv = amax == amax ? inv_scale(amax, eps, kQ) : amax;
+  if (threadIdx.x == 0 && (blockIdx.x == 0 || inv != inv)) *scale_out = 1.0f / inv;
+
+  // Pass 2: cast the held steps from registers, then re-read the others.
+#pragma unroll
+  for (int k = 0; k < HS; ++k) {
+    const int64_t c0 = (held0 + k) * GS + cb;
+    const int64_t left = n8 - c0;
+    if (left > 0) {
+      const auto rs = rsrc(q + c0 * 8, (left < SB ? left : SB) * 8);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        cast_store8_buf<DT, FP8>(r[k * U + u], inv, rs, u * kFusedBlock * 8 + qo);
+    }
+  }
+  for (int64_t i = 0; i < held0; ++i) {
+    Raw8<DT> v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = ld8_at<DT>(xw + (i * GS + u * kFusedBlock) * EB, xo);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      cast_store8<DT, FP8>(v[u], inv, qw + (i * GS + u * kFusedBlock) * 8, qo);
+  }
+  if (blockIdx.x == 0 && threadIdx.x < 8 && n8 * 8 + threadIdx.x < n) {
+    const float v = tail * inv;
+    q[n8 * 8 + threadIdx.x] = FP8 ? q_fp8_1(v) : static_cast<uint8_t>(q_int8(v));
   }
 }
 
@@ -659,10 +905,49 @@ int64_t tensor_grid(int64_t n, bool vec) {
   return g < 1 ? 1 : g;
 }
 
+// Polls a one-launch wait makes before giving up: kFusedSpinLimit, or the
+// CBQ_TENSOR_SPIN_LIMIT environment variable read at the first call (a host
+// switch that lets tests exercise the timeout path with every kernel still
+// ending normally).
+uint32_t fused_spin_limit() {
+  static const uint32_t v = [] {
+    const char* e = getenv("CBQ_TENSOR_SPIN_LIMIT");
+    if (!e || !*e) return kFusedSpinLimit;
+    return static_cast<uint32_t>(strtoul(e, nullptr, 10));
+  }();
+  return v;
+}
+
+// True if one workgroup of the one-launch kernel fits on a CU, i.e. a grid
+// of one workgroup per CU is resident at once (cached per device and kernel).
+template <int DT, bool FP8>
+bool fused_fits() {
+  static int cached[64];   // 0 unknown, 1 fits, 2 does not
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  if (cached[dev] == 0) {
+    int nb = 0;
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &nb, reinterpret_cast<const void*>(&k_quant_tensor_1pass<DT, FP8>), kFusedBlock, 0);
+    cached[dev] = (e == hipSuccess && nb >= 1) ? 1 : 2;
+  }
+  return cached[dev] == 1;
+}
+
 template <int DT>
-int tensor_quant_t(const void* x, int64_t n, float eps, float* partial, uint8_t* q, float* scale,
-                   bool fp8, hipStream_t s) {
+int tensor_quant_t(const void* x, int64_t n, float eps, float* partial, char* ctl, uint8_t* q,
+                   float* scale, bool fp8, hipStream_t s) {
   const bool vec = aligned(x, 16) && aligned(q, 8);
+  const char* what = fp8 ? "cbq_quant_fp8_tensor" : "cbq_quant_int8_tensor";
+  if (vec && n >= kFusedMinElems && device_cus() <= kMaxFusedGrid &&
+      (fp8 ? fused_fits<DT, true>() : fused_fits<DT, false>())) {
+    const dim3 g(static_cast<unsigned>(device_cus())), b(kFusedBlock);
+    if (fp8)
+      k_quant_tensor_1pass<DT, true><<<g, b, 0, s>>>(x, n, eps, q, scale, ctl, fused_spin_limit());
+    else
+      k_quant_tensor_1pass<DT, false><<<g, b, 0, s>>>(x, n, eps, q, scale, ctl, fused_spin_limit());
+    return launch_status(what);
+  }
   const int64_t grid = tensor_grid(n, vec);
   const dim3 g(static_cast<unsigned>(grid)), b(kBlock);
   k_amax_tensor<DT><<<g, b, 0, s>>>(x, n, vec ? 1 : 0, partial);
@@ -673,7 +958,7 @@ int tensor_quant_t(const void* x, int64_t n, float eps, float* partial, uint8_t*
     k_cast_tensor<DT, false><<<g, b, 0, s>>>(x, n, vec ? 1 : 0, partial, static_cast<int>(grid),
                                              eps, q, scale);
   }
-  return launch_status(fp8 ? "cbq_quant_fp8_tensor" : "cbq_quant_int8_tensor");
+  return launch_status(what);
 }
 
 size_t tensor_ws_bytes() { return CBQ_WS_CTRL_BYTES + sizeof(float) * kMaxTensorWg; }
@@ -687,11 +972,12 @@ int tensor_quant(const void* x, int dt, int64_t n, float eps, void* ws, size_t w
   CBQ_REQUIRE(x && q && scale, "%s: null pointer", what);
   CBQ_REQUIRE(ws && ws_bytes >= tensor_ws_bytes() && aligned(ws, 16),
               "%s: workspace must be >= %zu bytes, 16-byte aligned", what, tensor_ws_bytes());
-  float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + CBQ_WS_CTRL_BYTES);
+  char* ctl = static_cast<char*>(ws);
+  float* partial = reinterpret_cast<float*>(ctl + CBQ_WS_CTRL_BYTES);
   switch (dt) {
-    case kF16: return tensor_quant_t<kF16>(x, n, eps, partial, q, scale, fp8, s);
-    case kBF16: return tensor_quant_t<kBF16>(x, n, eps, partial, q, scale, fp8, s);
-    default: return tensor_quant_t<kF32>(x, n, eps, partial, q, scale, fp8, s);
+    case kF16: return tensor_quant_t<kF16>(x, n, eps, partial, ctl, q, scale, fp8, s);
+    case kBF16: return tensor_quant_t<kBF16>(x, n, eps, partial, ctl, q, scale, fp8, s);
+    default: return tensor_quant_t<kF32>(x, n, eps, partial, ctl, q, scale, fp8, s);
   }
 }
 

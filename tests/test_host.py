@@ -336,7 +336,46 @@ def test_state_dict_saves_reference_layout():
 
 
 def test_oracle_not_imported_by_product():
-    """The product package never imports the oracle (test infrastructure)."""
-    for p in (ROOT / "cublade_amd").rglob("*.py"):
-        text = p.read_text()
-        assert "import oracle" not in text and "from oracle" not in text, p
+    """The product packages never import the oracle (test infrastructure)."""
+    for pkg in ("cublade_amd", "cublade"):
+        for p in (ROOT / pkg).rglob("*.py"):
+            text = p.read_text()
+            assert "import oracle" not in text and "from oracle" not in text, p
+
+
+def test_reference_import_name_resolves_without_gpu():
+    """``cublade.*`` (the reference's import name, quantization/__init__.py:1-17,
+    bindings/cuda/__init__.py:1-4, _loader.py:24-125) names the modules of
+    cublade_amd themselves, with bindings.cuda -> bindings.hip."""
+    import importlib
+
+    import cublade
+    import cublade_amd
+    from cublade.quantization import (QuantizedTensor, cuBladeW8A16LinearLayer,
+                                      dequantize_tensor, detect_outlier_columns, quantize_model,
+                                      quantize_tensor, separate_outliers,
+                                      split_weights_by_outliers)
+    from cublade._loader import CSRC, is_loaded, load_cuda_module, load_error
+    from cublade.bindings.cuda.quantize_fp8 import quantize_per_tensor_fp8
+    from cublade.bindings.cuda.dequantize_int8 import dequantize_per_group_int8
+    q = cublade_amd.quantization
+    assert (quantize_tensor, dequantize_tensor, QuantizedTensor, quantize_model) == (
+        q.quantize_tensor, q.dequantize_tensor, q.QuantizedTensor, q.quantize_model)
+    assert cuBladeW8A16LinearLayer is q.cuBladeW8A16LinearLayer
+    assert (detect_outlier_columns, separate_outliers, split_weights_by_outliers) == (
+        q.detect_outlier_columns, q.separate_outliers, q.split_weights_by_outliers)
+    assert load_cuda_module is cublade_amd._loader.load_hip_module
+    assert CSRC == cublade_amd._loader.CSRC and is_loaded is cublade_amd._loader.is_loaded
+    assert load_error is cublade_amd._loader.load_error
+    assert quantize_per_tensor_fp8 is cublade_amd.bindings.hip.quantize_per_tensor_fp8
+    assert dequantize_per_group_int8 is cublade_amd.bindings.hip.dequantize_per_group_int8
+    assert cublade.bindings.cuda is cublade_amd.bindings.hip
+    assert importlib.import_module("cublade.quantization.linear") is \
+        importlib.import_module("cublade_amd.quantization.linear")
+    # the real module keeps its own spec
+    assert cublade.quantization.__spec__.name == "cublade_amd.quantization"
+    assert cublade.quantize_tensor is quantize_tensor
+    assert cublade.quantize_per_tensor_int8 is cublade_amd.bindings.hip.quantize_per_tensor_int8
+    for missing in ("cublade.kernels", "cublade.bindings.triton"):
+        with pytest.raises(ImportError):
+            importlib.import_module(missing)
