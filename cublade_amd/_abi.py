@@ -44,6 +44,7 @@ SIGNATURES = {
     "cbq_quant_tensor_ws_bytes": (_SZ, []),
     "cbq_quant_int8_channel_ws_bytes": (_SZ, [_I64, _I64, _I32]),
     "cbq_quant_fp8_tensor": (_I32, [_P, _I32, _I64, _F, _P, _SZ, _P, _P, _P]),
+    "cbq_quant_fp8_tensor_noalloc": (_I32, [_P, _I32, _I64, _F, _P, _P, _P]),
     "cbq_dequant_fp8_tensor": (_I32, [_P, _P, _I64, _P, _I32, _P]),
     "cbq_quant_int8_tensor": (_I32, [_P, _I32, _I64, _F, _P, _SZ, _P, _P, _P]),
     "cbq_quant_int8_channel": (_I32, [_P, _I32, _I64, _I64, _I32, _F, _P, _SZ, _P, _P, _P]),

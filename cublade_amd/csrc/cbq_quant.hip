@@ -47,6 +47,7 @@
 // Numerics: see cbq_device.h. Every kernel guards its indices against the
 // sizes it is given; the entry points check shapes, dtypes and alignment.
 #include <cstdlib>
+#include <mutex>
 
 #include "cbq_device.h"
 #include "cbq_host.h"
@@ -961,7 +962,7 @@ int tensor_quant_t(const void* x, int64_t n, float eps, float* partial, char* ct
   return launch_status(what);
 }
 
-size_t tensor_ws_bytes() { return CBQ_WS_CTRL_BYTES + sizeof(float) * kMaxTensorWg; }
+constexpr size_t tensor_ws_bytes() { return CBQ_WS_CTRL_BYTES + sizeof(float) * kMaxTensorWg; }
 
 int tensor_quant(const void* x, int dt, int64_t n, float eps, void* ws, size_t ws_bytes,
                  uint8_t* q, float* scale, bool fp8, hipStream_t s) {
@@ -1188,7 +1189,68 @@ int seg_quant_t(const void* x, int64_t outer, int64_t channels, int64_t inner, f
 }  // namespace
 }  // namespace cbq
 
+// ---------------------------------------------------------------------------
+// Scratch of cbq_quant_fp8_tensor_noalloc: the per-tensor workspace (control
+// block + partial maxima) as device memory of the library, one copy per GPU,
+// held until the process ends. Zero-initialised when the code object loads,
+// which is the state the exchange protocol starts from; every call leaves it
+// valid for the next (see k_quant_tensor_1pass), so nothing is cleared per
+// call. Host code uses only the per-device address from hipGetSymbolAddress.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t kNoAllocScratchBytes = 24576;
+static_assert(cbq::tensor_ws_bytes() <= kNoAllocScratchBytes, "scratch too small");
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};
+
+// Address of this device's copy of scratch (looked up once per device, with
+// the device current).
+int scratch_for_current_device(void** out, const char* what) {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  CBQ_REQUIRE(e == hipSuccess && dev >= 0 && dev < 64, "%s: no current HIP device (%s)", what,
+              hipGetErrorString(e));
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t g = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (g != hipSuccess || !p) {
+      cbq::set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", what, dev,
+                     hipGetErrorString(g));
+      return CBQ_ELAUNCH;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return CBQ_OK;
+}
+}  // namespace
+
 using namespace cbq;
+
+extern "C" int cbq_quant_fp8_tensor_noalloc(const void* x, int dtype, int64_t n, float eps,
+                                            uint8_t* q, float* scale, cbq_stream_t stream) {
+  clear_error();
+  const char* what = "cbq_quant_fp8_tensor_noalloc";
+  // argument checks before any device call (as in tensor_quant)
+  CBQ_REQUIRE(valid_dtype(dtype, false), "%s: unsupported input dtype code %d", what, dtype);
+  CBQ_REQUIRE(n >= 0, "%s: negative element count", what);
+  if (n == 0) return CBQ_OK;
+  CBQ_REQUIRE(x && q && scale, "%s: null pointer", what);
+  CBQ_REQUIRE(tensor_ws_bytes() <= kNoAllocScratchBytes,
+              "%s: needs %zu bytes of scratch, the static array holds %zu", what,
+              tensor_ws_bytes(), kNoAllocScratchBytes);
+  void* ws = nullptr;
+  const int rc = scratch_for_current_device(&ws, what);
+  if (rc != CBQ_OK) return rc;
+  return tensor_quant(x, dtype, n, eps, ws, kNoAllocScratchBytes, q, scale, true,
+                      as_stream(stream));
+}
 
 extern "C" int cbq_quant_fp8_tensor(const void* x, int dtype, int64_t n, float eps, void* ws,
                                     size_t ws_bytes, uint8_t* q, float* scale,

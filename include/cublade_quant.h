@@ -77,6 +77,18 @@ int cbq_quant_fp8_tensor(const void* x, int dtype, int64_t n, float eps,
                          void* ws, size_t ws_bytes, uint8_t* q, float* scale,
                          cbq_stream_t stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): cbq_quant_fp8_tensor without the workspace argument, same
+ * kernels and results. Its workspace is a 24 KiB static device array inside
+ * the library, one per GPU, held until the process ends and shared by every
+ * call on that GPU: calls that overlap in time on one GPU (other streams,
+ * other threads) race and must be serialised by the caller. Allocates nothing;
+ * the first call on a device looks the array's address up
+ * (hipGetSymbolAddress), so make that call outside graph capture. */
+int cbq_quant_fp8_tensor_noalloc(const void* x, int dtype, int64_t n, float eps,
+                                 uint8_t* q, float* scale, cbq_stream_t stream);
+
 /* Replaces dequantize_per_tensor_fp8_cuda (dequantize_per_tensor_fp8.cu:84-109;
  * kernel :23-66), bound as dequantize_fp8.dequantize_per_tensor_fp8
  * (bindings/cuda/dequantize_fp8.py:15-35). out_dtype: CBQ_F16 or CBQ_BF16. */

@@ -34,7 +34,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     L = _lib()
     names = declared_symbols()
-    assert len(names) == 21
+    assert len(names) == 22
     for n in names:
         assert hasattr(L, n), n
     from cublade_amd import _abi
@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_slot():
     L = _lib()
-    assert L.cbq_abi_version() == 103
+    assert L.cbq_abi_version() == 104
     assert L.cbq_last_error() in (b"",) or isinstance(L.cbq_last_error(), bytes)
 
 
@@ -58,6 +58,11 @@ def test_abi_rejects_bad_arguments_without_device_work():
     P = ctypes.c_void_p
     fake = P(0x1000)
     _einval(L.cbq_quant_fp8_tensor(fake, 0, 16, 1e-12, fake, 256, fake, fake, None), "dtype")
+    # the allocation-free variant checks its arguments before any device call
+    _einval(L.cbq_quant_fp8_tensor_noalloc(fake, 0, 16, 1e-12, fake, fake, None), "dtype")
+    _einval(L.cbq_quant_fp8_tensor_noalloc(None, 2, 16, 1e-12, fake, fake, None), "null")
+    _einval(L.cbq_quant_fp8_tensor_noalloc(fake, 2, -1, 1e-12, fake, fake, None), "negative")
+    assert L.cbq_quant_fp8_tensor_noalloc(None, 2, 0, 1e-12, None, None, None) == 0
     _einval(L.cbq_quant_int8_tensor(fake, 1, 16, 1e-12, fake, 1024, fake, fake, None), "workspace")
     _einval(L.cbq_quant_int8_group(fake, 2, 4, 0, 1e-12, fake, fake, None), "group_size")
     _einval(L.cbq_quant_int8_group(fake, 2, 4, 4097, 1e-12, fake, fake, None), "group_size")
