@@ -2,36 +2,43 @@
 
 Workload: per-tensor symmetric INT8 of an fp16
 [8192, 8192] tensor of 0.5 * Student-t(df=3) values, seed 1. One step is the
-whole hot path over that tensor through the public API: quantize_tensor
-(amax kernel + cast kernel) then dequantize_tensor (dequant kernel).
+whole hot path over that tensor through the public API: quantize_tensor (one
+launch of k_quant_tensor_1pass) then dequantize_tensor (k_deq_tensor).
 
-Timing: inputs resident in HBM. Before each timed phase a read-only sweep of
-a 512 MiB buffer evicts the 256 MB Infinity Cache and the L2s (leaving clean
-lines) and keeps the GPU busy while the host enqueues the phase; each phase
-is timed with HIP events on its launch stream, the sweep outside the events.
-value = algorithmic bytes of the K steps / summed phase time (GB/s).
-Algorithmic bytes per step (N = 67,108,864): amax 2N + cast 2N + N + 4 +
-dequant N + 2N + 4 = 536,870,920.
+Timing: inputs resident in HBM. Before each timed phase a sweep of a 512 MiB
+buffer evicts the 256 MB Infinity Cache and the L2s and keeps the GPU busy
+while the host enqueues the phase; each phase is timed with HIP events on its
+launch stream, the sweep outside the events. The headline uses a read-only
+sweep (clean cache lines); the same steps are then repeated after a write
+sweep (every line dirty, the worst case after a large producer) and reported
+next to it as "dirty".
 
-Roofline: the dequant kernel k_deq_tensor<int8, fp16>, the longest of the
-three. Algorithmic bytes per launch: N codes read + 2N output bytes written +
-4 scale bytes = 201,326,596 B. Its duration is measured live as the mean of
-ROOF_LAUNCHES back-to-back launches between two HIP events on the launch
-stream, after a cache sweep, each launch on its own copy of the codes and its
-own output: ROOF_LAUNCHES x 201 MB = 2 GB of distinct buffers, so no launch
-finds its codes, or the lines it writes, in the 256 MB Infinity Cache (the
-steady-state HBM rate); peak 8 TB/s. traffic: HBM bytes per launch from
-rocprofv3 FETCH_SIZE + WRITE_SIZE runs, read from
-profiles/dequant_int8_c2_traffic.json when present (null otherwise).
+Algorithmic bytes (N = 67,108,864 elements): each op's minimum HBM traffic,
+quant 2N read + N codes + 4 scale bytes, dequant N + 4 read + 2N written;
+6N + 8 = 402,653,192 bytes per step. value = those bytes of the K steps /
+the summed phase time (GB/s).
 
-Extra keys: per-phase GB/s, the W8A16 linear at M = 4096 (BASELINE
-configs[4]) in TFLOP/s against the 2.5 PFLOP/s dense fp16 MFMA peak, and
-copy_ceiling: a plain device-to-device copy moving the roofline kernel's
-byte count, timed the same way (distinct buffers per launch), the
-achievable HBM rate next to the 8 TB/s spec.
+Roofline: every kernel of the step is timed live as the mean of ROOF_LAUNCHES
+back-to-back launches between two HIP events on the launch stream, after one
+cache sweep, each launch on its own input and output buffers (about 2 GB of
+distinct buffers per kernel, so no launch finds its data in the 256 MB
+Infinity Cache); `roofline` reports the longest one (the quant kernel),
+`kernels` all of them. achieved = the kernel's algorithmic bytes per launch /
+its mean launch time; peak 8 TB/s. traffic: HBM bytes per launch from
+rocprofv3 FETCH_SIZE and WRITE_SIZE runs of this script, calibrated on a
+256 MiB device copy (profiles/quant_int8_c2_traffic.json; null if absent).
 
-cpu_baseline: the C oracle (test infrastructure, single thread) on the first
-8,388,608 elements of the same tensor, repeated for about 10 s.
+Extras, timed in the same run (HIP events around each op after a clean
+sweep, median of EXTRA_REPS): every other BASELINE config (C1 FP8 per
+tensor, C3 per channel on both axes, C4 per group, W8A16 at M = 16, 256 and
+4096). Their inputs follow the configs' distributions but are drawn on the
+GPU (torch's device generator), which makes no difference to the timing of
+these data-independent kernels; the parity tests use the CPU-seeded recipes.
+
+cpu_baseline: the torch CPU restatement of the same formulas
+(oracle/torch_cpu.py) on the full workload tensor, torch.set_num_threads(
+os.cpu_count()), one warm-up then the median of CPU_REPS quant + dequant
+steps, with its codes and outputs compared to the GPU's.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -41,6 +48,7 @@ import argparse
 import dataclasses
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -52,12 +60,13 @@ os.environ.setdefault("CUBLADE_SKIP_WARMUP", "1")
 HBM_PEAK = 8.0e12
 FP16_PEAK = 2.5e15
 N_ELEM = 8192 * 8192
-BYTES_AMAX = 2 * N_ELEM
-BYTES_CAST = 2 * N_ELEM + N_ELEM + 4
-BYTES_DEQ = N_ELEM + 2 * N_ELEM + 4
-BYTES_STEP = BYTES_AMAX + BYTES_CAST + BYTES_DEQ
+BYTES_QUANT = 2 * N_ELEM + N_ELEM + 4
+BYTES_DEQ = N_ELEM + 4 + 2 * N_ELEM
+BYTES_STEP = BYTES_QUANT + BYTES_DEQ
 ROOF_LAUNCHES = 10
-TRAFFIC_FILE = ROOT / "profiles" / "dequant_int8_c2_traffic.json"
+EXTRA_REPS = 10
+CPU_REPS = 3
+TRAFFIC_FILE = ROOT / "profiles" / "quant_int8_c2_traffic.json"
 
 
 def parse():
@@ -66,36 +75,49 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-w8a16", action="store_true", help="skip the W8A16 extra")
-    ap.add_argument("--flush", default="clean", choices=["clean", "dirty"])
+    ap.add_argument("--no-extras", action="store_true", help="skip the other configs")
+    ap.add_argument("--no-w8a16", action="store_true", help="skip the W8A16 extras")
     return ap.parse_args()
 
 
-def cpu_baseline(x_cpu):
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(x_cpu, q_gpu, y_gpu):
     import numpy as np
     import torch
 
-    import oracle
+    from oracle import torch_cpu
 
-    sample = x_cpu.reshape(-1)[: 8 * 1024 * 1024].contiguous()
-    xb = sample.view(torch.int16).numpy().view(np.uint16)
-    n = xb.size
-    t_total, reps = 0.0, 0
-    while t_total < 10.0 and reps < 500:
+    torch.set_num_threads(os.cpu_count() or 1)
+    times = []
+    for r in range(CPU_REPS + 1):
         t0 = time.perf_counter()
-        q, s = oracle.quant_int8_tensor(xb, oracle.F16)
-        oracle.dequant_int8_tensor(q, s, oracle.F16)
-        t_total += time.perf_counter() - t0
-        reps += 1
-    per_elem = 2 + 3 + 3
+        q, s = torch_cpu.quant_tensor(x_cpu, torch.int8)
+        y = torch_cpu.dequant_tensor(q, s, torch.float16)
+        dt = time.perf_counter() - t0
+        if r:
+            times.append(dt)
+    med = statistics.median(times)
+    same = bool(torch.equal(q, q_gpu.cpu())) and bool(
+        np.array_equal(y.view(torch.int16).numpy(), y_gpu.cpu().view(torch.int16).numpy()))
     return {
-        "value": round(per_elem * n * reps / t_total / 1e9, 3),
+        "value": round(BYTES_STEP / med / 1e9, 3),
         "unit": "GB/s",
-        "cores": 1,
+        "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"C oracle (oracle/cbq_oracle.c, 1 thread) quant+dequant of the first "
-                  f"{n} elements of the workload tensor, {reps} reps, {t_total:.1f} s; "
-                  f"host {os.cpu_count()} logical CPUs",
+        "sample": f"the full workload tensor ({N_ELEM} fp16 elements): torch CPU restatement "
+                  f"(oracle/torch_cpu.py) of quant + dequant, median of {CPU_REPS} steps after "
+                  f"1 warm-up, {med * 1e3:.1f} ms per step; os.cpu_count() = {os.cpu_count()}, "
+                  f"torch threads = {torch.get_num_threads()}, CPU: {cpu_model()}; codes and "
+                  f"outputs bit-identical to the GPU's: {same}",
     }
 
 
@@ -119,8 +141,8 @@ def timed_rotation(torch, stream, flush, ev, fns):
 
 def copy_ceiling(torch, dev, stream, flush, ev):
     """Achievable HBM rate next to the 8 TB/s spec: the runtime's
-    device-to-device copy moving the roofline kernel's byte count (half
-    read, half written), over ROOF_LAUNCHES distinct buffer pairs."""
+    device-to-device copy moving the dequant kernel's byte count (half read,
+    half written), over ROOF_LAUNCHES distinct buffer pairs."""
     nbytes = (BYTES_DEQ - 4) // 2
     pairs = [(torch.ones(nbytes, dtype=torch.uint8, device=dev),
               torch.empty(nbytes, dtype=torch.uint8, device=dev)) for _ in range(ROOF_LAUNCHES)]
@@ -133,23 +155,71 @@ def copy_ceiling(torch, dev, stream, flush, ev):
             "frac": round(gbs * 1e9 / HBM_PEAK, 4)}
 
 
-def w8a16_extra(torch, reps):
+def _rate(bytes_, us):
+    return {"us": round(us, 2), "gbs": round(bytes_ / us / 1e3, 1),
+            "hbm_frac": round(bytes_ / (us * 1e-6) / HBM_PEAK, 4)}
+
+
+def extras(torch, dev, no_w8a16):
+    """Every other BASELINE config through the public API, op-level HIP
+    event times after a clean sweep (median of EXTRA_REPS)."""
     from cublade_amd.benchmark import configs
     from cublade_amd.benchmark.core import MallFlush, time_op
-    from cublade_amd.quantization import cuBladeW8A16LinearLayer
+    from cublade_amd.quantization import (cuBladeW8A16LinearLayer, dequantize_tensor,
+                                          quantize_tensor)
 
-    dev = torch.device("cuda")
-    x, w = configs.c5_w8a16(4096)
-    N, K = w.shape
-    layer = cuBladeW8A16LinearLayer(K, N, bias=False, dtype=torch.float16)
-    layer.quantize(w.to(dev))
-    xd = x.to(dev)
-    us = time_op(lambda: layer(xd), reps, 2, MallFlush(dev))
-    us_med = sorted(us)[len(us) // 2]
-    flops = 2.0 * 4096 * N * K
-    return {"w8a16_m4096_us": round(us_med, 2),
-            "w8a16_m4096_tflops": round(flops / us_med / 1e6, 2),
-            "w8a16_m4096_mfma_frac": round(flops / (us_med * 1e-6) / FP16_PEAK, 4)}
+    flush = MallFlush(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    out = {}
+
+    def qdq(name, x, qkw, q_bytes, dq_bytes):
+        qt = quantize_tensor(x, **qkw)
+        tq = statistics.median(time_op(lambda: quantize_tensor(x, **qkw), EXTRA_REPS, 2, flush))
+        td = statistics.median(time_op(lambda: dequantize_tensor(qt), EXTRA_REPS, 2, flush))
+        out[name] = {"quant": _rate(q_bytes, tq), "dequant": _rate(dq_bytes, td)}
+        print(f"[bench] {name}: quant {tq:.1f} us, dequant {td:.1f} us", file=sys.stderr,
+              flush=True)
+
+    x = torch.randn(4096, 4096, device=dev, generator=g).bfloat16()
+    n = x.numel()
+    qdq("c1_fp8_tensor_bf16_4096x4096", x, dict(dtype=torch.float8_e4m3fn, mode="tensor"),
+        3 * n + 4, 3 * n + 4)
+    del x
+    x = 0.02 * torch.randn(28672, 8192, device=dev, generator=g)
+    cols = torch.randperm(8192, device=dev, generator=g)[:8]
+    x[:, cols] *= 20
+    x = x.bfloat16()
+    n, C, F = x.numel(), x.shape[0], x.shape[1]
+    qdq("c3_channel_axis0_bf16_28672x8192", x, dict(dtype=torch.int8, mode="channel", ch_axis=0),
+        3 * n + 4 * C, 3 * n + 4 * C)
+    qdq("c3_channel_axis1_bf16_28672x8192", x, dict(dtype=torch.int8, mode="channel", ch_axis=1),
+        3 * n + 4 * F, 3 * n + 4 * F)
+    del x
+    x = torch.randn(16384, 14336, device=dev, generator=g)
+    x *= 0.1 + 9.9 * torch.rand(16384, 1, device=dev, generator=g)
+    x = x.bfloat16()
+    n = x.numel()
+    qdq("c4_group128_bf16_16384x14336", x,
+        dict(dtype=torch.int8, mode="group", group_size=128, ch_axis=-1),
+        3 * n + 4 * (n // 128), 3 * n + 4 * (n // 128))
+    del x
+    if not no_w8a16:
+        for M in (16, 256, 4096):
+            xa, w = configs.c5_w8a16(M)
+            N, K = w.shape
+            layer = cuBladeW8A16LinearLayer(K, N, bias=False, dtype=torch.float16)
+            layer.quantize(w.to(dev))
+            xd = xa.to(dev)
+            us = statistics.median(time_op(lambda: layer(xd), EXTRA_REPS, 2, flush))
+            flops = 2.0 * M * N * K
+            bytes_ = N * K + 2 * N + 2 * M * K + 2 * M * N
+            out[f"c5_w8a16_m{M}"] = {"us": round(us, 2), "tflops": round(flops / us / 1e6, 2),
+                                     "mfma_frac": round(flops / (us * 1e-6) / FP16_PEAK, 4),
+                                     "gbs": round(bytes_ / us / 1e3, 1),
+                                     "hbm_frac": round(bytes_ / (us * 1e-6) / HBM_PEAK, 4)}
+            print(f"[bench] w8a16 M={M}: {us:.1f} us", file=sys.stderr, flush=True)
+            del layer, xd
+    return out
 
 
 def load_traffic():
@@ -171,58 +241,79 @@ def main():
     from cublade_amd import _abi
     from cublade_amd.benchmark import configs
     from cublade_amd.benchmark.core import MallFlush
+    from cublade_amd.bindings.hip import quantize_per_tensor_int8
     from cublade_amd.quantization import dequantize_tensor, quantize_tensor
 
     _abi.lib()
     dev = torch.device("cuda:0")
     x_cpu = configs.c2_int8_tensor()
     x = x_cpu.to(dev)
-    flush = MallFlush(dev, mode=args.flush)
     stream = torch.cuda.current_stream(dev)
 
     def ev():
         return torch.cuda.Event(enable_timing=True)
 
-    def step(t_q, t_d):
-        flush()
-        e0, e1, e2, e3 = ev(), ev(), ev(), ev()
-        e0.record(stream)
-        qt = quantize_tensor(x, dtype=torch.int8, mode="tensor")
-        e1.record(stream)
-        flush()
-        e2.record(stream)
-        y = dequantize_tensor(qt)
-        e3.record(stream)
-        t_q.append((e0, e1))
-        t_d.append((e2, e3))
-        return qt, y
+    def run_steps(flush, nsteps, nwarm):
+        def step(t_q, t_d):
+            flush()
+            e0, e1, e2, e3 = ev(), ev(), ev(), ev()
+            e0.record(stream)
+            qt = quantize_tensor(x, dtype=torch.int8, mode="tensor")
+            e1.record(stream)
+            flush()
+            e2.record(stream)
+            y = dequantize_tensor(qt)
+            e3.record(stream)
+            t_q.append((e0, e1))
+            t_d.append((e2, e3))
+            return qt, y
 
-    for _ in range(args.warmup):
-        step([], [])
-    torch.cuda.synchronize()
+        for _ in range(nwarm):
+            step([], [])
+        torch.cuda.synchronize()
+        tq, td = [], []
+        for _ in range(nsteps):
+            qt, y = step(tq, td)
+        torch.cuda.synchronize()
+        q_ms = [a.elapsed_time(b) for a, b in tq]
+        d_ms = [a.elapsed_time(b) for a, b in td]
+        return qt, y, q_ms, d_ms
 
-    tq, td = [], []
-    torch.cuda.synchronize()
+    clean = MallFlush(dev, mode="clean")
     w0 = time.perf_counter()
-    for _ in range(args.steps):
-        qt, y = step(tq, td)
-    torch.cuda.synchronize()
+    qt, y, q_ms, d_ms = run_steps(clean, args.steps, args.warmup)
     wall = time.perf_counter() - w0
-    q_ms = [a.elapsed_time(b) for a, b in tq]
-    d_ms = [a.elapsed_time(b) for a, b in td]
     sum_s = (sum(q_ms) + sum(d_ms)) / 1e3
     value = BYTES_STEP * args.steps / sum_s / 1e9
     quant_us = sum(q_ms) / len(q_ms) * 1e3
     deq_us = sum(d_ms) / len(d_ms) * 1e3
 
-    # roofline kernel: back-to-back dequant launches after one sweep, each on
-    # its own copy of the codes (2 GB of distinct inputs and outputs)
+    dirty = MallFlush(dev, mode="dirty")
+    _, _, q_ms2, d_ms2 = run_steps(dirty, args.steps, 1)
+    del dirty
+    quant_us2 = sum(q_ms2) / len(q_ms2) * 1e3
+    deq_us2 = sum(d_ms2) / len(d_ms2) * 1e3
+
+    # every kernel of the step, back to back on distinct buffers
+    xs = [x.clone() for _ in range(ROOF_LAUNCHES)]
+    quant_kernel_us = timed_rotation(torch, stream, clean, ev,
+                                     [lambda t=t: quantize_per_tensor_int8(t) for t in xs])
+    del xs
     qts = [dataclasses.replace(qt, data=qt.data.clone()) for _ in range(ROOF_LAUNCHES)]
-    roof_us = timed_rotation(torch, stream, flush, ev,
-                             [lambda t=t: dequantize_tensor(t) for t in qts])
+    deq_kernel_us = timed_rotation(torch, stream, clean, ev,
+                                   [lambda t=t: dequantize_tensor(t) for t in qts])
     del qts
-    achieved = BYTES_DEQ / (roof_us * 1e-6) / 1e9
-    copy = copy_ceiling(torch, dev, stream, flush, ev)
+    kernels = {
+        "k_quant_tensor_1pass<fp16, int8>": {"bytes_per_launch": BYTES_QUANT,
+                                             **_rate(BYTES_QUANT, quant_kernel_us)},
+        "k_deq_tensor<int8, fp16>": {"bytes_per_launch": BYTES_DEQ,
+                                     **_rate(BYTES_DEQ, deq_kernel_us)},
+    }
+    roof_name = max(kernels, key=lambda k: kernels[k]["us"])
+    roof = kernels[roof_name]
+    achieved = roof["bytes_per_launch"] / (roof["us"] * 1e-6) / 1e9
+    copy = copy_ceiling(torch, dev, stream, clean, ev)
+    status = _abi.tensor_quant_status(dev)
 
     out = {
         "metric": "quant/dequant HBM GB/s (% of peak) at 1 MI355X; W8A16 TFLOPS at M=4096",
@@ -239,23 +330,35 @@ def main():
         "data": "synthetic (BASELINE configs[1] recipe, seed 1)",
         "config": {"workload": "INT8 per-tensor quantize_tensor + dequantize_tensor, fp16 "
                                "[8192, 8192] 0.5*t(df=3), seed 1 (BASELINE configs[1])",
+                   "bytes_per_step": BYTES_STEP,
                    "hbm_frac": round(value * 1e9 / HBM_PEAK, 4),
-                   "cache_sweep": args.flush},
+                   "cache_sweep": "clean (read-only 512 MiB sweep before each phase)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": round(achieved * 1e9 / HBM_PEAK, 4),
-                     "traffic": load_traffic(), "kernel": "k_deq_tensor<int8, fp16>",
-                     "bytes_per_launch": BYTES_DEQ, "avg_launch_us": round(roof_us, 2)},
-        "copy_ceiling": copy,
+                     "traffic": load_traffic(), "kernel": roof_name,
+                     "bytes_per_launch": roof["bytes_per_launch"], "avg_launch_us": roof["us"]},
+        "kernels": kernels,
         "phases": {"quant_us": round(quant_us, 2),
-                   "quant_gbs": round((BYTES_AMAX + BYTES_CAST) / quant_us / 1e3, 2),
+                   "quant_gbs": round(BYTES_QUANT / quant_us / 1e3, 2),
                    "dequant_us": round(deq_us, 2),
                    "dequant_gbs": round(BYTES_DEQ / deq_us / 1e3, 2)},
+        "dirty": {"what": "the same steps after a write sweep (every cache line dirty)",
+                  "value": round(BYTES_STEP / ((quant_us2 + deq_us2) * 1e-6) / 1e9, 2),
+                  "quant_us": round(quant_us2, 2), "dequant_us": round(deq_us2, 2)},
+        "copy_ceiling": copy,
+        "exchange_status": status,
         "wall_s_incl_sweeps": round(wall, 3),
     }
-    if not args.no_w8a16:
-        out.update(w8a16_extra(torch, max(3, args.steps // 2)))
+    if not args.no_extras:
+        ex = extras(torch, dev, args.no_w8a16)
+        out["extras"] = ex
+        if "c5_w8a16_m4096" in ex:
+            m = ex["c5_w8a16_m4096"]
+            out["w8a16_m4096_us"] = m["us"]
+            out["w8a16_m4096_tflops"] = m["tflops"]
+            out["w8a16_m4096_mfma_frac"] = m["mfma_frac"]
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(x_cpu)
+        out["cpu_baseline"] = cpu_baseline(x_cpu, qt.data, y)
     print(json.dumps(out), flush=True)
 
 

@@ -2,7 +2,8 @@
 
 Owns: the library handle and its function signatures, dtype codes, the HIP
 stream of the current torch stream, and the per-(device, stream) workspace
-whose first CBQ_WS_CTRL_BYTES bytes are a self-resetting control block.
+whose first CBQ_WS_CTRL_BYTES bytes are the library's control block (zero
+when created; the library keeps state there between calls).
 
 There is no fallback: if the library cannot be built or loaded, every call
 raises.
@@ -57,7 +58,7 @@ SIGNATURES = {
     "cbq_quant_int8_group_nd": (_I32, [_P, _I32, _I64, _I64, _I64, _I64, _F, _P, _P, _P]),
     "cbq_dequant_int8_channel_nd": (_I32, [_P, _P, _I64, _I64, _I64, _P, _I32, _P]),
     "cbq_dequant_int8_group_nd": (_I32, [_P, _P, _I64, _I64, _I64, _I64, _P, _I32, _P]),
-    "cbq_w8a16_ws_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
+    "cbq_w8a16_ws_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I32]),
     "cbq_w8a16_linear": (_I32, [_P, _I32, _P, _P, _P, _P, _I64, _P, _I64, _I64, _I64,
                                 _P, _SZ, _P, _P]),
     "cbq_mm_ws_bytes": (_SZ, [_I64, _I64, _I64, _I32, _I32]),
@@ -123,20 +124,50 @@ def on_device(device: torch.device):
 
 
 _ws: dict[tuple[int, int], torch.Tensor] = {}
+# Workspaces replaced by a larger one. They are never freed: a HIP graph
+# captured on that stream may hold their address (the per-tensor control
+# block, split-K partials) and replays would otherwise write into memory
+# the caching allocator has handed to another tensor.
+_ws_retired: list[torch.Tensor] = []
 _ws_lock = threading.Lock()
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Zero-initialised workspace for (device, current stream), at least
-    ``nbytes`` long. The library leaves its control block zeroed after every
-    call, so the buffer is reused as-is; a larger request replaces it with a
-    fresh zeroed one (allocated on the same stream, hence ordered)."""
+    """Workspace for (device, current stream), at least ``nbytes`` long,
+    zero-filled when created. The library keeps state in its control block
+    between calls (the one-launch per-tensor quant's call count and slots),
+    so the buffer is reused as-is. A larger request replaces it with a fresh
+    zero-filled one (allocated on the same stream, hence ordered); the old
+    one is kept alive for graphs captured with it. Growing during a graph
+    capture raises: run one call of each captured shape on the capture
+    stream first."""
     nbytes = max(int(nbytes), WS_CTRL_BYTES)
     key = (device_index(device), stream_handle(device))
     with _ws_lock:
         buf = _ws.get(key)
         if buf is None or buf.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    f"cublade: the workspace of the capture stream must grow to {nbytes} bytes "
+                    f"during graph capture; run one call of every captured shape on that stream "
+                    f"before capturing")
             size = max(nbytes, 2 * (buf.numel() if buf is not None else 0), 1 << 12)
-            buf = torch.zeros(size, dtype=torch.uint8, device=device)
-            _ws[key] = buf
+            new = torch.zeros(size, dtype=torch.uint8, device=device)
+            if buf is not None:
+                _ws_retired.append(buf)
+            _ws[key] = new
+            buf = new
         return buf
+
+
+def tensor_quant_status(device: torch.device) -> int:
+    """The sticky status word of the one-launch per-tensor quant in the
+    current stream's workspace (0: every exchange completed; 1: a wait timed
+    out and the workspace is poisoned until its control block is zeroed).
+    Synchronises with the device."""
+    key = (device_index(device), stream_handle(device))
+    with _ws_lock:
+        buf = _ws.get(key)
+    if buf is None:
+        return 0
+    return int(buf[512:516].view(torch.int32).item())

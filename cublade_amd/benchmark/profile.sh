@@ -3,17 +3,20 @@
 #
 #   bash cublade_amd/benchmark/profile.sh OUTDIR
 #
-# 1. kernel trace of bench.py (BASELINE configs[1] step + W8A16 M=4096)
-# 2. FETCH_SIZE and WRITE_SIZE of bench.py (one counter per run), and of a
-#    256 MiB device copy (copy_calib.py) to calibrate both counters
-# 3. the per-config suite (configs 1-5, fp32 W8A16 and the next rows): its
-#    HIP-event timings from a run without the profiler (suite.json; the
-#    tracer's per-launch host cost would otherwise show in host-bound ops),
-#    then a kernel trace
+# 1. kernel trace of bench.py (BASELINE configs[1] step, the roofline
+#    rotations and the other configs' extras)
+# 2. FETCH_SIZE and WRITE_SIZE of bench.py (one counter per run) and of a
+#    256 MiB device copy (copy_calib.py) to calibrate both counters: the
+#    headline kernels' HBM bytes per launch
+# 3. the per-config suite: HIP-event timings from a run without the profiler
+#    (suite.json; the tracer's per-launch host cost would otherwise show in
+#    host-bound ops), then a kernel trace, then FETCH_SIZE / WRITE_SIZE runs
+#    of configs 1-5 (every suite kernel's HBM bytes per dispatch)
 # 4. rocprof's derived MfmaUtil counter (MFMA busy cycles over active cycles
 #    x SIMDs) for the MFMA kernels: W8A16 (config 5) and the dense GEMM (f4)
-# Summaries: OUTDIR/bench_c2_kernels.txt, OUTDIR/dequant_int8_c2_traffic.json,
-# OUTDIR/suite_kernels.txt, OUTDIR/suite.json, OUTDIR/mfma_util.txt. Raw
+# Summaries: OUTDIR/bench_c2_kernels.txt, OUTDIR/quant_int8_c2_traffic.json,
+# OUTDIR/dequant_int8_c2_traffic.json, OUTDIR/suite_kernels.txt,
+# OUTDIR/suite_traffic.txt, OUTDIR/suite.json, OUTDIR/mfma_util.txt. Raw
 # databases stay in OUTDIR/raw.
 # Run from the repository root on a GPU machine. Every GPU step has its own
 # time limit; the script stops at the first failing step.
@@ -24,6 +27,7 @@ mkdir -p "$RAW"
 export TMPDIR=/tmp
 PY="python -u"
 R="python -m cublade_amd.benchmark.rocprof"
+BENCH_SHORT="bench.py --no-cpu --no-extras --steps 3 --warmup 1"
 
 step() { echo "[profile] $*"; }
 
@@ -32,10 +36,10 @@ timeout -k 10 300 rocprofv3 --kernel-trace --stats -d "$RAW/trace" -o bench -- \
   $PY bench.py --no-cpu > "$RAW/trace.log" 2>&1 || exit $?
 step "counter FETCH_SIZE: bench.py"
 timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE --kernel-trace -d "$RAW/fetch" -o bench -- \
-  $PY bench.py --no-cpu --no-w8a16 --steps 3 --warmup 1 > "$RAW/fetch.log" 2>&1 || exit $?
+  $PY $BENCH_SHORT > "$RAW/fetch.log" 2>&1 || exit $?
 step "counter WRITE_SIZE: bench.py"
 timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE --kernel-trace -d "$RAW/write" -o bench -- \
-  $PY bench.py --no-cpu --no-w8a16 --steps 3 --warmup 1 > "$RAW/write.log" 2>&1 || exit $?
+  $PY $BENCH_SHORT > "$RAW/write.log" 2>&1 || exit $?
 step "counter FETCH_SIZE: 256 MiB copy"
 timeout -s KILL 60 rocprofv3 --pmc FETCH_SIZE --kernel-trace -d "$RAW/cal_fetch" -o calib -- \
   $PY -m cublade_amd.benchmark.copy_calib > "$RAW/cal_fetch.log" 2>&1 || exit $?
@@ -47,14 +51,20 @@ timeout -k 10 500 $PY -m cublade_amd.benchmark.suite --json "$OUT/suite.json" > 
 step "kernel trace: suite"
 timeout -k 10 500 rocprofv3 --kernel-trace --stats -d "$RAW/suite" -o suite -- \
   $PY -m cublade_amd.benchmark.suite --reps 10 > "$RAW/suite.log" 2>&1 || exit $?
-
+step "counter FETCH_SIZE: suite configs c1-c5"
+timeout -s KILL 300 rocprofv3 --pmc FETCH_SIZE --kernel-trace -d "$RAW/sfetch" -o suite -- \
+  $PY -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5 --reps 3 --warmup 1 > "$RAW/sfetch.log" 2>&1 || exit $?
+step "counter WRITE_SIZE: suite configs c1-c5"
+timeout -s KILL 300 rocprofv3 --pmc WRITE_SIZE --kernel-trace -d "$RAW/swrite" -o suite -- \
+  $PY -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5 --reps 3 --warmup 1 > "$RAW/swrite.log" 2>&1 || exit $?
 step "counter MfmaUtil: suite configs c5,f4"
 timeout -s KILL 300 rocprofv3 --pmc MfmaUtil --kernel-trace -d "$RAW/mfma" -o suite -- \
   $PY -m cublade_amd.benchmark.suite --configs c5,f4 --reps 3 --warmup 1 > "$RAW/mfma.log" 2>&1 || exit $?
 
 step "summaries"
+CAL="$RAW/cal_fetch/calib_results.db $RAW/cal_write/calib_results.db 262144"
 {
-  echo "# rocprofv3 kernel trace of bench.py (BASELINE configs[1] step, W8A16 M=4096 extra)"
+  echo "# rocprofv3 kernel trace of bench.py (BASELINE configs[1] step, roofline rotations, extras)"
   echo "# command: rocprofv3 --kernel-trace --stats -d RAW/trace -o bench -- python -u bench.py --no-cpu"
   echo "# durations in microseconds"
   $R kernels "$RAW/trace/bench_results.db"
@@ -62,16 +72,26 @@ step "summaries"
   echo "# bench.py output line under the profiler:"
   grep '"metric"' "$RAW/trace.log"
 } > "$OUT/bench_c2_kernels.txt" || exit $?
-$R traffic "k_deq_tensor<false, 1, 2>" "$RAW/fetch/bench_results.db" "$RAW/write/bench_results.db" \
-  "$RAW/cal_fetch/calib_results.db" "$RAW/cal_write/calib_results.db" 262144 \
-  | python -c 'import json,sys; d=json.load(sys.stdin); d["command"]="bash cublade_amd/benchmark/profile.sh OUTDIR: rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --kernel-trace -- python -u bench.py --no-cpu --no-w8a16 --steps 3 --warmup 1; calibration: the same counters over python -m cublade_amd.benchmark.copy_calib (256 MiB copy = 262144 KiB)"; d["algorithmic_bytes_per_launch"]=201326596; d["traffic_over_algorithmic"]=round(d["hbm_bytes_per_launch"]/201326596,4); print(json.dumps(d, indent=1))' \
-  > "$OUT/dequant_int8_c2_traffic.json" || exit $?
+traffic_json() {   # KERNEL ALGO_BYTES OUTFILE
+  $R traffic "$1" "$RAW/fetch/bench_results.db" "$RAW/write/bench_results.db" $CAL \
+  | python -c 'import json,sys; d=json.load(sys.stdin); a=int(sys.argv[1]); d["command"]="bash cublade_amd/benchmark/profile.sh OUTDIR: rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --kernel-trace -- python -u bench.py --no-cpu --no-extras --steps 3 --warmup 1; calibration: the same counters over python -m cublade_amd.benchmark.copy_calib (256 MiB copy = 262144 KiB)"; d["algorithmic_bytes_per_launch"]=a; d["traffic_over_algorithmic"]=round(d["hbm_bytes_per_launch"]/a,4); print(json.dumps(d, indent=1))' "$2" \
+  > "$3"
+}
+traffic_json "k_quant_tensor_1pass<1, false>" 201326596 "$OUT/quant_int8_c2_traffic.json" || exit $?
+traffic_json "k_deq_tensor<false, 1, 2>" 201326596 "$OUT/dequant_int8_c2_traffic.json" || exit $?
 {
-  echo "# rocprofv3 kernel trace of the per-config suite (configs 1-5, 10 timed calls each)"
+  echo "# rocprofv3 kernel trace of the per-config suite (10 timed calls each)"
   echo "# command: rocprofv3 --kernel-trace --stats -d RAW/suite -o suite -- python -u -m cublade_amd.benchmark.suite --reps 10"
   echo "# durations in microseconds"
   $R kernels "$RAW/suite/suite_results.db"
 } > "$OUT/suite_kernels.txt" || exit $?
+{
+  echo "# HBM bytes per dispatch of every kernel of suite configs c1-c5, from FETCH_SIZE and WRITE_SIZE"
+  echo "# (KiB per dispatch, one counter per run) scaled by the factors a 256 MiB device copy gives"
+  echo "# (its counters read back against 262144 KiB moved; see *_traffic.json for the factors)"
+  echo "# commands: rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --kernel-trace -d RAW/sfetch -o suite -- python -u -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5 --reps 3 --warmup 1"
+  $R traffic-all "$RAW/sfetch/suite_results.db" "$RAW/swrite/suite_results.db" $CAL
+} > "$OUT/suite_traffic.txt" || exit $?
 {
   echo "# rocprof derived counter MfmaUtil = sum(SQ_VALU_MFMA_BUSY_CYCLES) / (max(GRBM_GUI_ACTIVE) * SIMDs) * 100,"
   echo "# per kernel: mean and median over dispatches, then the values in dispatch order (the first is the"

@@ -11,6 +11,10 @@
     python -m cublade_amd.benchmark.rocprof traffic KERNEL FETCH.db WRITE.db \
         CAL_FETCH.db CAL_WRITE.db CAL_KIB
 
+    # the same for every kernel of the runs (a text table)
+    python -m cublade_amd.benchmark.rocprof traffic-all FETCH.db WRITE.db \
+        CAL_FETCH.db CAL_WRITE.db CAL_KIB
+
 The calibration runs profile a copy of CAL_KIB KiB (copy_calib.py); the
 factor for each counter is CAL_KIB / (its mean over the copy dispatches).
 Kernel names are shortened to their template signature. Output is plain
@@ -86,11 +90,34 @@ def traffic(kernel, fetch_db, write_db, cal_fetch_db, cal_write_db, cal_kib):
             "hbm_bytes_per_launch": int(read_b + write_b)}
 
 
+def traffic_all(fetch_db, write_db, cal_fetch_db, cal_write_db, cal_kib):
+    """[(kernel, dispatches, read_bytes, write_bytes)] per dispatch, calibrated."""
+    cal_kib = float(cal_kib)
+    cf, _ = _mean_for(counter_stats(cal_fetch_db), "copyBuffer", "FETCH_SIZE")
+    cw, _ = _mean_for(counter_stats(cal_write_db), "copyBuffer", "WRITE_SIZE")
+    fs, ws = counter_stats(fetch_db), counter_stats(write_db)
+    rows = []
+    for (k, c), vals in fs.items():
+        if c != "FETCH_SIZE":
+            continue
+        wv = ws.get((k, "WRITE_SIZE"))
+        if not wv:
+            continue
+        rows.append((k, len(vals), sum(vals) / len(vals) * cal_kib / cf * 1024,
+                     sum(wv) / len(wv) * cal_kib / cw * 1024))
+    return sorted(rows, key=lambda r: -(r[2] + r[3]))
+
+
 def main(argv=None):
     argv = argv if argv is not None else sys.argv[1:]
     if argv and argv[0] == "traffic" and len(argv) == 7:
         import json
         print(json.dumps(traffic(*argv[1:]), indent=1))
+        return 0
+    if argv and argv[0] == "traffic-all" and len(argv) == 6:
+        print(f"{'kernel':110s} {'calls':>6s} {'read_MB':>10s} {'write_MB':>10s} {'total_MB':>10s}")
+        for k, n, rb, wb in traffic_all(*argv[1:]):
+            print(f"{k:110s} {n:6d} {rb / 1e6:10.2f} {wb / 1e6:10.2f} {(rb + wb) / 1e6:10.2f}")
         return 0
     if len(argv) != 2 or argv[0] not in ("kernels", "counters"):
         print(__doc__)

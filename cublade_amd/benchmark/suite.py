@@ -4,9 +4,9 @@ Each op is timed through the public API with HIP events, the Infinity Cache
 flushed before every call, and reported as algorithmic bytes (or FLOPs) per
 second and as a fraction of the MI355X roofline (8 TB/s HBM, 2.5 PFLOP/s
 dense fp16 MFMA). Algorithmic bytes per op (N elements, C channels, G
-groups): per-tensor quant 2N read (amax) + 2N read + N written + 4 (cast);
-row / group quant 2N + N + 4C (one pass); column quant 2N + 2N + N + 4F (two
-passes); dequant N + 2N + 4 * scales. W8A16 and the dense GEMM: 2 * M * N * K
+groups): the op's minimum HBM traffic, 2N read + N written + 4 * scales for
+every quant (x read once, codes and scales written), N + 4 * scales read +
+2N written for every dequant. W8A16 and the dense GEMM: 2 * M * N * K
 FLOPs (int8 GEMMs against the 5.0 POP/s dense int8 peak, the fp32-activation
 W8A16 against the 157.3 TFLOP/s fp32 peak).
 
@@ -59,12 +59,12 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
         x = configs.c1_fp8_tensor().to(dev)
         n = x.numel()
         q_and_dq("c1", x, dict(dtype=torch.float8_e4m3fn, mode="tensor"),
-                 2 * n + 2 * n + n + 4, n + 2 * n + 4)
+                 2 * n + n + 4, n + 2 * n + 4)
         del x
     if "c2" in selected:
         x = configs.c2_int8_tensor().to(dev)
         n = x.numel()
-        q_and_dq("c2", x, dict(dtype=torch.int8, mode="tensor"), 2 * n + 2 * n + n + 4,
+        q_and_dq("c2", x, dict(dtype=torch.int8, mode="tensor"), 2 * n + n + 4,
                  n + 2 * n + 4)
         del x
     if "c3" in selected:
@@ -73,7 +73,7 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
         q_and_dq("c3", x, dict(dtype=torch.int8, mode="channel", ch_axis=0),
                  2 * n + n + 4 * C, n + 2 * n + 4 * C, "_axis0")
         q_and_dq("c3", x, dict(dtype=torch.int8, mode="channel", ch_axis=1),
-                 2 * n + 2 * n + n + 4 * F, n + 2 * n + 4 * F, "_axis1")
+                 2 * n + n + 4 * F, n + 2 * n + 4 * F, "_axis1")
         del x
     if "c4" in selected:
         x = configs.c4_int8_group().to(dev)
@@ -198,7 +198,7 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
         x = configs.c3_int8_channel().to(dev).view(7, 4096, 8192)
         n, C = x.numel(), 4096
         q_and_dq("f3", x, dict(dtype=torch.int8, mode="channel", ch_axis=1),
-                 2 * n + 2 * n + n + 4 * C, n + 2 * n + 4 * C, "_channel_axis1_3d")
+                 2 * n + n + 4 * C, n + 2 * n + 4 * C, "_channel_axis1_3d")
 
         def channel_via_copies():
             qt = quantize_tensor(x.movedim(1, 0).contiguous(), dtype=torch.int8,
@@ -206,7 +206,7 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
             return qt.data.movedim(0, 1).contiguous()
 
         r = _rec("f3", "quant_channel_axis1_3d_via_copies",
-                 time_op(channel_via_copies, reps, warmup, flush), 2 * n + 2 * n + n + 4 * C)
+                 time_op(channel_via_copies, reps, warmup, flush), 2 * n + n + 4 * C)
         r["speedup_in_place"] = round(r["us_median"] / out[-2]["us_median"], 3)
         out.append(r)
         print(json.dumps(r), flush=True)

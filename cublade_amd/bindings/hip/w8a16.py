@@ -71,7 +71,7 @@ def w8a16_linear(
         return y
     L = _abi.lib()
     with _abi.on_device(dev):
-        ws = _abi.workspace(dev, L.cbq_w8a16_ws_bytes(M, N, K, n_out))
+        ws = _abi.workspace(dev, L.cbq_w8a16_ws_bytes(M, N, K, n_out, _abi.DTYPE_CODE[dt]))
         rc = L.cbq_w8a16_linear(_abi.ptr(x2d), _abi.DTYPE_CODE[dt], _abi.ptr(wq), _abi.ptr(s),
                                 _abi.ptr(b), _abi.ptr(oc), n_out, _abi.ptr(wo), M, N, K,
                                 _abi.ptr(ws), ws.numel(), _abi.ptr(y), _abi.stream_handle(dev))

@@ -197,9 +197,13 @@ __global__ __launch_bounds__(kBlock) void k_cast_tensor(
 // gen + 1, and polls all slots until every tag is gen + 1; workgroup 0 then
 // stores gen + 1 (every workgroup has read gen by then: its slot carries it).
 // Each call rewrites every slot, so no word needs resetting, and a stale tag
-// is always the previous call's. A wait gives up after spin_limit polls;
-// the workgroup then sets status and writes NaN codes (INT8: 0) and a NaN
-// scale instead of quietly wrong ones.
+// is always the previous call's. A wait gives up after spin_limit polls
+// (only possible when the grid is not resident at once, e.g. other work
+// holding CUs for about a second): the workgroup sets status and writes NaN
+// codes (INT8: 0) and a NaN scale instead of quietly wrong ones. A timed-out
+// call can leave slots tagged for the next call, so a set status poisons the
+// workspace: every later call writes NaN codes and scale without exchanging,
+// until the caller zero-fills the control block again.
 // ---------------------------------------------------------------------------
 constexpr int kFusedBlock = 1024;                // 16 waves: four per SIMD
 constexpr int kFusedU = 4;                       // chunks per thread and step
@@ -270,18 +274,23 @@ __device__ __forceinline__ void cast_store8_buf(const Raw8<DT>& r, float inv,
 // NaN if the wait timed out. Every thread of the workgroup gets the result.
 __device__ float grid_max_exchange(float m, char* ctl, uint32_t spin_limit, float* red) {
   __shared__ unsigned long long s_gen;
+  __shared__ int s_poisoned;
   auto* gen_w = reinterpret_cast<unsigned long long*>(ctl + kCtlGen);
   auto* status = reinterpret_cast<unsigned int*>(ctl + kCtlStatus);
   auto* slots = reinterpret_cast<unsigned long long*>(ctl + kCtlSlots);
   if (threadIdx.x == 0) {
     const unsigned long long gen = __hip_atomic_load(gen_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned st = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_gen = gen;
-    __hip_atomic_store(slots + blockIdx.x,
-                       (static_cast<unsigned long long>(static_cast<uint32_t>(gen + 1)) << 32) |
-                           __float_as_uint(m),
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_poisoned = st != 0;
+    if (st == 0)
+      __hip_atomic_store(slots + blockIdx.x,
+                         (static_cast<unsigned long long>(static_cast<uint32_t>(gen + 1)) << 32) |
+                             __float_as_uint(m),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
+  if (s_poisoned) return __builtin_nanf("");
   const uint32_t tag = static_cast<uint32_t>(s_gen + 1);
   const int G = static_cast<int>(gridDim.x);
   uint32_t spins = 0;

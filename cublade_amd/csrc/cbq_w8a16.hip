@@ -1568,13 +1568,17 @@ int w8a16_t(const void* x, const int8_t* wq, const void* scales, const void* bia
 
 using namespace cbq;
 
-extern "C" size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_out) {
+extern "C" size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_out,
+                                     int act_dtype) {
   (void)n_out;
   if (M <= 0 || N <= 0 || K <= 0) return CBQ_WS_CTRL_BYTES;
-  // The larger of the MFMA split-K partials and the general path's partial
-  // sums (the dtype and alignment that choose between them are not known here).
-  const int64_t mfma = splitk_bytes(M, N, split_plan(M, N, K));
-  return CBQ_WS_CTRL_BYTES + static_cast<size_t>(std::max(mfma, general_split_bytes(M, N, K)));
+  // fp16 / bf16 with K % 16 == 0 run the MFMA kernels (split-K partials of
+  // the last wave of tiles); fp32 and K % 16 != 0 run the general kernel
+  // (its partial sums). Unaligned fp16 / bf16 operands also take the general
+  // kernel; with this size it then runs without a split (same results).
+  const bool mfma = (act_dtype == kF16 || act_dtype == kBF16) && K % 16 == 0;
+  const int64_t bytes = mfma ? splitk_bytes(M, N, split_plan(M, N, K)) : general_split_bytes(M, N, K);
+  return CBQ_WS_CTRL_BYTES + static_cast<size_t>(bytes);
 }
 
 extern "C" int cbq_w8a16_linear(const void* x, int act_dtype, const int8_t* wq,

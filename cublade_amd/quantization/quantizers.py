@@ -67,14 +67,19 @@ _ZERO_POINTS: dict = {}
 
 def _zero_scalar(device: torch.device) -> torch.Tensor:
     """The 0-d fp32 zero point of the symmetric scheme. One tensor per device
-    is shared by every QuantizedTensor (read-only by contract), so a quantize
+    is shared by QuantizedTensors (do not modify it in place), so a quantize
     call launches no fill kernel for it (the reference allocates a fresh
-    torch.zeros(()) per call, quantizers.py:53-54)."""
+    torch.zeros(()) per call, quantizers.py:53-54). It is created and cached
+    only outside graph capture (a fill recorded in a capture runs at replay
+    time), and replaced by a fresh zero if it was modified in place (its
+    version counter moved)."""
     key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
-    z = _ZERO_POINTS.get(key)
-    if z is None:
-        z = torch.zeros((), dtype=torch.float32, device=device)
-        _ZERO_POINTS[key] = z
+    entry = _ZERO_POINTS.get(key)
+    if entry is not None and entry[0]._version == entry[1]:
+        return entry[0]
+    z = torch.zeros((), dtype=torch.float32, device=device)
+    if not torch.cuda.is_current_stream_capturing():
+        _ZERO_POINTS[key] = (z, z._version)
     return z
 
 

@@ -188,16 +188,17 @@ int cbq_dequant_int8_group_nd(const int8_t* q, const float* scale,
 
 /* ---- W8A16 linear ------------------------------------------------------- */
 
-/* Workspace bytes for cbq_w8a16_linear at this shape: the control block,
- * plus room for the larger of two split-K scratch areas: the general
- * (fp32 / unaligned) path's fp32 partial sums, up to 16 x M x N x 4 bytes
- * when its tiles give fewer than two workgroups per CU, and, for M > 64 when
- * the last wave of output tiles is short, the MFMA path's fp32 partial
- * tiles of that wave (ranges x tail tiles x 256 / 192 / 128 KiB for tiles of
- * 256 / 192 / 128 x 256; at most 16 ranges and at most one partial tile per
- * CU, i.e. <= 64 MiB on MI355X). The reference allocates its temporaries
- * inside the forward (linear.py:105-131). */
-size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_out);
+/* Workspace bytes for cbq_w8a16_linear at this shape and activation dtype:
+ * the control block, plus the split-K scratch of the kernel that dtype
+ * selects. CBQ_F16 / CBQ_BF16 with K % 16 == 0 (MFMA): for M > 64 when the
+ * last wave of output tiles is short, the fp32 partial tiles of that wave
+ * (ranges x tail tiles x 256 / 192 / 128 KiB for tiles of 256 / 192 / 128 x
+ * 256; at most 16 ranges and at most one partial tile per CU, i.e. <= 64 MiB
+ * on MI355X), else nothing. CBQ_F32 and K % 16 != 0 (general kernel): fp32
+ * partial sums, up to 16 x M x N x 4 bytes when its tiles give fewer than
+ * two workgroups per CU. The reference allocates its temporaries inside the
+ * forward (linear.py:105-131). */
+size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_out, int act_dtype);
 
 /* Replaces the forward chain of cuBladeW8A16LinearLayer
  * (quantization/linear.py:83-137): int8 -> activation copy of the weight

@@ -32,10 +32,3 @@ def cases(kind: str):
 
 def ids(kind: str):
     return [m["name"] for m, _ in cases(kind)]
-
-
-def f16_bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
-    """Bit equality for fp16/bf16 patterns, treating any NaN as equal to any NaN."""
-    a = np.asarray(a, np.uint16)
-    b = np.asarray(b, np.uint16)
-    return bool(np.array_equal(a, b))

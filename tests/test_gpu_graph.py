@@ -97,3 +97,59 @@ def test_graph_group_and_fp8():
     g, out = _capture(fn, torch.cuda.Stream())
     _check_replays(x, lambda i: torch.randn(512, 1024, generator=torch.Generator()
                                             .manual_seed(20 + i)).bfloat16().to(DEV), fn, g, out)
+
+
+def test_graph_workspace_survives_growth():
+    """Two graphs captured on one stream whose second warm-up grows that
+    stream's workspace: the first graph's workspace (its per-tensor control
+    block) stays allocated, and its replays stay exact while the caching
+    allocator hands out fresh memory in between. Growing inside a capture
+    raises instead of allocating."""
+    from cublade_amd import _abi
+    from cublade_amd.quantization import cuBladeW8A16LinearLayer, quantize_tensor
+    s = torch.cuda.Stream()
+    n = 1 << 22
+    x = torch.randn(n, generator=torch.Generator().manual_seed(3)).half().to(DEV)
+
+    def quant():
+        qt = quantize_tensor(x, dtype=torch.int8, mode="tensor")
+        return qt.data, qt.scale
+
+    g1, out1 = _capture(quant, s)
+    with torch.cuda.stream(s):
+        ws1 = _abi.workspace(x.device, 0)
+    ptr1, size1 = ws1.data_ptr(), ws1.numel()
+    del ws1
+    # M = 256, N = 11008: split-K partials, a workspace far larger than size1
+    N, K, M = 11008, 4096, 256
+    layer = cuBladeW8A16LinearLayer(K, N, bias=False, dtype=torch.float16)
+    layer.quantize((0.02 * torch.randn(N, K, generator=torch.Generator().manual_seed(4)))
+                   .half().to(DEV))
+    xa = torch.randn(M, K, generator=torch.Generator().manual_seed(5)).half().to(DEV)
+    with torch.no_grad():
+        g2, out2 = _capture(lambda: layer(xa), s)
+    with torch.cuda.stream(s):
+        ws2 = _abi.workspace(x.device, 0)
+    assert ws2.numel() > size1 and ws2.data_ptr() != ptr1
+    assert any(t.data_ptr() == ptr1 for t in _abi._ws_retired)
+    # fresh allocations that would reuse a freed workspace
+    junk = [torch.full((size1,), 0x5A, dtype=torch.uint8, device=DEV) for _ in range(4)]
+    _check_replays(x, lambda i: (2.0 + i) * torch.randn(n, generator=torch.Generator()
+                                                        .manual_seed(30 + i)).half().to(DEV),
+                   quant, g1, out1)
+    with torch.no_grad():
+        g2.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out2, layer(xa))
+    assert all(bool((j == 0x5A).all()) for j in junk)
+    # a shape that needs more workspace than the capture stream holds
+    big = cuBladeW8A16LinearLayer(K, 4 * N, bias=False, dtype=torch.float16)
+    big.quantize(torch.zeros(4 * N, K, dtype=torch.float16, device=DEV))
+    xb = torch.randn(1536, K, generator=torch.Generator().manual_seed(6)).half().to(DEV)
+    need = _abi.lib().cbq_w8a16_ws_bytes(1536, 4 * N, K, 0, _abi.F16)
+    if need > ws2.numel():
+        g3 = torch.cuda.CUDAGraph()
+        with pytest.raises(RuntimeError, match="during graph capture"):
+            with torch.no_grad(), torch.cuda.graph(g3, stream=s):
+                big(xb)
+    torch.cuda.synchronize()

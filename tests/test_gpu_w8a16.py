@@ -182,7 +182,7 @@ def test_splitk_workspace_fallback():
     x, wq, s, b, _, _ = make_case(M, K, N, torch.float16, 21, bias=True)
     xd, wd, sd, bd = x.to(DEV), wq.to(DEV), s.to(DEV), b.to(DEV)
     L = _abi.lib()
-    assert L.cbq_w8a16_ws_bytes(M, N, K, 0) > _abi.WS_CTRL_BYTES     # split-K shape
+    assert L.cbq_w8a16_ws_bytes(M, N, K, 0, _abi.F16) > _abi.WS_CTRL_BYTES     # split-K shape
     y_split = w8a16(xd, wd, sd, bd)
     y_small = torch.empty_like(y_split)
     ws = torch.zeros(_abi.WS_CTRL_BYTES, dtype=torch.uint8, device=DEV)
@@ -195,13 +195,13 @@ def test_splitk_workspace_fallback():
     np.testing.assert_allclose(y_split.float().cpu().numpy()[[0, 99, 255]], ref, **TOL)
 
 
-@pytest.mark.parametrize("M,K,N", [(1024, 2048, 1100), (1500, 1024, 700)])
+@pytest.mark.parametrize("M,K,N", [(1024, 2048, 1100), (1500, 2048, 700)])
 def test_splitk_large_m_few_tiles(M, K, N):
     """M >= 1024 with fewer tiles than CUs takes the split-K path; rows
     against the oracle and the no-split kernel (control-block workspace)."""
     from cublade_amd import _abi
     L = _abi.lib()
-    assert L.cbq_w8a16_ws_bytes(M, N, K, 0) > _abi.WS_CTRL_BYTES
+    assert L.cbq_w8a16_ws_bytes(M, N, K, 0, _abi.BF16) > _abi.WS_CTRL_BYTES
     x, wq, s, b, _, _ = make_case(M, K, N, torch.bfloat16, M + N, bias=True)
     xd, wd, sd, bd = x.to(DEV), wq.to(DEV), s.to(DEV), b.to(DEV)
     y_split = w8a16(xd, wd, sd, bd)
@@ -234,8 +234,9 @@ def test_dma_plans(M, K, N, dt, n_out, path):
     """Each x-tile height (128, 192, 256 rows) and split plan of the MFMA tile
     path (whole tiles, all tiles over k-ranges, full waves whole plus a split
     tail; the host's time model picks them per shape): sampled rows against
-    the oracle, and the full output against the same call with a
-    control-block workspace (no split)."""
+    the oracle, the full output against an fp32 product of the same operands
+    (GPU matmul, independent of the kernel's tiling), and against the same
+    call with a control-block workspace (no split)."""
     from cublade_amd import _abi
     print(f"[w8a16] {dt} M={M} K={K} N={N} outliers={n_out} ({path})", flush=True)
     rows = [0, M // 2 + 3, 2 * M // 3, M - 1]
@@ -253,6 +254,11 @@ def test_dma_plans(M, K, N, dt, n_out, path):
                             ws.numel(), _abi.ptr(y_one), _abi.stream_handle(xd.device))
     assert rc == 0
     torch.testing.assert_close(y.float(), y_one.float(), **TOL)
+    wf = wd.float() * sd.float()[:, None]
+    ref_full = xd.float() @ wf.t().contiguous() + bd.float()
+    if oc:
+        ref_full += xd.float()[:, ocd] @ wod.float().t().contiguous()
+    torch.testing.assert_close(y.float(), ref_full, **TOL)
 
 
 def test_mfma_bit_stability_across_calls():
@@ -282,7 +288,12 @@ def test_config5_shapes(M):
     layer.quantize(w.to(DEV))
     assert layer.int8_weights.is_cuda and layer.scales.dtype == torch.float16
     y = layer(x.to(DEV))
-    rows = np.arange(M) if M <= 16 else np.array([0, 1, M // 2, M - 1], np.int64)
+    # every row at M = 16; else one row in every 64-row block (at a different
+    # offset in each, so every x-tile and wave row position is sampled) plus
+    # the first and last rows, against the oracle's exact accumulation
+    rows = (np.arange(M) if M <= 16 else
+            np.unique(np.r_[0, M - 1, [b * 64 + (b * 37 + 5) % 64 for b in range(M // 64)]])
+            .astype(np.int64))
     ref = oracle_y(bits(x), oracle.F16, bits(layer.int8_weights), bits(layer.scales),
                    rows=rows)
     np.testing.assert_allclose(y.float().cpu().numpy()[rows], ref, **TOL)

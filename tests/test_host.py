@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_slot():
     L = _lib()
-    assert L.cbq_abi_version() == 104
+    assert L.cbq_abi_version() == 105
     assert L.cbq_last_error() in (b"",) or isinstance(L.cbq_last_error(), bytes)
 
 
@@ -92,26 +92,33 @@ def test_workspace_sizes():
     assert L.cbq_quant_tensor_ws_bytes() == C + 4 * 2048
     big = L.cbq_quant_int8_channel_ws_bytes(28672, 8192, 1)
     assert big >= C + 8192 * 4 * 2 and big < 64 << 20
-    # M <= 16: room for the general path's k-split partial sums (16 ranges of
-    # [16, 11008] fp32 over 43 tiles of 16 x 256)
-    assert L.cbq_w8a16_ws_bytes(16, 11008, 4096, 0) == C + 16 * 16 * 11008 * 4
-    assert L.cbq_w8a16_ws_bytes(4096, 11008, 4096, 0) == C
+    F16, F32 = _abi.F16, _abi.F32
+    # M <= 16, fp16: the weight-streaming kernel, no partials; fp32 activations
+    # take the general kernel: 16 k-ranges of [16, 11008] fp32 partial sums
+    assert L.cbq_w8a16_ws_bytes(16, 11008, 4096, 0, F16) == C
+    assert L.cbq_w8a16_ws_bytes(16, 11008, 4096, 0, F32) == C + 16 * 16 * 11008 * 4
+    assert L.cbq_w8a16_ws_bytes(4096, 11008, 4096, 0, F16) == C
     # split-K tile path, 256 CUs (also the CPU-only fallback count): 2 k-ranges
     # x 86 tiles of 128 x 256 (128 KiB of fp32 partials each)
-    assert L.cbq_w8a16_ws_bytes(256, 11008, 4096, 0) == C + 2 * 86 * 128 * 1024
-    assert L.cbq_w8a16_ws_bytes(512, 11008, 4096, 3) == C      # 172 whole 128-row tiles
-    assert L.cbq_w8a16_ws_bytes(256, 11008, 4000, 0) == C      # K % 64 != 0
+    assert L.cbq_w8a16_ws_bytes(256, 11008, 4096, 0, F16) == C + 2 * 86 * 128 * 1024
+    assert L.cbq_w8a16_ws_bytes(256, 11008, 4096, 0, _abi.BF16) == C + 2 * 86 * 128 * 1024
+    assert L.cbq_w8a16_ws_bytes(512, 11008, 4096, 3, F16) == C      # 172 whole 128-row tiles
+    assert L.cbq_w8a16_ws_bytes(256, 11008, 4000, 0, F16) == C      # K % 64 != 0
     # few tiles (the MLP down projection): 8 k-ranges x 32 tiles of 128 x 256,
     # 4 k-ranges x 64 tiles of 192 x 256 (192 KiB each); <= 256 workgroups
-    assert L.cbq_w8a16_ws_bytes(256, 4096, 11008, 0) == C + 8 * 32 * 128 * 1024
-    assert L.cbq_w8a16_ws_bytes(768, 4096, 11008, 0) == C + 4 * 64 * 192 * 1024
+    assert L.cbq_w8a16_ws_bytes(256, 4096, 11008, 0, F16) == C + 8 * 32 * 128 * 1024
+    assert L.cbq_w8a16_ws_bytes(768, 4096, 11008, 0, F16) == C + 4 * 64 * 192 * 1024
     # 24 < M <= 64 with K > 8192: the split MFMA path (11 ranges x 16 tiles of 128 x 256)
-    assert L.cbq_w8a16_ws_bytes(64, 4096, 11008, 0) == C + 11 * 16 * 128 * 1024
-    assert L.cbq_w8a16_ws_bytes(32, 4096, 11008, 0) == C + 11 * 16 * 128 * 1024
-    # M = 24: k_stream<2>, no MFMA partials; only the general path's 16 ranges of [24, 4096] fp32
-    assert L.cbq_w8a16_ws_bytes(24, 4096, 11008, 0) == C + 16 * 24 * 4096 * 4
+    assert L.cbq_w8a16_ws_bytes(64, 4096, 11008, 0, F16) == C + 11 * 16 * 128 * 1024
+    assert L.cbq_w8a16_ws_bytes(32, 4096, 11008, 0, F16) == C + 11 * 16 * 128 * 1024
+    # M = 24: k_stream<2>, no MFMA partials; fp32: 16 ranges of [24, 4096] fp32
+    assert L.cbq_w8a16_ws_bytes(24, 4096, 11008, 0, F16) == C
+    assert L.cbq_w8a16_ws_bytes(24, 4096, 11008, 0, F32) == C + 16 * 24 * 4096 * 4
+    # K % 16 != 0 takes the general kernel whatever the dtype
+    assert L.cbq_w8a16_ws_bytes(16, 11008, 4090, 0, F16) == L.cbq_w8a16_ws_bytes(
+        16, 11008, 4090, 0, F32)
     # 258 tiles of 256 x 256: one full wave whole, the 2 left over split 16 ways
-    assert L.cbq_w8a16_ws_bytes(1536, 11008, 4096, 0) == C + 16 * 2 * 256 * 1024
+    assert L.cbq_w8a16_ws_bytes(1536, 11008, 4096, 0, F16) == C + 16 * 2 * 256 * 1024
 
 
 def test_nd_entry_points_validate_and_size():

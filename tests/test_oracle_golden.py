@@ -14,6 +14,7 @@ import torch
 
 import oracle
 from tests import _golden as G
+from tests._util import assert_bits_equal_16, bits
 
 
 def _y_key(out_code):
@@ -159,3 +160,34 @@ def test_w8a16_matches_numpy_float64():
     y = oracle.w8a16_linear(_bf16(x), oracle.F16, wq.numpy(), _bf16(s), bias=_bf16(b))
     ref = (x.double().numpy() @ wq.double().numpy().T) * s.double().numpy() + b.double().numpy()
     np.testing.assert_allclose(y, ref.astype(np.float32), rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("qd", [torch.int8, torch.float8_e4m3fn])
+def test_torch_cpu_restatement_matches_c_oracle(dt, qd):
+    """oracle/torch_cpu.py (the CPU baseline of bench.py) gives the C
+    oracle's codes, scale and dequantized values bit for bit, NaN / inf /
+    -0 / tiny inputs included."""
+    from oracle import torch_cpu
+    if qd == torch.float8_e4m3fn and dt == torch.float32:
+        pytest.skip("FP8 takes fp16 / bf16 inputs only")
+    g = torch.Generator().manual_seed(7)
+    x = (torch.randn(50_003, generator=g) * 3).to(dt)
+    x[5] = float("nan")
+    x[7] = 60000.0 if dt == torch.float16 else float("inf")
+    x[9] = -0.0
+    x[11] = 1e-30 if dt != torch.float16 else 1e-7
+    code = {torch.float16: oracle.F16, torch.bfloat16: oracle.BF16, torch.float32: oracle.F32}[dt]
+    q, s = torch_cpu.quant_tensor(x, qd)
+    if qd == torch.int8:
+        qo, so = oracle.quant_int8_tensor(bits(x), code)
+    else:
+        qo, so = oracle.quant_fp8_tensor(bits(x), code)
+    assert np.array_equal(bits(q).view(np.uint8), qo.view(np.uint8))
+    assert np.float32(s.item()).view(np.uint32) == np.float32(so).view(np.uint32)
+    out = torch.bfloat16 if dt == torch.float32 else dt
+    y = torch_cpu.dequant_tensor(q, s, out)
+    oc = oracle.BF16 if out == torch.bfloat16 else oracle.F16
+    yo = (oracle.dequant_int8_tensor(qo, so, oc) if qd == torch.int8
+          else oracle.dequant_fp8_tensor(qo, so, oc))
+    assert_bits_equal_16(bits(y), yo, oc, "dequant")   # any NaN matches any NaN
