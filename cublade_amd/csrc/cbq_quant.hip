@@ -214,6 +214,14 @@ constexpr int kMaxFusedGrid = (CBQ_WS_CTRL_BYTES - kCtlSlots) / 8;
 
 // Steps held in registers: 24 chunks (96 VGPRs) of 2-byte input, 12 of fp32.
 template <int DT> constexpr int fused_hold_steps() { return DT == kF32 ? 3 : 6; }
+// The first streamed steps are parked in LDS (128 KiB of a workgroup's
+// 160 KiB): two steps of 2-byte input, one of fp32. With the registers, a
+// 2-byte x of up to 128 MiB (fp32: 80 MiB) is read from HBM exactly once.
+constexpr int kFusedLdsBytes = 128 * 1024;
+template <int DT>
+constexpr int fused_lds_steps() {
+  return kFusedLdsBytes / (kFusedBlock * kFusedU * 8 * elem_bytes<DT>());
+}
 
 // Chunk loads and code stores addressed as a wave-uniform base plus a 32-bit
 // per-thread offset (keeps one offset register per thread instead of one
@@ -324,9 +332,13 @@ __global__ __launch_bounds__(kFusedBlock) void k_quant_tensor_1pass(
     float* __restrict__ scale_out, char* __restrict__ ctl, uint32_t spin_limit) {
   constexpr int U = kFusedU;
   constexpr int HS = fused_hold_steps<DT>();
+  constexpr int LS = fused_lds_steps<DT>();
   constexpr int EB = 8 * elem_bytes<DT>();            // bytes of x per chunk
+  constexpr int QW = EB / 16;                         // 16-byte words per chunk
   constexpr float kQ = FP8 ? kQmaxFp8 : kQmaxInt8;
   __shared__ float red[kFusedBlock / kWave];
+  // parked steps: word w of chunk (i, u) of lane t at ((i * U + u) * QW + w) * B + t
+  __shared__ u32x4 park[LS * U * QW * kFusedBlock];
 
   const int64_t SB = static_cast<int64_t>(kFusedBlock) * U;   // chunks per workgroup and step
   const int64_t GS = static_cast<int64_t>(gridDim.x) * SB;    // chunks per grid step
@@ -339,7 +351,8 @@ __global__ __launch_bounds__(kFusedBlock) void k_quant_tensor_1pass(
   uint8_t* qw = q + static_cast<int64_t>(blockIdx.x) * SB * 8;
   const uint32_t xo = threadIdx.x * EB, qo = threadIdx.x * 8;
 
-  // Pass 1: |x| max; streamed steps first, then the held steps into r[].
+  // Pass 1: |x| max; streamed steps first (the first LS of them parked in
+  // LDS), then the held steps into r[].
   float m = 0.0f;
   for (int64_t i = 0; i < held0; ++i) {
     Raw8<DT> v[U];
@@ -350,6 +363,14 @@ __global__ __launch_bounds__(kFusedBlock) void k_quant_tensor_1pass(
       float f[8];
       cvt8<DT>(v[u], f);
       m = absmax8(f, m);
+    }
+    if (i < LS) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        u32x4* pk = park + (static_cast<int>(i) * U + u) * QW * kFusedBlock + threadIdx.x;
+        pk[0] = u32x4{v[u].a.x, v[u].a.y, v[u].a.z, v[u].a.w};
+        if constexpr (DT == kF32) pk[kFusedBlock] = u32x4{v[u].b.x, v[u].b.y, v[u].b.z, v[u].b.w};
+      }
     }
   }
   // Held steps through buffer resources bounded at the end of x (the
@@ -390,7 +411,8 @@ __global__ __launch_bounds__(kFusedBlock) void k_quant_tensor_1pass(
   const float inv = amax == amax ? inv_scale(amax, eps, kQ) : amax;
   if (threadIdx.x == 0 && (blockIdx.x == 0 || inv != inv)) *scale_out = 1.0f / inv;
 
-  // Pass 2: cast the held steps from registers, then re-read the others.
+  // Pass 2: cast the held steps from registers, then the parked ones from
+  // LDS, then re-read the others.
 #pragma unroll
   for (int k = 0; k < HS; ++k) {
     const int64_t c0 = (held0 + k) * GS + cb;
@@ -402,7 +424,22 @@ __global__ __launch_bounds__(kFusedBlock) void k_quant_tensor_1pass(
         cast_store8_buf<DT, FP8>(r[k * U + u], inv, rs, u * kFusedBlock * 8 + qo);
     }
   }
-  for (int64_t i = 0; i < held0; ++i) {
+  const int64_t parked = held0 < LS ? held0 : LS;
+  for (int64_t i = 0; i < parked; ++i) {            // each lane reads back its own words
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const u32x4* pk = park + (static_cast<int>(i) * U + u) * QW * kFusedBlock + threadIdx.x;
+      Raw8<DT> v;
+      const u32x4 a = pk[0];
+      v.a = make_uint4(a.x, a.y, a.z, a.w);
+      if constexpr (DT == kF32) {
+        const u32x4 b = pk[kFusedBlock];
+        v.b = make_uint4(b.x, b.y, b.z, b.w);
+      }
+      cast_store8<DT, FP8>(v, inv, qw + (i * GS + u * kFusedBlock) * 8, qo);
+    }
+  }
+  for (int64_t i = parked; i < held0; ++i) {
     Raw8<DT> v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) v[u] = ld8_at<DT>(xw + (i * GS + u * kFusedBlock) * EB, xo);
