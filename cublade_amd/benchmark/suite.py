@@ -10,7 +10,7 @@ every quant (x read once, codes and scales written), N + 4 * scales read +
 FLOPs (int8 GEMMs against the 5.0 POP/s dense int8 peak, the fp32-activation
 W8A16 against the 157.3 TFLOP/s fp32 peak).
 
-    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5,c5f32,f1,f3,f4,f4s [--json out.json]
+    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5,c5o,c5f32,f1,f3,f4,f4s [--json out.json]
 """
 from __future__ import annotations
 
@@ -97,6 +97,29 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
             out.append(r)
             print(json.dumps(r), flush=True)
             del layer, xd
+    if "c5o" in selected:
+        # config 5 with its outlier threshold applied the LLM.int8 way (the
+        # layer's opt-in activation mode): the 6 outlier features of x run
+        # through the fp16 side-GEMM in the epilogue; the plain layer on the
+        # same operands beside it gives the side-GEMM's cost
+        for M in (16, 256, 4096):
+            x, w = configs.c5_w8a16(M)
+            N, K = w.shape
+            lo = cuBladeW8A16LinearLayer(K, N, bias=False, dtype=torch.float16,
+                                         handle_outliers=True, outlier_mode="activation")
+            lo.quantize(w.to(dev), activations=x)
+            xd = x.to(dev)
+            us = time_op(lambda: lo(xd), reps, warmup, flush)
+            bytes_ = N * K + 2 * N + 2 * M * K + 2 * M * N
+            r = _rec("c5o", f"w8a16_outliers_m{M}", us, bytes_, 2.0 * M * N * K)
+            r["n_out"] = int(lo.outlier_cols.numel())
+            lp = cuBladeW8A16LinearLayer(K, N, bias=False, dtype=torch.float16)
+            lp.quantize(w.to(dev))
+            r["plain_us_median"] = round(statistics.median(time_op(lambda: lp(xd), reps, warmup,
+                                                                   flush)), 2)
+            out.append(r)
+            print(json.dumps(r), flush=True)
+            del lo, lp, xd
     if "c5f32" in selected:
         # The same layer with fp32 activations (an fp32 model under
         # quantize_model gets fp32 layers, utils.py:46): the general kernel,
@@ -274,7 +297,7 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,c5f32,f1,f3,f4,f4s")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,c5o,c5f32,f1,f3,f4,f4s")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--json", default=None)

@@ -318,6 +318,14 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t nb) {
   return b < (per << 3) ? (b & 7) * per + (b >> 3) : b;
 }
 
+// Raw buffer resources (gfx9 word 3: 32-bit dword data format) and the
+// cache-policy argument of the buffer load / store builtins: kAuxNT marks an
+// access non-temporal, kAuxSc1 gives it device (agent) scope, the bits the
+// compiler uses for agent-scope atomic loads and stores on gfx950.
+constexpr int kBufDword3 = 0x00020000;
+constexpr int kAuxNT = 2;
+constexpr int kAuxSc1 = 16;
+
 // Reciprocal scale and stored scale, both correctly rounded fp32 divisions
 // (quantize_int8.cu:120-126 computes them in double and narrows once, which
 // is the same value; quantize_per_tensor_fp8.cu:99-102 intends the same).

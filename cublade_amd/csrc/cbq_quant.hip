@@ -246,8 +246,6 @@ __device__ __forceinline__ void cast_store8(const Raw8<DT>& r, float inv, uint8_
 // chunk past the end of x reads as zeros and its code store is dropped by the
 // hardware, without branches (a guarded load would make the compiler wait
 // for every outstanding load where the branch rejoins).
-constexpr int kBufDword3 = 0x00020000;           // gfx9 raw buffer: 32-bit dword data format
-constexpr int kAuxNT = 2;                        // cache policy bit: non-temporal
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
   const int nr = bytes <= 0 ? 0 : static_cast<int>(bytes);   // callers pass <= 128 KiB

@@ -36,6 +36,10 @@
 // over several k-ranges into fp32 partial tiles in the caller's workspace and
 // k_splitk_reduce sums them in a fixed order (no cross-workgroup fences);
 // dma_plan picks the tile height and the split with a fitted time model.
+// Outlier columns run on the matrix cores too: per 16 columns the tile's
+// gathered x columns and w_out rows are staged in LDS in one round of loads,
+// then one rank-16 MFMA update per 32 x 32 block (onto the scaled
+// accumulators, or, in a split, into one more partial plane).
 //
 // k_stream1<ACT> (M <= 16) and k_stream<ACT, TM> (M <= 64): persistent
 // weight streaming for large weights (see the kernels' comments).
@@ -142,20 +146,40 @@ __device__ __forceinline__ void decode_tile(int b, const GemmArgs& a, int& tm, i
 }
 
 // Outlier side-GEMM for 4 consecutive outputs y[m, nb .. nb+3]:
-// v[r] += sum_j x[m, oc[j]] * w_out[nb + r, j], in j order. The loop is kept
-// rolled so that the unrolled tile epilogues stay small enough to keep their
-// accumulators in registers.
+// v[r] += sum_j x[m, oc[j]] * w_out[nb + r, j], in j order. Columns go in
+// groups of 4 whose loads (indices, x values, weights) are all issued before
+// any is used: addresses are clamped to valid elements and the terms of
+// missing columns / rows or of an index outside [0, K) are zeroed by selects,
+// so no branch makes the compiler wait for each load in turn (a dependent
+// chain of 3 loads per column and quad cost 2x the whole GEMM at M = 4096,
+// N = 11008 with 6 columns). The group loop is kept rolled so that the
+// unrolled tile epilogues stay small enough to keep their accumulators in
+// registers.
 template <int ACT>
 __device__ __forceinline__ f4 outlier_quad(const GemmArgs& a, int m, int nb, f4 v) {
+  constexpr int G = 4;
+  const int64_t xrow = static_cast<int64_t>(m) * a.K;
 #pragma nounroll
-  for (int jj = 0; jj < a.n_out; ++jj) {
-    const int64_t k = a.oc[jj];
-    if (k < 0 || k >= a.K) continue;
-    const float xv = act_to_f32<ACT>(a.x[static_cast<int64_t>(m) * a.K + k]);
+  for (int j0 = 0; j0 < a.n_out; j0 += G) {
+    float xv[G], wv[G][4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (nb + r < a.N)
-        v[r] += xv * act_to_f32<ACT>(a.w_out[static_cast<int64_t>(nb + r) * a.n_out + jj]);
+    for (int g = 0; g < G; ++g) {
+      const int j = min(j0 + g, a.n_out - 1);
+      const int64_t k = a.oc[j];
+      const bool ok = j0 + g < a.n_out && k >= 0 && k < a.K;
+      const int64_t kc = k < 0 ? 0 : (k >= a.K ? a.K - 1 : k);
+      const float x = act_to_f32<ACT>(a.x[xrow + kc]);
+      xv[g] = ok ? x : 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = min(nb + r, a.N - 1);
+        wv[g][r] = act_to_f32<ACT>(a.w_out[static_cast<int64_t>(n) * a.n_out + j]);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] += xv[g] * wv[g][r];
   }
   return v;
 }
@@ -382,8 +406,68 @@ __device__ __forceinline__ f16x mfma32x32x16(const u32x4& a, const u32x4& b, f16
                                                    __builtin_bit_cast(b8, b), c, 0, 0, 0);
 }
 
+// Outlier side-GEMM of a tile on the matrix cores, 16 outlier columns at a
+// time (a rank-16 update with v_mfma_f32_32x32x16, the layout of the main
+// accumulators). stage_outliers writes the tile's operands for columns
+// c0 .. c0 + 15 to LDS in one round of independent loads by the whole
+// workgroup: xo[r][0, 16) = x[m0 + r, oc[c0 ..]] (BM rows, 32 B each),
+// then wo[r][0, 16) = w_out[n0 + r, c0 ..] (256 rows). Columns past n_out
+// and indices outside [0, K) give zeros; rows past M / N are clamped for
+// the loads (their outputs are never stored). Thread t fills 16 bytes: row
+// t / 2, columns 8 (t % 2) .. + 8. A lane then reads its MFMA fragment (row
+// l % 32, columns 8 (l / 32) .. + 8) with one ds_read_b128.
+constexpr int kOutStageBytes = (256 + 256) * 32;
+
+template <int ACT, int BM>
+__device__ __forceinline__ void stage_outliers(const GemmArgs& a, int m0, int n0, int c0,
+                                               uint8_t* so) {
+  const int t = threadIdx.x, row = t >> 1, cb = c0 + 8 * (t & 1);
+  uint32_t v[8];
+  if (row < BM) {
+    const int64_t xrow = static_cast<int64_t>(min(m0 + row, a.M - 1)) * a.K;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int j = cb + e;
+      const int64_t k = a.oc[min(j, a.n_out - 1)];
+      const int64_t kc = k < 0 ? 0 : (k >= a.K ? a.K - 1 : k);
+      const uint32_t x = a.x[xrow + kc];
+      v[e] = (j < a.n_out && k >= 0 && k < a.K) ? x : 0u;
+    }
+    *reinterpret_cast<u32x4*>(so + t * 16) =
+        u32x4{v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16), v[6] | (v[7] << 16)};
+  }
+  const uint16_t* wr = a.w_out + static_cast<int64_t>(min(n0 + row, a.N - 1)) * a.n_out;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int j = cb + e;
+    v[e] = j < a.n_out ? wr[min(j, a.n_out - 1)] : 0u;
+  }
+  *reinterpret_cast<u32x4*>(so + BM * 32 + t * 16) =
+      u32x4{v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16), v[6] | (v[7] << 16)};
+}
+
 constexpr int kDmaThreads = 512;   // 8 waves, two per SIMD
 constexpr int kDmaTN = 2;          // 32-row weight tiles per wave
+
+// acc[i][j] += the side-GEMM block of the staged chunk (see stage_outliers)
+// for the wave's weight rows 32 i .. of its 64 and x rows 32 j .. of its
+// 32 TM (the accumulator layout of k_gemm_dma).
+template <int ACT, int TM>
+__device__ __forceinline__ void outlier_mfma(const uint8_t* so, int wm, int wn, int lane,
+                                             f16x (&acc)[kDmaTN][TM]) {
+  constexpr int BM = 64 * TM;
+  const int r32 = lane & 31, h = lane >> 5;
+  u32x4 wf[kDmaTN];
+#pragma unroll
+  for (int i = 0; i < kDmaTN; ++i)
+    wf[i] = *reinterpret_cast<const u32x4*>(so + BM * 32 + (wn * 64 + i * 32 + r32) * 32 + h * 16);
+#pragma unroll
+  for (int j = 0; j < TM; ++j) {
+    const u32x4 xf = *reinterpret_cast<const u32x4*>(so + (wm * TM * 32 + j * 32 + r32) * 32 + h * 16);
+#pragma unroll
+    for (int i = 0; i < kDmaTN; ++i) acc[i][j] = mfma32x32x16<ACT>(wf[i], xf, acc[i][j]);
+  }
+}
 
 // TM: 32-row x tiles per wave; the workgroup tile is 64 TM x 256 (TM = 4:
 // 256 x 256; TM = 3 or 2: 192 or 128 x 256 for small M and for tile counts
@@ -402,7 +486,11 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
   constexpr int WL = WB / (kDmaThreads * 16);   // 2
   constexpr int TN = kDmaTN;
   static_assert(TM >= 2 && TM <= 4, "x tile of 128, 192 or 256 rows");
+  // operand stages; after the main loop the outlier staging area (at the
+  // start) and the epilogue's output tiles
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * SB];
+  static_assert(kOutStageBytes <= NS * SB, "outlier stage fits in LDS");
+  uint8_t* const so = smem;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -612,6 +700,9 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
   if (SPLIT && partial) {
     // Partial tile in lane order: f4 (split, tail tile, wave, i, j, q, lane),
     // one contiguous 1 KiB store per (i, j, q); k_splitk_reduce finishes it.
+    // With outlier columns, the first k-range also stores the tile's
+    // side-GEMM block (matrix cores, see outlier_w_frag) as one more plane,
+    // after the `splits` planes, which the reduce adds after the scale.
     const int rest = a.tiles_m * a.tiles_n - a.full_tiles;
     f4* dst = reinterpret_cast<f4*>(a.part) +
               ((static_cast<int64_t>(split) * rest + ptile) * 8 + wave) * (TN * TM * 4 * 64) + lane;
@@ -623,6 +714,43 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
         for (int q = 0; q < 4; ++q)
           dst[((i * TM + j) * 4 + q) * 64] =
               f4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+    if (a.n_out > 0 && split == 0) {
+      // one block live at a time; later chunks add onto the stored plane
+      // (each lane re-reads only its own stores)
+      f4* od = reinterpret_cast<f4*>(a.part) +
+               ((static_cast<int64_t>(a.splits) * rest + ptile) * 8 + wave) * (TN * TM * 4 * 64) +
+               lane;
+      for (int c0 = 0; c0 < a.n_out; c0 += 16) {
+        __syncthreads();   // every wave is done with the operand stages / previous chunk
+        stage_outliers<ACT, BM>(a, m0, n0, c0, so);
+        __syncthreads();
+        u32x4 wf[TN];
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+          wf[i] = *reinterpret_cast<const u32x4*>(so + BM * 32 + (wn * 64 + i * 32 + r32) * 32 + h * 16);
+#pragma unroll
+        for (int j = 0; j < TM; ++j) {
+          const u32x4 xf =
+              *reinterpret_cast<const u32x4*>(so + (wm * TM * 32 + j * 32 + r32) * 32 + h * 16);
+#pragma unroll
+          for (int i = 0; i < TN; ++i) {
+            f4* o = od + ((i * TM + j) * 4) * 64;
+            f16x ob = f16x{};
+            if (c0 > 0) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const f4 v = o[q * 64];
+                ob[4 * q] = v[0]; ob[4 * q + 1] = v[1]; ob[4 * q + 2] = v[2]; ob[4 * q + 3] = v[3];
+              }
+            }
+            ob = mfma32x32x16<ACT>(wf[i], xf, ob);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              o[q * 64] = f4{ob[4 * q], ob[4 * q + 1], ob[4 * q + 2], ob[4 * q + 3]};
+          }
+        }
+      }
+    }
     return;
   }
   // Epilogue. Accumulator values 4q .. 4q+3 of tile (i, j) are the wave's
@@ -635,6 +763,30 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
   static_assert(8 * TM * 32 * EPS * 2 <= NS * SB, "epilogue tile fits in LDS");
   dma_wait_barrier<0>();     // every wave is done with the operand stages
   uint16_t* ep = reinterpret_cast<uint16_t*>(smem) + wave * (TM * 32 * EPS);
+  const bool outl = a.n_out > 0;
+  if (outl) {
+    // y = s * acc + sum_j x[m, oc[j]] w_out[n, j] + bias: the scale first, in
+    // place, then the side-GEMM accumulates onto the scaled tiles (fp32, one
+    // rank-16 MFMA update per 16 outlier columns and block)
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int n = nw + i * 32 + 8 * q + 4 * h + r;
+          const float sc = n < a.N ? act_to_f32<ACT>(a.scales[n]) : 0.0f;
+#pragma unroll
+          for (int j = 0; j < TM; ++j) acc[i][j][4 * q + r] *= sc;
+        }
+    for (int c0 = 0; c0 < a.n_out; c0 += 16) {
+      if (c0 > 0) __syncthreads();   // every wave has read the previous chunk
+      stage_outliers<ACT, BM>(a, m0, n0, c0, so);
+      __syncthreads();
+      outlier_mfma<ACT, TM>(so, wm, wn, lane, acc);
+    }
+    __syncthreads();   // the output tiles below overwrite the stage
+  }
 #pragma unroll
   for (int i = 0; i < TN; ++i) {
 #pragma unroll
@@ -644,7 +796,7 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int n = nw + nl + r;
-        sc[r] = n < a.N ? act_to_f32<ACT>(a.scales[n]) : 0.0f;
+        sc[r] = outl ? 1.0f : (n < a.N ? act_to_f32<ACT>(a.scales[n]) : 0.0f);   // x 1: exact
         bs[r] = (a.bias && n < a.N) ? act_to_f32<ACT>(a.bias[n]) : 0.0f;
       }
 #pragma unroll
@@ -652,8 +804,6 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
         f4 v;
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[r] = acc[i][j][4 * q + r] * sc[r];
-        const int m = mw + j * 32 + r32;
-        if (a.n_out > 0 && m < a.M) v = outlier_quad<ACT>(a, m, nw + nl, v);
         if (a.bias) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) v[r] += bs[r];
@@ -714,6 +864,29 @@ __global__ __launch_bounds__(kBlock) void k_splitk_reduce(GemmArgs a) {
   const int m = tm * 64 * TM + (wave & 1) * 32 * TM + j * 32 + (lane & 31);
   const int nb = tn * 256 + (wave >> 1) * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
   if (m >= a.M || nb >= a.N) return;
+  if (a.n_out > 0) {
+    // outlier block plane (after the `splits` planes): added after the scale
+    const f4 o = src[a.splits * per_split];
+    f4 v;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      v[r] = nb + r < a.N ? sum[r] * act_to_f32<ACT>(a.scales[nb + r]) + o[r] : 0.0f;
+    if (a.bias) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (nb + r < a.N) v[r] += act_to_f32<ACT>(a.bias[nb + r]);
+    }
+    uint16_t* dst = a.y + static_cast<int64_t>(m) * a.N + nb;
+    if ((a.N % 4) == 0 && nb + 3 < a.N) {
+      *reinterpret_cast<uint2*>(dst) = make_uint2(pack2_out<ACT>(v[0], v[1]),
+                                                  pack2_out<ACT>(v[2], v[3]));
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (nb + r < a.N) dst[r] = out1<ACT>(v[r]);
+    }
+    return;
+  }
   store_quad<ACT>(a, sum, m, nb, (a.N % 4) == 0);
 }
 
@@ -724,11 +897,12 @@ struct DmaPlan {
   int tm, full, splits;
 };
 
-// Bytes of split-K partials of a plan: one fp32 tile per tail tile and range.
-int64_t splitk_bytes(int64_t M, int64_t N, const DmaPlan& p) {
+// Bytes of split-K partials of a plan: one fp32 tile per tail tile and range,
+// plus one per tail tile for the outlier side-GEMM block when n_out > 0.
+int64_t splitk_bytes(int64_t M, int64_t N, const DmaPlan& p, int64_t n_out = 0) {
   if (p.splits <= 1) return 0;
   const int64_t tiles = cdiv(M, 64 * p.tm) * cdiv(N, 256);
-  return (tiles - p.full) * p.splits * (p.tm * 64) * 256 * 4;
+  return (tiles - p.full) * (p.splits + (n_out > 0 ? 1 : 0)) * (p.tm * 64) * 256 * 4;
 }
 
 template <int ACT, int TM>
@@ -1417,7 +1591,7 @@ DmaPlan split_plan(int64_t M, int64_t N, int64_t K) {
   return dma_plan(M, N, K, true);
 }
 
-Kind choose(int64_t M, int64_t N, int64_t K, size_t ws_bytes, DmaPlan& plan) {
+Kind choose(int64_t M, int64_t N, int64_t K, int64_t n_out, size_t ws_bytes, DmaPlan& plan) {
   const int64_t cus = device_cus();
   const bool stream = stream_ok(M, N, K);
   if (M <= 16)
@@ -1429,7 +1603,7 @@ Kind choose(int64_t M, int64_t N, int64_t K, size_t ws_bytes, DmaPlan& plan) {
   if (!dma_ok(M, N, K)) return M < 1024 ? kTileMid : kTileLarge;
   plan = dma_plan(M, N, K, true);
   if (plan.splits > 1 &&
-      ws_bytes >= static_cast<size_t>(CBQ_WS_CTRL_BYTES + splitk_bytes(M, N, plan)))
+      ws_bytes >= static_cast<size_t>(CBQ_WS_CTRL_BYTES + splitk_bytes(M, N, plan, n_out)))
     return kTileDmaSplit;
   if (M <= 64) return narrow;
   if (M < 384) return kTileMid;
@@ -1556,7 +1730,7 @@ int w8a16_t(const void* x, const int8_t* wq, const void* scales, const void* bia
   a.K = static_cast<int>(K);
   a.n_out = static_cast<int>(n_out);
   DmaPlan plan{4, 0, 1};
-  const Kind kind = choose(M, N, K, ws ? ws_bytes : 0, plan);
+  const Kind kind = choose(M, N, K, n_out, ws ? ws_bytes : 0, plan);
   if (kind == kTileDmaSplit)
     a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + CBQ_WS_CTRL_BYTES);
   launch_kind<ACT>(kind, a, plan, s);
@@ -1570,14 +1744,14 @@ using namespace cbq;
 
 extern "C" size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_out,
                                      int act_dtype) {
-  (void)n_out;
   if (M <= 0 || N <= 0 || K <= 0) return CBQ_WS_CTRL_BYTES;
   // fp16 / bf16 with K % 16 == 0 run the MFMA kernels (split-K partials of
   // the last wave of tiles); fp32 and K % 16 != 0 run the general kernel
   // (its partial sums). Unaligned fp16 / bf16 operands also take the general
   // kernel; with this size it then runs without a split (same results).
   const bool mfma = (act_dtype == kF16 || act_dtype == kBF16) && K % 16 == 0;
-  const int64_t bytes = mfma ? splitk_bytes(M, N, split_plan(M, N, K)) : general_split_bytes(M, N, K);
+  const int64_t bytes =
+      mfma ? splitk_bytes(M, N, split_plan(M, N, K), n_out) : general_split_bytes(M, N, K);
   return CBQ_WS_CTRL_BYTES + static_cast<size_t>(bytes);
 }
 

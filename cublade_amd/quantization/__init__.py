@@ -5,7 +5,8 @@ from .tensor import QuantizedTensor
 from .dequantizers import dequantize_tensor
 from .linear import cuBladeW8A16LinearLayer, cubladeW8A16LinearLayer
 from .quantizers import quantize_tensor, quantize_model
-from .outlier_utils import detect_outlier_columns, separate_outliers, split_weights_by_outliers
+from .outlier_utils import (detect_activation_outlier_columns, detect_outlier_columns,
+                            separate_outliers, split_weights_by_outliers)
 
 __all__ = [
     "quantize_model",
@@ -15,6 +16,7 @@ __all__ = [
     "cuBladeW8A16LinearLayer",
     "cubladeW8A16LinearLayer",
     "detect_outlier_columns",
+    "detect_activation_outlier_columns",
     "separate_outliers",
     "split_weights_by_outliers",
 ]

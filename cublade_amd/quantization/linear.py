@@ -27,7 +27,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
-from .outlier_utils import detect_outlier_columns
+from .outlier_utils import detect_activation_outlier_columns, detect_outlier_columns
 from .quantizers import quantize_tensor
 from cublade_amd.bindings.hip.w8a16 import w8a16_linear
 
@@ -41,12 +41,16 @@ class cuBladeW8A16LinearLayer(nn.Module):
         dtype=torch.bfloat16,
         handle_outliers=False,
         outlier_threshold=6.0,
+        outlier_mode="weight",
     ):
         super().__init__()
+        if outlier_mode not in ("weight", "activation"):
+            raise ValueError(f"outlier_mode must be 'weight' or 'activation', got {outlier_mode!r}")
         self.in_features = in_features
         self.out_features = out_features
         self.handle_outliers = handle_outliers
         self.outlier_threshold = outlier_threshold
+        self.outlier_mode = outlier_mode
         self.register_buffer("int8_weights",
                              torch.empty(out_features, in_features, dtype=torch.int8))
         self.register_buffer("scales", torch.ones(out_features, dtype=dtype))
@@ -56,14 +60,22 @@ class cuBladeW8A16LinearLayer(nn.Module):
         self.bias = nn.Parameter(torch.zeros(out_features, dtype=dtype)) if bias else None
 
     @torch.no_grad()
-    def quantize(self, weight_fp: torch.Tensor):
+    def quantize(self, weight_fp: torch.Tensor, activations: torch.Tensor | None = None):
         """Quantize a [out, in] weight per output channel (INT8, symmetric).
 
-        With handle_outliers, the columns holding any |w| > outlier_threshold
-        are kept in the weight's dtype for the side-GEMM and zeroed in the
-        INT8 copy (so their scales come from the normal columns only, as in
-        linear.py:48-66). The quantization itself runs on the GPU.
+        With handle_outliers, the outlier columns are kept in the weight's
+        dtype for the side-GEMM and zeroed in the INT8 copy (so their scales
+        come from the normal columns only, as in linear.py:48-66). Which
+        columns: outlier_mode "weight" (the reference's rule, the default):
+        any |w| > outlier_threshold in the column; "activation" (opt-in,
+        LLM.int8's rule): any |x| > outlier_threshold in that input feature
+        of `activations`, a calibration batch [..., in_features] that this
+        mode requires. The quantization itself runs on the GPU.
         """
+        if self.handle_outliers and self.outlier_mode == "activation" and (
+                activations is None or activations.shape[-1] != self.in_features):
+            raise ValueError("outlier_mode='activation' needs a calibration batch "
+                             f"[..., {self.in_features}] passed as activations=")
         home = weight_fp.device
         w = weight_fp.detach()
         w = (w if w.is_cuda else w.cuda()).contiguous()
@@ -71,7 +83,11 @@ class cuBladeW8A16LinearLayer(nn.Module):
             raise ValueError(f"weight must be [{self.out_features}, {self.in_features}], "
                              f"got {tuple(w.shape)}")
         if self.handle_outliers:
-            outlier_cols = detect_outlier_columns(w, threshold=self.outlier_threshold)
+            if self.outlier_mode == "activation":
+                outlier_cols = detect_activation_outlier_columns(activations,
+                                                                 self.outlier_threshold)
+            else:
+                outlier_cols = detect_outlier_columns(w, threshold=self.outlier_threshold)
             outlier_set = set(outlier_cols)
             normal_cols = [c for c in range(self.in_features) if c not in outlier_set]
             self.outlier_weights = w[:, outlier_cols].to(home)

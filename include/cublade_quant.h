@@ -194,7 +194,8 @@ int cbq_dequant_int8_group_nd(const int8_t* q, const float* scale,
  * last wave of output tiles is short, the fp32 partial tiles of that wave
  * (ranges x tail tiles x 256 / 192 / 128 KiB for tiles of 256 / 192 / 128 x
  * 256; at most 16 ranges and at most one partial tile per CU, i.e. <= 64 MiB
- * on MI355X), else nothing. CBQ_F32 and K % 16 != 0 (general kernel): fp32
+ * on MI355X), with n_out > 0 one more tile per tail tile for the outlier
+ * side-GEMM block, else nothing. CBQ_F32 and K % 16 != 0 (general kernel): fp32
  * partial sums, up to 16 x M x N x 4 bytes when its tiles give fewer than
  * two workgroups per CU. The reference allocates its temporaries inside the
  * forward (linear.py:105-131). */

@@ -220,12 +220,12 @@ def test_splitk_large_m_few_tiles(M, K, N):
 @pytest.mark.parametrize("M,K,N,dt,n_out,path", [
     (128, 4096, 11008, torch.float16, 3, "128-row tiles, K in 4 ranges"),
     (512, 4096, 11008, torch.bfloat16, 0, "128-row tiles, whole"),
-    (2137, 2048, 8192, torch.bfloat16, 2, "128-row tiles, 512 whole + the rest over 4 ranges"),
-    (768, 4096, 11008, torch.float16, 2, "192-row tiles, whole (172 tiles in one wave)"),
+    (2137, 2048, 8192, torch.bfloat16, 20, "128-row tiles, 512 whole + the rest over 4 ranges"),
+    (768, 4096, 11008, torch.float16, 33, "192-row tiles, whole (172 tiles in one wave)"),
     (139, 4096, 11008, torch.bfloat16, 1, "192-row tiles, K in 4 ranges, M tail"),
     (2211, 1024, 11008, torch.float16, 0, "192-row tiles, 512 whole + the rest over 4 ranges"),
     (1536, 4096, 11008, torch.bfloat16, 2, "256-row tiles, 256 whole + 2 over 16 ranges"),
-    (3000, 1024, 5500, torch.float16, 0, "256-row tiles, 256 whole + 8 over 4 ranges, M and N tails"),
+    (3000, 1024, 5500, torch.float16, 18, "256-row tiles, 256 whole + 8 over 4 ranges, M and N tails"),
     (64, 11008, 4096, torch.float16, 2, "M <= 64 with long K: 128-row tiles over 11 ranges"),
     (32, 11008, 4096, torch.bfloat16, 1, "M = 32 with long K: 128-row tiles over 11 ranges"),
     (40, 16384, 1000, torch.bfloat16, 0, "M <= 64 with long K, N tail"),
@@ -300,6 +300,41 @@ def test_config5_shapes(M):
     # whole output against a GPU fp32 product of the same operands
     wf = layer.int8_weights.float() * layer.scales.float()[:, None]
     ref_full = x.to(DEV).float() @ wf.t().contiguous()
+    torch.testing.assert_close(y.float(), ref_full, **TOL)
+
+
+@pytest.mark.parametrize("M", [16, 256, 4096])
+def test_config5_activation_outliers(M):
+    """BASELINE config 5 with the outlier threshold 6.0 applied the LLM.int8
+    way (the layer's opt-in activation mode): the 6 feature columns of x at
+    magnitude U(8, 20) become outlier columns, their weights stay fp16 for the
+    side-GEMM and are zero in the INT8 copy; rows against the oracle (one in
+    every 64-row block) and the whole output against an fp32 product."""
+    from cublade_amd.benchmark import configs
+    from cublade_amd.quantization import cuBladeW8A16LinearLayer
+    x, w = configs.c5_w8a16(M)
+    K, N = x.shape[1], w.shape[0]
+    layer = cuBladeW8A16LinearLayer(K, N, bias=False, dtype=torch.float16, handle_outliers=True,
+                                    outlier_threshold=6.0, outlier_mode="activation")
+    layer.quantize(w.to(DEV), activations=x)
+    oc = layer.outlier_cols.tolist()
+    g = torch.Generator().manual_seed(4)
+    torch.randn(M, K, generator=g)
+    want = torch.sort(torch.randperm(K, generator=g)[:6]).values.tolist()
+    assert oc == want, (oc, want)
+    wq = layer.int8_weights
+    assert int(wq[:, oc].abs().sum()) == 0
+    xd = x.to(DEV)
+    y = layer(xd)
+    rows = (np.arange(M) if M <= 16 else
+            np.unique(np.r_[0, M - 1, [b * 64 + (b * 29 + 3) % 64 for b in range(M // 64)]])
+            .astype(np.int64))
+    ref = oracle_y(bits(x), oracle.F16, bits(wq), bits(layer.scales), oc=oc,
+                   w_out=bits(layer.outlier_weights), rows=rows)
+    np.testing.assert_allclose(y.float().cpu().numpy()[rows], ref, **TOL)
+    wf = wq.float() * layer.scales.float()[:, None]
+    ref_full = xd.float() @ wf.t().contiguous() + \
+        xd.float()[:, oc] @ layer.outlier_weights.float().t().contiguous()
     torch.testing.assert_close(y.float(), ref_full, **TOL)
 
 

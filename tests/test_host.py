@@ -391,3 +391,26 @@ def test_reference_import_name_resolves_without_gpu():
     for missing in ("cublade.kernels", "cublade.bindings.triton"):
         with pytest.raises(ImportError):
             importlib.import_module(missing)
+
+
+def test_activation_outlier_columns_and_mode_checks():
+    """LLM.int8's activation criterion (opt-in layer mode): a feature is an
+    outlier when any |x| in it is > threshold (strict), NaN never counts,
+    every leading dimension is reduced; the layer rejects an unknown mode
+    and an activation mode without a calibration batch before any GPU work."""
+    from cublade_amd.quantization import (cuBladeW8A16LinearLayer,
+                                          detect_activation_outlier_columns)
+    x = torch.zeros(2, 3, 8)
+    x[0, 1, 2] = 6.5
+    x[1, 2, 5] = -7.0
+    x[0, 0, 4] = 6.0                 # not > threshold
+    x[1, 0, 7] = float("nan")
+    assert detect_activation_outlier_columns(x, 6.0) == [2, 5]
+    assert detect_activation_outlier_columns(x, 7.5) == []
+    with pytest.raises(ValueError, match="outlier_mode"):
+        cuBladeW8A16LinearLayer(8, 4, outlier_mode="rows")
+    layer = cuBladeW8A16LinearLayer(8, 4, handle_outliers=True, outlier_mode="activation")
+    with pytest.raises(ValueError, match="calibration batch"):
+        layer.quantize(torch.zeros(4, 8))
+    with pytest.raises(ValueError, match="calibration batch"):
+        layer.quantize(torch.zeros(4, 8), activations=torch.zeros(3, 7))
