@@ -1,7 +1,7 @@
 #!/bin/bash
 # Profiles the benchmark workloads with rocprofv3 and writes text summaries.
 #
-#   bash cublade_amd/benchmark/profile.sh OUTDIR
+#   bash cublade_amd/benchmark/profile.sh OUTDIR [RAWDIR]
 #
 # 1. kernel trace of bench.py (BASELINE configs[1] step, the roofline
 #    rotations and the other configs' extras)
@@ -9,21 +9,23 @@
 #    256 MiB device copy (copy_calib.py) to calibrate both counters: the
 #    headline kernels' HBM bytes per launch
 # 3. the per-config suite: HIP-event timings from a run without the profiler
-#    (suite.json; the tracer's per-launch host cost would otherwise show in
+#    (suite_configs.json; the tracer's per-launch host cost would otherwise show in
 #    host-bound ops), then a kernel trace, then FETCH_SIZE / WRITE_SIZE runs
 #    of configs 1-5 (every suite kernel's HBM bytes per dispatch)
 # 4. rocprof's derived MfmaUtil counter (MFMA busy cycles over active cycles
 #    x SIMDs) for the MFMA kernels: W8A16 (config 5) and the dense GEMM (f4)
 # Summaries: OUTDIR/bench_c2_kernels.txt, OUTDIR/quant_int8_c2_traffic.json,
 # OUTDIR/dequant_int8_c2_traffic.json, OUTDIR/suite_kernels.txt,
-# OUTDIR/suite_traffic.txt, OUTDIR/suite.json, OUTDIR/mfma_util.txt. Raw
-# databases stay in OUTDIR/raw.
+# OUTDIR/suite_traffic.txt, OUTDIR/suite_configs.json, OUTDIR/mfma_util.txt. Raw
+# databases go to RAWDIR (default OUTDIR/raw; they total about 80 MiB), the
+# programs' output to OUTDIR/logs.
 # Run from the repository root on a GPU machine. Every GPU step has its own
 # time limit; the script stops at the first failing step.
 set -u
-OUT=${1:?usage: profile.sh OUTDIR}
-RAW="$OUT/raw"
-mkdir -p "$RAW"
+OUT=${1:?usage: profile.sh OUTDIR [RAWDIR]}
+RAW=${2:-"$OUT/raw"}
+LOGS="$OUT/logs"
+mkdir -p "$RAW" "$LOGS"
 export TMPDIR=/tmp
 PY="python -u"
 R="python -m cublade_amd.benchmark.rocprof"
@@ -33,33 +35,33 @@ step() { echo "[profile] $*"; }
 
 step "kernel trace: bench.py"
 timeout -k 10 300 rocprofv3 --kernel-trace --stats -d "$RAW/trace" -o bench -- \
-  $PY bench.py --no-cpu > "$RAW/trace.log" 2>&1 || exit $?
+  $PY bench.py --no-cpu > "$LOGS/trace.log" 2>&1 || exit $?
 step "counter FETCH_SIZE: bench.py"
 timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE --kernel-trace -d "$RAW/fetch" -o bench -- \
-  $PY $BENCH_SHORT > "$RAW/fetch.log" 2>&1 || exit $?
+  $PY $BENCH_SHORT > "$LOGS/fetch.log" 2>&1 || exit $?
 step "counter WRITE_SIZE: bench.py"
 timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE --kernel-trace -d "$RAW/write" -o bench -- \
-  $PY $BENCH_SHORT > "$RAW/write.log" 2>&1 || exit $?
+  $PY $BENCH_SHORT > "$LOGS/write.log" 2>&1 || exit $?
 step "counter FETCH_SIZE: 256 MiB copy"
 timeout -s KILL 60 rocprofv3 --pmc FETCH_SIZE --kernel-trace -d "$RAW/cal_fetch" -o calib -- \
-  $PY -m cublade_amd.benchmark.copy_calib > "$RAW/cal_fetch.log" 2>&1 || exit $?
+  $PY -m cublade_amd.benchmark.copy_calib > "$LOGS/cal_fetch.log" 2>&1 || exit $?
 step "counter WRITE_SIZE: 256 MiB copy"
 timeout -s KILL 60 rocprofv3 --pmc WRITE_SIZE --kernel-trace -d "$RAW/cal_write" -o calib -- \
-  $PY -m cublade_amd.benchmark.copy_calib > "$RAW/cal_write.log" 2>&1 || exit $?
+  $PY -m cublade_amd.benchmark.copy_calib > "$LOGS/cal_write.log" 2>&1 || exit $?
 step "suite (HIP-event timing, no profiler attached)"
-timeout -k 10 500 $PY -m cublade_amd.benchmark.suite --json "$OUT/suite.json" > "$RAW/suite_plain.log" 2>&1 || exit $?
+timeout -k 10 500 $PY -m cublade_amd.benchmark.suite --json "$OUT/suite_configs.json" > "$LOGS/suite_plain.log" 2>&1 || exit $?
 step "kernel trace: suite"
 timeout -k 10 500 rocprofv3 --kernel-trace --stats -d "$RAW/suite" -o suite -- \
-  $PY -m cublade_amd.benchmark.suite --reps 10 > "$RAW/suite.log" 2>&1 || exit $?
+  $PY -m cublade_amd.benchmark.suite --reps 10 > "$LOGS/suite.log" 2>&1 || exit $?
 step "counter FETCH_SIZE: suite configs c1-c5"
 timeout -s KILL 300 rocprofv3 --pmc FETCH_SIZE --kernel-trace -d "$RAW/sfetch" -o suite -- \
-  $PY -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5 --reps 3 --warmup 1 > "$RAW/sfetch.log" 2>&1 || exit $?
+  $PY -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5 --reps 3 --warmup 1 > "$LOGS/sfetch.log" 2>&1 || exit $?
 step "counter WRITE_SIZE: suite configs c1-c5"
 timeout -s KILL 300 rocprofv3 --pmc WRITE_SIZE --kernel-trace -d "$RAW/swrite" -o suite -- \
-  $PY -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5 --reps 3 --warmup 1 > "$RAW/swrite.log" 2>&1 || exit $?
+  $PY -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5 --reps 3 --warmup 1 > "$LOGS/swrite.log" 2>&1 || exit $?
 step "counter MfmaUtil: suite configs c5,f4"
 timeout -s KILL 300 rocprofv3 --pmc MfmaUtil --kernel-trace -d "$RAW/mfma" -o suite -- \
-  $PY -m cublade_amd.benchmark.suite --configs c5,f4 --reps 3 --warmup 1 > "$RAW/mfma.log" 2>&1 || exit $?
+  $PY -m cublade_amd.benchmark.suite --configs c5,f4 --reps 3 --warmup 1 > "$LOGS/mfma.log" 2>&1 || exit $?
 
 step "summaries"
 CAL="$RAW/cal_fetch/calib_results.db $RAW/cal_write/calib_results.db 262144"
@@ -70,7 +72,7 @@ CAL="$RAW/cal_fetch/calib_results.db $RAW/cal_write/calib_results.db 262144"
   $R kernels "$RAW/trace/bench_results.db"
   echo
   echo "# bench.py output line under the profiler:"
-  grep '"metric"' "$RAW/trace.log"
+  grep '"metric"' "$LOGS/trace.log"
 } > "$OUT/bench_c2_kernels.txt" || exit $?
 traffic_json() {   # KERNEL ALGO_BYTES OUTFILE
   $R traffic "$1" "$RAW/fetch/bench_results.db" "$RAW/write/bench_results.db" $CAL \

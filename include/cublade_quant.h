@@ -45,10 +45,18 @@ enum { CBQ_OK = 0, CBQ_EINVAL = 1, CBQ_ELAUNCH = 2 };
 
 /* Workspace contract.  Entry points that take (ws, ws_bytes) need a
  * 16-byte aligned device buffer of at least the size their *_ws_bytes query
- * returns. The first CBQ_WS_CTRL_BYTES bytes are a control block reserved for
- * counters: zero-filled before the first call, and left zero-filled by every
- * call; the rest is per-call scratch. One workspace serves one stream at a
- * time: calls that overlap in time must not share it. */
+ * returns. The first CBQ_WS_CTRL_BYTES bytes are a control block: zero-fill
+ * it once before the first call on that workspace and do not write to it
+ * afterwards (zero-filling all of it again is allowed between calls: it
+ * resets it). The per-tensor quant entry points keep their cross-workgroup
+ * state there (a generation counter at byte 0, tagged per-workgroup slots
+ * from byte 1024) and a sticky int32 status word at byte 512: nonzero after
+ * a call whose workgroups gave up waiting for each other, after which every
+ * per-tensor call on that workspace writes a NaN scale (FP8 codes NaN, INT8
+ * codes 0) until the block is zero-filled again. The other entry points
+ * leave the control block alone. The rest is per-call scratch. One workspace
+ * serves one stream at a time: calls that overlap in time must not share
+ * it. */
 #define CBQ_WS_CTRL_BYTES 16384
 
 /* Message of the last failed call on this thread ("" if none). */
