@@ -841,32 +841,20 @@ void launch_gemm_dma(GemmArgs a, hipStream_t s) {
   k_gemm_dma<ACT, false, TM><<<dim3(grid), dim3(kDmaThreads), 0, s>>>(a);
 }
 
-// Split-K finish: one thread per partial f4 (4 outputs y[m, n .. n+3]) of a
-// tail tile; sums the splits in order (deterministic), then scale, outliers,
-// bias and one rounding, as in the tile kernels' epilogue. Partial index,
-// fastest first: lane (64), q (4), j (TM), i (2), wave (8), tail tile.
-template <int ACT, int TM>
-__global__ __launch_bounds__(kBlock) void k_splitk_reduce(GemmArgs a) {
-  constexpr int kWaveF4 = kDmaTN * TM * 4 * 64;
-  constexpr int kTileF4 = 8 * kWaveF4;
-  const int rest = a.tiles_m * a.tiles_n - a.full_tiles;
-  const int64_t per_split = static_cast<int64_t>(rest) * kTileF4;
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-  if (idx >= per_split) return;
-  const f4* src = reinterpret_cast<const f4*>(a.part) + idx;
-  f4 sum = src[0];
-  for (int sp = 1; sp < a.splits; ++sp) sum += src[sp * per_split];
-  const int w = static_cast<int>(idx % kWaveF4);
-  const int lane = w & 63, q = (w >> 6) & 3, j = (w >> 8) % TM, i = (w >> 8) / TM;
-  const int wave = static_cast<int>((idx / kWaveF4) & 7);
-  int tm, tn;
-  group_tile(a.full_tiles + static_cast<int>(idx / kTileF4), a, tm, tn);
-  const int m = tm * 64 * TM + (wave & 1) * 32 * TM + j * 32 + (lane & 31);
-  const int nb = tn * 256 + (wave >> 1) * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
+// Split-K finish: each thread takes two partial f4 of a tail tile, kBlock
+// apart (4 outputs y[m, n .. n+3] each); sums the splits in order
+// (deterministic), then scale, outliers, bias and one rounding, as in the
+// tile kernels' epilogue. Partial index, fastest first: lane (64), q (4),
+// j (TM), i (2), wave (8), tail tile.
+constexpr int kReduceF4 = 2;   // partial f4 per thread
+
+template <int ACT>
+__device__ __forceinline__ void splitk_finish(const GemmArgs& a, f4 sum, const f4* oplane,
+                                              int m, int nb) {
   if (m >= a.M || nb >= a.N) return;
   if (a.n_out > 0) {
     // outlier block plane (after the `splits` planes): added after the scale
-    const f4 o = src[a.splits * per_split];
+    const f4 o = *oplane;
     f4 v;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -888,6 +876,54 @@ __global__ __launch_bounds__(kBlock) void k_splitk_reduce(GemmArgs a) {
     return;
   }
   store_quad<ACT>(a, sum, m, nb, (a.N % 4) == 0);
+}
+
+template <int ACT, int TM>
+__global__ __launch_bounds__(kBlock) void k_splitk_reduce(GemmArgs a) {
+  constexpr int kWaveF4 = kDmaTN * TM * 4 * 64;
+  constexpr int kTileF4 = 8 * kWaveF4;
+  static_assert(kTileF4 % (kBlock * kReduceF4) == 0, "a thread's f4 share a tile");
+  const int rest = a.tiles_m * a.tiles_n - a.full_tiles;
+  const int64_t per_split = static_cast<int64_t>(rest) * kTileF4;
+  const int64_t idx0 = static_cast<int64_t>(blockIdx.x) * (kBlock * kReduceF4) + threadIdx.x;
+  if (idx0 >= per_split) return;   // then every idx0 + u * kBlock is in range
+  const f4* src = reinterpret_cast<const f4*>(a.part) + idx0;
+  // planes summed in order 0, 1, ..., splits - 1 (deterministic); the loads
+  // of up to 8 planes are issued before their adds (a plane at a time was
+  // latency-bound: 6.2 us for 2 tail tiles over 16 ranges)
+  f4 sum[kReduceF4];
+#pragma unroll
+  for (int u = 0; u < kReduceF4; ++u) sum[u] = src[u * kBlock];
+  int sp = 1;
+  for (; sp + 4 <= a.splits; sp += 4) {
+    f4 v[4][kReduceF4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int u = 0; u < kReduceF4; ++u) v[p][u] = src[(sp + p) * per_split + u * kBlock];
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int u = 0; u < kReduceF4; ++u) sum[u] += v[p][u];
+  }
+  for (; sp < a.splits; ++sp) {
+    f4 v[kReduceF4];
+#pragma unroll
+    for (int u = 0; u < kReduceF4; ++u) v[u] = src[sp * per_split + u * kBlock];
+#pragma unroll
+    for (int u = 0; u < kReduceF4; ++u) sum[u] += v[u];
+  }
+  int tm, tn;
+  group_tile(a.full_tiles + static_cast<int>(idx0 / kTileF4), a, tm, tn);
+#pragma unroll
+  for (int u = 0; u < kReduceF4; ++u) {
+    const int w = static_cast<int>((idx0 + u * kBlock) % kWaveF4);
+    const int lane = w & 63, q = (w >> 6) & 3, j = (w >> 8) % TM, i = (w >> 8) / TM;
+    const int wave = static_cast<int>(((idx0 + u * kBlock) / kWaveF4) & 7);
+    const int m = tm * 64 * TM + (wave & 1) * 32 * TM + j * 32 + (lane & 31);
+    const int nb = tn * 256 + (wave >> 1) * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
+    splitk_finish<ACT>(a, sum[u], src + a.splits * per_split + u * kBlock, m, nb);
+  }
 }
 
 // Launch plan of the k_gemm_dma path: x tile of 64 tm rows; tiles
@@ -917,7 +953,8 @@ void launch_gemm_dma_splitk(GemmArgs a, const DmaPlan& p, hipStream_t s) {
   const unsigned grid = static_cast<unsigned>(a.full_tiles + rest * a.splits);
   k_gemm_dma<ACT, true, TM><<<dim3(grid), dim3(kDmaThreads), 0, s>>>(a);
   const int64_t n4 = static_cast<int64_t>(rest) * 8 * kDmaTN * TM * 4 * 64;
-  k_splitk_reduce<ACT, TM><<<dim3(static_cast<unsigned>(cdiv(n4, kBlock))), dim3(kBlock), 0, s>>>(a);
+  k_splitk_reduce<ACT, TM><<<dim3(static_cast<unsigned>(cdiv(n4, kBlock * kReduceF4))),
+                             dim3(kBlock), 0, s>>>(a);
 }
 
 // Small M (M <= 16 * TM): weight streaming. A workgroup owns 16 * TN weight
@@ -1206,9 +1243,9 @@ __global__ __launch_bounds__(64 * kStreamWaves) void k_stream(GemmArgs a) {
 //
 // One 16-wave workgroup owns 3 consecutive row tiles (48 weight rows).
 // Every wave issues all of its weight loads at once, as 1 KiB row-contiguous
-// requests (wave w: rows 3 w .. 3 w + 2, each row's 4 KiB in sequence; 64
-// lanes x 16 bytes per request), which stream from HBM far faster than MFMA-shaped
-// requests (16 rows x 64 bytes). Per 1024-k step the rows are written to a
+// requests (wave w: rows 3 w .. 3 w + 2, step by step; 64 lanes x 16 bytes
+// per request), which stream from HBM far faster than MFMA-shaped requests
+// (16 rows x 64 bytes). Per 1024-k step the rows are written to a
 // padded LDS stage (row stride 1040 bytes: the 16 rows of a fragment read
 // fall in distinct bank groups), one barrier, and read back in the MFMA
 // layout: wave w takes 64-k block w of the step for all 3 tiles, with its
@@ -1234,30 +1271,6 @@ __global__ __launch_bounds__(1024) void k_stream1(GemmArgs a) {
   const int n0 = blockIdx.x * kStream1Rows;
   const int nsteps = a.K / 1024;
 
-  // Weight rows n0 + 3 wave + i (clamped), issued row by row so that each
-  // row's 4 KiB is requested in sequence.
-  u32x4 wr[NST][RT];
-#pragma unroll
-  for (int i = 0; i < RT; ++i)
-#pragma unroll
-    for (int s = 0; s < NST; ++s) {
-      const int n = min(n0 + 3 * wave + i, a.N - 1);
-      const int sc = min(s, nsteps - 1);
-      wr[s][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-          a.wq + static_cast<int64_t>(n) * a.K + sc * 1024 + lane * 16));
-    }
-  // x fragments of block `wave` of every step (row `row`, rows past M
-  // repeat row M - 1; their outputs are never stored).
-  const int mr = min(row, a.M - 1);
-  u32x4 xl[NST], xh[NST];
-#pragma unroll
-  for (int s = 0; s < NST; ++s) {
-    const int sc = min(s, nsteps - 1);
-    const u32x4* xp = reinterpret_cast<const u32x4*>(
-        a.x + static_cast<int64_t>(mr) * a.K + sc * 1024 + wave * 64 + 16 * g);
-    xl[s] = xp[0];
-    xh[s] = xp[1];
-  }
   // Scale and bias of this lane's outputs (wave r < 3 finishes tile r).
   const int nq = n0 + wave * 16 + g * 4;
   const uint16_t* bsrc = a.bias ? a.bias : a.scales;
@@ -1267,6 +1280,33 @@ __global__ __launch_bounds__(1024) void k_stream1(GemmArgs a) {
     const int n = min(nq + q, a.N - 1);
     sraw[q] = a.scales[n];
     braw[q] = bsrc[n];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // Loads in step order: the x fragments of block `wave` of step s (row
+  // `row`; rows past M repeat row M - 1, their outputs are never stored),
+  // then step s of this wave's weight rows n0 + 3 wave + i (clamped), each
+  // a 1 KiB row-contiguous request. Loads complete in issue order, so step
+  // s can start once its own loads have landed. Pinned with scheduling
+  // barriers; measured at M = 16, N = 11008, K = 4096: 15.3 us event-timed,
+  // against 16.3 us with each row's four steps issued together and x last,
+  // and 16.8 us with all of x first.
+  const int mr = min(row, a.M - 1);
+  u32x4 xl[NST], xh[NST], wr[NST][RT];
+#pragma unroll
+  for (int s = 0; s < NST; ++s) {
+    const int sc = min(s, nsteps - 1);
+    const u32x4* xp = reinterpret_cast<const u32x4*>(
+        a.x + static_cast<int64_t>(mr) * a.K + sc * 1024 + wave * 64 + 16 * g);
+    xl[s] = xp[0];
+    xh[s] = xp[1];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      const int n = min(n0 + 3 * wave + i, a.N - 1);
+      wr[s][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+          a.wq + static_cast<int64_t>(n) * a.K + sc * 1024 + lane * 16));
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   f4 acc[RT];
@@ -1486,7 +1526,15 @@ __global__ __launch_bounds__(kBlock) void k_general_reduce(GenArgs a) {
   const int64_t mn = a.M * a.N;
   if (idx >= mn) return;
   float sum = a.part[idx];
-  for (int sp = 1; sp < a.splits; ++sp) sum += a.part[sp * mn + idx];
+  int sp = 1;
+  for (; sp + 8 <= a.splits; sp += 8) {   // in order; 8 loads issued before their adds
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = a.part[(sp + u) * mn + idx];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) sum += v[u];
+  }
+  for (; sp < a.splits; ++sp) sum += a.part[sp * mn + idx];
   general_out<ACT>(a, idx / a.N, idx % a.N, sum);
 }
 
