@@ -55,9 +55,13 @@ SIGNATURES = {
     "cbq_dequant_int8_group": (_I32, [_P, _P, _I64, _I64, _P, _I32, _P]),
     "cbq_quant_int8_channel_nd_ws_bytes": (_SZ, [_I64, _I64, _I64]),
     "cbq_quant_int8_channel_nd": (_I32, [_P, _I32, _I64, _I64, _I64, _F, _P, _SZ, _P, _P, _P]),
-    "cbq_quant_int8_group_nd": (_I32, [_P, _I32, _I64, _I64, _I64, _I64, _F, _P, _P, _P]),
+    "cbq_quant_int8_group_nd_ws_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
+    "cbq_quant_int8_group_nd": (_I32, [_P, _I32, _I64, _I64, _I64, _I64, _F, _P, _SZ, _P, _P,
+                                       _P]),
     "cbq_dequant_int8_channel_nd": (_I32, [_P, _P, _I64, _I64, _I64, _P, _I32, _P]),
-    "cbq_dequant_int8_group_nd": (_I32, [_P, _P, _I64, _I64, _I64, _I64, _P, _I32, _P]),
+    "cbq_dequant_int8_group_nd_ws_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
+    "cbq_dequant_int8_group_nd": (_I32, [_P, _P, _I64, _I64, _I64, _I64, _P, _SZ, _P, _I32,
+                                         _P]),
     "cbq_w8a16_ws_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I32]),
     "cbq_w8a16_linear": (_I32, [_P, _I32, _P, _P, _P, _P, _I64, _P, _I64, _I64, _I64,
                                 _P, _SZ, _P, _P]),

@@ -160,8 +160,10 @@ def dequantize_per_group_int8_nd(
         return y
     L = _abi.lib()
     with _abi.on_device(q.device):
+        ws = _abi.workspace(q.device,
+                            L.cbq_dequant_int8_group_nd_ws_bytes(outer, Lq, inner, group_size))
         rc = L.cbq_dequant_int8_group_nd(_abi.ptr(q), _abi.ptr(scale), outer, Lq, inner,
-                                         group_size, _abi.ptr(y), out,
+                                         group_size, _abi.ptr(ws), ws.numel(), _abi.ptr(y), out,
                                          _abi.stream_handle(q.device))
     _abi.check(rc, "dequantize_per_group_int8_nd")
     return y

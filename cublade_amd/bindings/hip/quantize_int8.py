@@ -179,8 +179,9 @@ def quantize_per_group_int8_nd(
         return q, scale
     L = _abi.lib()
     with _abi.on_device(dev):
+        ws = _abi.workspace(dev, L.cbq_quant_int8_group_nd_ws_bytes(outer, Lx, inner, group_size))
         rc = L.cbq_quant_int8_group_nd(_abi.ptr(x), code, outer, Lx, inner, group_size,
-                                       float(eps), _abi.ptr(q), _abi.ptr(scale),
-                                       _abi.stream_handle(dev))
+                                       float(eps), _abi.ptr(ws), ws.numel(), _abi.ptr(q),
+                                       _abi.ptr(scale), _abi.stream_handle(dev))
     _abi.check(rc, "quantize_per_group_int8_nd")
     return q, scale

@@ -269,7 +269,12 @@ __global__ __launch_bounds__(kBlock) void k_deq_group_strided(
 // len / G floats apart) than they gain.
 constexpr int kDgCols = kWave * 8;
 
-template <int OUT, int NW>
+// TS: scale is group-major scratch [outer, ng, inner] (the movedim order
+// transposed by k_transpose_f32 beforehand), so a thread's eight scales are
+// two contiguous 16-byte loads and short walks pay: RPTC > 0 is the walk
+// rounded up to a power of two at compile time (unguarded loads, clamped
+// past rpt; stores guarded).
+template <int OUT, int NW, bool TS = false, int RPTC = 0>
 __global__ __launch_bounds__(NW * kWave) void k_deq_group_tile(
     const int8_t* __restrict__ q, const float* __restrict__ scale, int64_t len, int64_t inner,
     int64_t G, int rpt, int64_t ng, int64_t tiles, void* __restrict__ y) {
@@ -279,10 +284,32 @@ __global__ __launch_bounds__(NW * kWave) void k_deq_group_tile(
   const int64_t i = ti * kDgCols + lane * 8;
   if (i >= inner) return;
   float s[8];
+  if constexpr (TS) {
+    const float4* sp = reinterpret_cast<const float4*>(scale + (o * ng + g) * inner + i);
+    const float4 a = sp[0], c = sp[1];
+    s[0] = a.x; s[1] = a.y; s[2] = a.z; s[3] = a.w; s[4] = c.x; s[5] = c.y; s[6] = c.z; s[7] = c.w;
+  } else {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) s[j] = scale[(o * inner + i + j) * ng + g];
+    for (int j = 0; j < 8; ++j) s[j] = scale[(o * inner + i + j) * ng + g];
+  }
   const int64_t base = (o * len + g * G + w) * inner + i;
   const int64_t rs = static_cast<int64_t>(NW) * inner;
+  if constexpr (RPTC > 0) {
+    uint2 raw[RPTC];
+#pragma unroll
+    for (int k = 0; k < RPTC; ++k) raw[k] = ldg8(q + base + min(k, rpt - 1) * rs);
+#pragma unroll
+    for (int k = 0; k < RPTC; ++k)
+      if (k < rpt) {
+        float f[8];
+        int8x4_to_f32(raw[k].x, f);
+        int8x4_to_f32(raw[k].y, f + 4);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] *= s[j];
+        st8<OUT>(y, base + k * rs, f);
+      }
+    return;
+  }
   for (int k0 = 0; k0 < rpt; k0 += 8) {
     uint2 raw[8];
 #pragma unroll
@@ -411,6 +438,46 @@ void launch_deq_group_tile(const int8_t* q, const float* scale, int64_t outer, i
       q, scale, len, inner, G, static_cast<int>(G / NW), ng, tiles, y);
 }
 
+// Scale scratch for the tiled group dequant: ng > 1 and a 32-bit transpose
+// grid (as in the group quant).
+bool deq_group_scratch_applies(int64_t outer, int64_t ng, int64_t inner) {
+  return ng > 1 && outer * cdiv(ng, static_cast<int64_t>(kTrTile)) *
+                           cdiv(inner, static_cast<int64_t>(kTrTile)) < (1LL << 31);
+}
+
+// The scratch path: the scales transposed to group-major [outer, ng, inner]
+// in tmp, then 8 waves per group (G % 8 == 0, G <= 128: walks of at most 16
+// positions, compile-time) or the 1-2 wave tiles reading the scratch.
+template <int OUT>
+void launch_deq_group_scratch(const int8_t* q, const float* scale, int64_t outer, int64_t len,
+                              int64_t inner, int64_t G, float* tmp, void* y, hipStream_t s) {
+  const int64_t ng = len / G, tiles = cdiv(inner, kDgCols);
+  const int64_t rt = cdiv(inner, static_cast<int64_t>(kTrTile));
+  const int64_t ct = cdiv(ng, static_cast<int64_t>(kTrTile));
+  k_transpose_f32<<<dim3(static_cast<unsigned>(outer * rt * ct)), dim3(kBlock), 0, s>>>(
+      scale, inner, ng, rt, ct, (ng % 4 == 0 && aligned(scale, 16)) ? 1 : 0, 1, tmp);
+  const int64_t nblocks = outer * tiles * ng;
+  const dim3 grid(static_cast<unsigned>(nblocks));
+  if (G % 8 == 0 && G / 8 <= 16) {
+    const int rpt = static_cast<int>(G / 8);
+    const dim3 block(8 * kWave);
+    const int rc = rpt <= 1 ? 1 : rpt <= 2 ? 2 : rpt <= 4 ? 4 : rpt <= 8 ? 8 : 16;
+    switch (rc) {
+      case 1: k_deq_group_tile<OUT, 8, true, 1><<<grid, block, 0, s>>>(q, tmp, len, inner, G, rpt, ng, tiles, y); break;
+      case 2: k_deq_group_tile<OUT, 8, true, 2><<<grid, block, 0, s>>>(q, tmp, len, inner, G, rpt, ng, tiles, y); break;
+      case 4: k_deq_group_tile<OUT, 8, true, 4><<<grid, block, 0, s>>>(q, tmp, len, inner, G, rpt, ng, tiles, y); break;
+      case 8: k_deq_group_tile<OUT, 8, true, 8><<<grid, block, 0, s>>>(q, tmp, len, inner, G, rpt, ng, tiles, y); break;
+      default: k_deq_group_tile<OUT, 8, true, 16><<<grid, block, 0, s>>>(q, tmp, len, inner, G, rpt, ng, tiles, y); break;
+    }
+  } else if (G % 2 == 0) {
+    k_deq_group_tile<OUT, 2, true><<<grid, dim3(2 * kWave), 0, s>>>(
+        q, tmp, len, inner, G, static_cast<int>(G / 2), ng, tiles, y);
+  } else {
+    k_deq_group_tile<OUT, 1, true><<<grid, dim3(kWave), 0, s>>>(
+        q, tmp, len, inner, G, static_cast<int>(G), ng, tiles, y);
+  }
+}
+
 }  // namespace
 }  // namespace cbq
 
@@ -477,9 +544,20 @@ extern "C" int cbq_dequant_int8_group(const int8_t* q, const float* scale, int64
   return deq_rows(q, scale, num_groups, group_size, y, out_dtype, as_stream(stream), what);
 }
 
+extern "C" size_t cbq_dequant_int8_group_nd_ws_bytes(int64_t outer, int64_t len, int64_t inner,
+                                                     int64_t group_size) {
+  if (outer <= 0 || len <= 0 || inner <= 1 || group_size <= 0 || len % group_size != 0 ||
+      inner % 8 != 0)
+    return CBQ_WS_CTRL_BYTES;
+  const int64_t ng = len / group_size;
+  if (!deq_group_scratch_applies(outer, ng, inner)) return CBQ_WS_CTRL_BYTES;
+  return CBQ_WS_CTRL_BYTES + static_cast<size_t>(outer * ng * inner) * 4;
+}
+
 extern "C" int cbq_dequant_int8_group_nd(const int8_t* q, const float* scale, int64_t outer,
-                                         int64_t len, int64_t inner, int64_t group_size, void* y,
-                                         int out_dtype, cbq_stream_t stream) {
+                                         int64_t len, int64_t inner, int64_t group_size,
+                                         void* ws, size_t ws_bytes, void* y, int out_dtype,
+                                         cbq_stream_t stream) {
   clear_error();
   const char* what = "cbq_dequant_int8_group_nd";
   CBQ_REQUIRE(valid_out(out_dtype), "%s: out_dtype must be fp16 or bf16 (code %d)", what,
@@ -497,6 +575,15 @@ extern "C" int cbq_dequant_int8_group_nd(const int8_t* q, const float* scale, in
     return deq_rows(q, scale, outer * ng, group_size, y, out_dtype, as_stream(stream), what);
   const int64_t tiles = cdiv(inner, kDgCols);
   if (inner % 8 == 0 && aligned(q, 8) && aligned(y, 16) && outer * tiles * ng < (1LL << 31)) {
+    if (ws && aligned(ws, 16) && deq_group_scratch_applies(outer, ng, inner) &&
+        ws_bytes >= CBQ_WS_CTRL_BYTES + static_cast<size_t>(outer * ng * inner) * 4) {
+      float* tmp = reinterpret_cast<float*>(static_cast<char*>(ws) + CBQ_WS_CTRL_BYTES);
+      if (out_dtype == kF16)
+        launch_deq_group_scratch<kF16>(q, scale, outer, len, inner, group_size, tmp, y, as_stream(stream));
+      else
+        launch_deq_group_scratch<kBF16>(q, scale, outer, len, inner, group_size, tmp, y, as_stream(stream));
+      return launch_status(what);
+    }
     const bool two = group_size % 2 == 0;
     if (out_dtype == kF16) {
       if (two) launch_deq_group_tile<kF16, 2>(q, scale, outer, len, inner, group_size, y, as_stream(stream));

@@ -793,27 +793,57 @@ __global__ __launch_bounds__(kBlock) void k_group_strided(
 // reads one contiguous 1 KiB (2-byte types) run of x. HOLD (rpt <= kGtHold):
 // the group stays in registers between the max and the cast, so x is read
 // once; otherwise the cast reads the tile again (L2 / Infinity Cache).
-// Logical workgroup index, after xcd_remap: g fastest, then the inner tile,
-// then o, so the scales of neighbouring groups - adjacent in the movedim
-// layout - are written from one XCD's L2.
+// TS (a workspace is given, ng > 1): inner tiles fastest, so the workgroups
+// that run together read whole rows of x, and the scales go to group-major
+// scratch [outer, ng, inner] (contiguous per workgroup); k_transpose_f32
+// then writes the movedim order. Measured on MI355X, groups of 128 along
+// axis 0 of [16384, 14336] bf16: the scattered 4-byte writes of the movedim
+// order (each 128-byte line filled by 32 workgroups) took ~30 of ~150 us.
+// Otherwise: logical workgroup index, after xcd_remap: g fastest, then the
+// inner tile, then o, so the scales of neighbouring groups - adjacent in the
+// movedim layout - are written from one XCD's L2.
 constexpr int kGtCols = kWave * 8;
 constexpr int kGtHold = 16;
 
-template <int DT, int NW, bool HOLD>
+template <int DT, int NW, bool HOLD, bool TS, int RPTC = 0>
 __global__ __launch_bounds__(NW * kWave) void k_group_tile(
     const void* __restrict__ x, int64_t len, int64_t inner, int64_t G, int rpt, int64_t ng,
     int64_t tiles, int64_t nblocks, float eps, int8_t* __restrict__ q,
     float* __restrict__ scale) {
-  const int64_t b = xcd_remap(blockIdx.x, nblocks);
-  const int64_t g = b % ng, ti = (b / ng) % tiles, o = b / (ng * tiles);
+  int64_t g, ti, o;
+  if constexpr (TS) {
+    // inner tiles fastest: the workgroups running together read whole rows
+    const int64_t b = blockIdx.x;
+    ti = b % tiles; g = (b / tiles) % ng; o = b / (ng * tiles);
+  } else {
+    const int64_t b = xcd_remap(blockIdx.x, nblocks);
+    g = b % ng; ti = (b / ng) % tiles; o = b / (ng * tiles);
+  }
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
   const int64_t i = ti * kGtCols + lane * 8;
   const bool act = i < inner;
   const int64_t base = (o * len + g * G + w) * inner + i;
   const int64_t rs = static_cast<int64_t>(NW) * inner;
   float m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  Raw8<DT> r[HOLD ? kGtHold : 8];
-  if constexpr (HOLD) {
+  Raw8<DT> r[HOLD ? (RPTC > 0 ? RPTC : kGtHold) : 8];
+  if constexpr (HOLD && RPTC > 0) {
+    // compile-time count (rpt rounded up to a power of two): unguarded loads,
+    // past rpt (and for lanes past inner) clamped to an in-bounds row and
+    // left out of the maximum. Guarded loads made the compiler wait for every
+    // outstanding load where the branches rejoin (groups of 128 along axis 0
+    // of [16384, 14336] bf16: 136.6 us with them).
+    const int64_t lb = act ? base : base - i;
+#pragma unroll
+    for (int k = 0; k < RPTC; ++k) r[k] = ld8<DT>(x, lb + min(k, rpt - 1) * rs);
+#pragma unroll
+    for (int k = 0; k < RPTC; ++k) {
+      float f[8];
+      cvt8<DT>(r[k], f);
+      const bool use = act && k < rpt;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m[j] = use ? fmaxf(m[j], __builtin_fabsf(f[j])) : m[j];
+    }
+  } else if constexpr (HOLD) {
 #pragma unroll
     for (int k = 0; k < kGtHold; ++k)
       if (k < rpt && act) r[k] = ld8<DT>(x, base + k * rs);
@@ -858,10 +888,28 @@ __global__ __launch_bounds__(NW * kWave) void k_group_tile(
 #pragma unroll
   for (int j = 0; j < 8; ++j) inv[j] = inv_scale(m[j], eps, kQmaxInt8);
   if (w == 0) {
+    if constexpr (TS) {
+      // group-major scratch [outer, ng, inner]: 32 contiguous bytes per lane
+      float4* d = reinterpret_cast<float4*>(scale + (o * ng + g) * inner + i);
+      d[0] = make_float4(1.0f / inv[0], 1.0f / inv[1], 1.0f / inv[2], 1.0f / inv[3]);
+      d[1] = make_float4(1.0f / inv[4], 1.0f / inv[5], 1.0f / inv[6], 1.0f / inv[7]);
+    } else {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) scale[(o * inner + i + j) * ng + g] = 1.0f / inv[j];
+      for (int j = 0; j < 8; ++j) scale[(o * inner + i + j) * ng + g] = 1.0f / inv[j];
+    }
   }
-  if constexpr (HOLD) {
+  if constexpr (HOLD && RPTC > 0) {
+#pragma unroll
+    for (int k = 0; k < RPTC; ++k)
+      if (k < rpt) {
+        float f[8];
+        reload_barrier<DT>(r[k]);
+        cvt8<DT>(r[k], f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] *= inv[j];
+        stg8(q + base + k * rs, pack8_int8(f, 1.0f));
+      }
+  } else if constexpr (HOLD) {
 #pragma unroll
     for (int k = 0; k < kGtHold; ++k)
       if (k < rpt) {
@@ -1158,33 +1206,74 @@ int cols_quant_t(const void* x, int64_t rows, int64_t cols, int64_t inner, float
 // two <= 8 dividing G, rpt = G / NW positions per wave.
 int group_tile_waves(int64_t G) { return G % 8 == 0 ? 8 : G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1; }
 
-template <int DT, int NW>
-void launch_group_tile(const void* x, int64_t outer, int64_t len, int64_t inner, int64_t G,
-                       float eps, int8_t* q, float* scale, hipStream_t s) {
+// Whether the tiled group path writes its scales through group-major
+// scratch: ng > 1 (otherwise the movedim order is already contiguous) and
+// 64 x 64 transpose tiles that fit a 32-bit grid.
+bool group_scratch_applies(int64_t outer, int64_t ng, int64_t inner) {
+  return ng > 1 && outer * cdiv(ng, static_cast<int64_t>(kTrTile)) *
+                           cdiv(inner, static_cast<int64_t>(kTrTile)) < (1LL << 31);
+}
+
+template <int DT, int NW, bool TS>
+void launch_group_tile_t(const void* x, int64_t outer, int64_t len, int64_t inner, int64_t G,
+                         float eps, int8_t* q, float* scale, hipStream_t s) {
   const int64_t ng = len / G, tiles = cdiv(inner, kGtCols);
   const int64_t nblocks = outer * tiles * ng;
   const int rpt = static_cast<int>(G / NW);
   const dim3 grid(static_cast<unsigned>(nblocks)), block(NW * kWave);
-  if (rpt <= kGtHold)
-    k_group_tile<DT, NW, true><<<grid, block, 0, s>>>(x, len, inner, G, rpt, ng, tiles, nblocks,
-                                                      eps, q, scale);
+  if (TS && NW == 8 && rpt <= kGtHold) {
+    // the scratch path of the usual group sizes (G % 8 == 0, G <= 128):
+    // compile-time held count
+    const int rc = rpt <= 1 ? 1 : rpt <= 2 ? 2 : rpt <= 4 ? 4 : rpt <= 8 ? 8 : 16;
+    switch (rc) {
+      case 1: k_group_tile<DT, NW, true, TS, 1><<<grid, block, 0, s>>>(x, len, inner, G, rpt, ng, tiles, nblocks, eps, q, scale); break;
+      case 2: k_group_tile<DT, NW, true, TS, 2><<<grid, block, 0, s>>>(x, len, inner, G, rpt, ng, tiles, nblocks, eps, q, scale); break;
+      case 4: k_group_tile<DT, NW, true, TS, 4><<<grid, block, 0, s>>>(x, len, inner, G, rpt, ng, tiles, nblocks, eps, q, scale); break;
+      case 8: k_group_tile<DT, NW, true, TS, 8><<<grid, block, 0, s>>>(x, len, inner, G, rpt, ng, tiles, nblocks, eps, q, scale); break;
+      default: k_group_tile<DT, NW, true, TS, 16><<<grid, block, 0, s>>>(x, len, inner, G, rpt, ng, tiles, nblocks, eps, q, scale); break;
+    }
+  } else if (rpt <= kGtHold)
+    k_group_tile<DT, NW, true, TS><<<grid, block, 0, s>>>(x, len, inner, G, rpt, ng, tiles,
+                                                          nblocks, eps, q, scale);
   else
-    k_group_tile<DT, NW, false><<<grid, block, 0, s>>>(x, len, inner, G, rpt, ng, tiles, nblocks,
-                                                       eps, q, scale);
+    k_group_tile<DT, NW, false, TS><<<grid, block, 0, s>>>(x, len, inner, G, rpt, ng, tiles,
+                                                           nblocks, eps, q, scale);
+}
+
+// tmp: group-major scratch of outer * ng * inner fp32, or null for direct
+// scale writes.
+template <int DT, int NW>
+void launch_group_tile(const void* x, int64_t outer, int64_t len, int64_t inner, int64_t G,
+                       float eps, int8_t* q, float* scale, float* tmp, hipStream_t s) {
+  if (!tmp) {
+    launch_group_tile_t<DT, NW, false>(x, outer, len, inner, G, eps, q, scale, s);
+    return;
+  }
+  launch_group_tile_t<DT, NW, true>(x, outer, len, inner, G, eps, q, tmp, s);
+  const int64_t ng = len / G;
+  const int64_t gtiles = cdiv(ng, static_cast<int64_t>(kTrTile));
+  const int64_t itiles = cdiv(inner, static_cast<int64_t>(kTrTile));
+  k_transpose_f32<<<dim3(static_cast<unsigned>(outer * gtiles * itiles)), dim3(kBlock), 0, s>>>(
+      tmp, ng, inner, gtiles, itiles, 1, (ng % 4 == 0 && aligned(scale, 16)) ? 1 : 0, scale);
 }
 
 template <int DT>
 int group_strided_t(const void* x, int64_t outer, int64_t len, int64_t inner, int64_t G,
-                    float eps, int8_t* q, float* scale, hipStream_t s, const char* what) {
+                    float eps, void* ws, size_t ws_bytes, int8_t* q, float* scale,
+                    hipStream_t s, const char* what) {
   const int64_t ng = len / G;
   const bool tile = inner % 8 == 0 && aligned(x, 16) && aligned(q, 8) &&
                     outer * cdiv(inner, kGtCols) * ng < (1LL << 31);
   if (tile) {
+    float* tmp = nullptr;
+    if (ws && aligned(ws, 16) && group_scratch_applies(outer, ng, inner) &&
+        ws_bytes >= CBQ_WS_CTRL_BYTES + static_cast<size_t>(outer * ng * inner) * 4)
+      tmp = reinterpret_cast<float*>(static_cast<char*>(ws) + CBQ_WS_CTRL_BYTES);
     switch (group_tile_waves(G)) {
-      case 8: launch_group_tile<DT, 8>(x, outer, len, inner, G, eps, q, scale, s); break;
-      case 4: launch_group_tile<DT, 4>(x, outer, len, inner, G, eps, q, scale, s); break;
-      case 2: launch_group_tile<DT, 2>(x, outer, len, inner, G, eps, q, scale, s); break;
-      default: launch_group_tile<DT, 1>(x, outer, len, inner, G, eps, q, scale, s); break;
+      case 8: launch_group_tile<DT, 8>(x, outer, len, inner, G, eps, q, scale, tmp, s); break;
+      case 4: launch_group_tile<DT, 4>(x, outer, len, inner, G, eps, q, scale, tmp, s); break;
+      case 2: launch_group_tile<DT, 2>(x, outer, len, inner, G, eps, q, scale, tmp, s); break;
+      default: launch_group_tile<DT, 1>(x, outer, len, inner, G, eps, q, scale, tmp, s); break;
     }
     return launch_status(what);
   }
@@ -1398,9 +1487,20 @@ extern "C" int cbq_quant_int8_group(const void* x, int dtype, int64_t num_groups
   return rows_quant(x, dtype, num_groups, group_size, eps, q, scale, as_stream(stream), what);
 }
 
+extern "C" size_t cbq_quant_int8_group_nd_ws_bytes(int64_t outer, int64_t len, int64_t inner,
+                                                   int64_t group_size) {
+  if (outer <= 0 || len <= 0 || inner <= 1 || group_size <= 0 || len % group_size != 0 ||
+      inner % 8 != 0)
+    return CBQ_WS_CTRL_BYTES;
+  const int64_t ng = len / group_size;
+  if (!group_scratch_applies(outer, ng, inner)) return CBQ_WS_CTRL_BYTES;
+  return CBQ_WS_CTRL_BYTES + static_cast<size_t>(outer * ng * inner) * 4;
+}
+
 extern "C" int cbq_quant_int8_group_nd(const void* x, int dtype, int64_t outer, int64_t len,
-                                       int64_t inner, int64_t group_size, float eps, int8_t* q,
-                                       float* scale, cbq_stream_t stream) {
+                                       int64_t inner, int64_t group_size, float eps, void* ws,
+                                       size_t ws_bytes, int8_t* q, float* scale,
+                                       cbq_stream_t stream) {
   clear_error();
   const char* what = "cbq_quant_int8_group_nd";
   CBQ_REQUIRE(valid_dtype(dtype, true), "%s: unsupported input dtype code %d", what, dtype);
@@ -1417,8 +1517,8 @@ extern "C" int cbq_quant_int8_group_nd(const void* x, int dtype, int64_t outer, 
     return rows_quant(x, dtype, outer * (len / group_size), group_size, eps, q, scale,
                       as_stream(stream), what);
   switch (dtype) {
-    case kF16: return group_strided_t<kF16>(x, outer, len, inner, group_size, eps, q, scale, as_stream(stream), what);
-    case kBF16: return group_strided_t<kBF16>(x, outer, len, inner, group_size, eps, q, scale, as_stream(stream), what);
-    default: return group_strided_t<kF32>(x, outer, len, inner, group_size, eps, q, scale, as_stream(stream), what);
+    case kF16: return group_strided_t<kF16>(x, outer, len, inner, group_size, eps, ws, ws_bytes, q, scale, as_stream(stream), what);
+    case kBF16: return group_strided_t<kBF16>(x, outer, len, inner, group_size, eps, ws, ws_bytes, q, scale, as_stream(stream), what);
+    default: return group_strided_t<kF32>(x, outer, len, inner, group_size, eps, ws, ws_bytes, q, scale, as_stream(stream), what);
   }
 }

@@ -153,11 +153,18 @@ int cbq_quant_int8_channel_nd(const void* x, int dtype, int64_t outer,
  * movedim(ch_axis, -1).contiguous() / view(-1, G) / kernel / movedim-back
  * sequence (quantizers.py:122-132, two full copies) with no copies. scale:
  * outer * inner * (len / group_size) fp32 in the reference's order,
- * index (o * inner + i) * (len / group_size) + g. */
+ * index (o * inner + i) * (len / group_size) + g. The workspace (optional:
+ * null or smaller gives the same results, slower) holds the scales in
+ * group-major order before one transposing pass writes that order:
+ * cbq_quant_int8_group_nd_ws_bytes() = the control block + 4 bytes per scale
+ * when inner % 8 == 0 and more than one group lies along len, else the
+ * control block. */
+size_t cbq_quant_int8_group_nd_ws_bytes(int64_t outer, int64_t len,
+                                        int64_t inner, int64_t group_size);
 int cbq_quant_int8_group_nd(const void* x, int dtype, int64_t outer,
                             int64_t len, int64_t inner, int64_t group_size,
-                            float eps, int8_t* q, float* scale,
-                            cbq_stream_t stream);
+                            float eps, void* ws, size_t ws_bytes, int8_t* q,
+                            float* scale, cbq_stream_t stream);
 
 /* Replaces dequantize_per_tensor_int8_cuda (dequantize_int8.cu:210-225; kernel
  * :29-64), bound as dequantize_int8.dequantize_per_tensor_int8
@@ -188,11 +195,16 @@ int cbq_dequant_int8_channel_nd(const int8_t* q, const float* scale,
 
 /* Group dequant along any axis (outer x len x inner, scale order as in
  * cbq_quant_int8_group_nd). Replaces the movedim / view / kernel / movedim
- * sequence of dequantizers.py:58-72 (two full copies). */
+ * sequence of dequantizers.py:58-72 (two full copies). The workspace
+ * (optional: null or smaller gives the same results, slower) receives the
+ * scales transposed to group-major order, read contiguously by the kernel;
+ * cbq_dequant_int8_group_nd_ws_bytes() sizes it as for the group quant. */
+size_t cbq_dequant_int8_group_nd_ws_bytes(int64_t outer, int64_t len,
+                                          int64_t inner, int64_t group_size);
 int cbq_dequant_int8_group_nd(const int8_t* q, const float* scale,
                               int64_t outer, int64_t len, int64_t inner,
-                              int64_t group_size, void* y, int out_dtype,
-                              cbq_stream_t stream);
+                              int64_t group_size, void* ws, size_t ws_bytes,
+                              void* y, int out_dtype, cbq_stream_t stream);
 
 /* ---- W8A16 linear ------------------------------------------------------- */
 

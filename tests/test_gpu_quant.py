@@ -550,6 +550,63 @@ def test_group_any_axis(code, shape, axis, G):
     assert_bits_equal_16(bits(y), np.moveaxis(yo, -1, axis), out, "group nd y")
 
 
+@pytest.mark.parametrize("shape,axis,G", [
+    ((256, 64), 0, 32), ((6, 96, 520), 1, 32), ((512, 1024), 0, 128), ((2, 12, 1032), 1, 4),
+    ((3, 70, 136), 1, 7), ((4, 200, 72), 1, 2)])
+def test_group_nd_scale_scratch_and_direct_agree(shape, axis, G):
+    """The tiled group quant kernels write the scales either through group-major
+    workspace scratch and a transposing pass (the API's path) or, without a
+    workspace, directly in the movedim order: same codes and scale bits. The
+    first path is pinned to the oracle by test_group_any_axis."""
+    from cublade_amd import _abi
+    from cublade_amd.bindings.hip.quantize_int8 import quantize_per_group_int8_nd
+    x = rand_bits(shape, oracle.BF16, seed=sum(shape) + G)
+    xt = from_bits(x.reshape(-1), oracle.BF16, DEV).view(*shape)
+    print(f"[group scratch] shape={shape} axis={axis} G={G}", flush=True)
+    q1, s1 = quantize_per_group_int8_nd(xt, axis, G)
+    outer = int(np.prod(shape[:axis], dtype=np.int64))
+    inner = int(np.prod(shape[axis + 1:], dtype=np.int64))
+    L = _abi.lib()
+    assert L.cbq_quant_int8_group_nd_ws_bytes(outer, shape[axis], inner, G) > _abi.WS_CTRL_BYTES
+    q2 = torch.empty_like(q1)
+    s2 = torch.empty_like(s1)
+    rc = L.cbq_quant_int8_group_nd(_abi.ptr(xt), _abi.DTYPE_CODE[torch.bfloat16], outer,
+                                   shape[axis], inner, G, 1e-12, None, 0, _abi.ptr(q2),
+                                   _abi.ptr(s2), _abi.stream_handle(xt.device))
+    _abi.check(rc, "group nd without workspace")
+    # with the workspace again, the scales written one float past a 16-byte
+    # boundary (the transposing pass's 4-byte store path)
+    q3 = torch.empty_like(q1)
+    s3 = torch.empty(s1.numel() + 1, dtype=torch.float32, device=xt.device)
+    nb = L.cbq_quant_int8_group_nd_ws_bytes(outer, shape[axis], inner, G)
+    ws = torch.zeros(nb, dtype=torch.uint8, device=xt.device)
+    rc = L.cbq_quant_int8_group_nd(_abi.ptr(xt), _abi.DTYPE_CODE[torch.bfloat16], outer,
+                                   shape[axis], inner, G, 1e-12, _abi.ptr(ws), nb, _abi.ptr(q3),
+                                   _abi.ptr(s3) + 4, _abi.stream_handle(xt.device))
+    _abi.check(rc, "group nd, unaligned scales")
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2) and torch.equal(q1, q3)
+    assert torch.equal(s1.view(torch.int32), s2.view(torch.int32))
+    assert torch.equal(s1.view(torch.int32), s3[1:].view(torch.int32))
+    # the group dequant: scales transposed into workspace scratch (the API's
+    # path), read in place without a workspace, and from unaligned scales
+    from cublade_amd.bindings.hip.dequantize_int8 import dequantize_per_group_int8_nd
+    y1 = dequantize_per_group_int8_nd(q1, s1, axis, G, torch.bfloat16)
+    assert L.cbq_dequant_int8_group_nd_ws_bytes(outer, shape[axis], inner, G) == nb
+    y2, y3 = torch.empty_like(y1), torch.empty_like(y1)
+    bf = _abi.DTYPE_CODE[torch.bfloat16]
+    rc = L.cbq_dequant_int8_group_nd(_abi.ptr(q1), _abi.ptr(s1), outer, shape[axis], inner, G,
+                                     None, 0, _abi.ptr(y2), bf, _abi.stream_handle(xt.device))
+    _abi.check(rc, "group nd dequant without workspace")
+    rc = L.cbq_dequant_int8_group_nd(_abi.ptr(q1), _abi.ptr(s3) + 4, outer, shape[axis], inner,
+                                     G, _abi.ptr(ws), nb, _abi.ptr(y3), bf,
+                                     _abi.stream_handle(xt.device))
+    _abi.check(rc, "group nd dequant, unaligned scales")
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    assert torch.equal(y1.view(torch.int16), y3.view(torch.int16))
+
+
 @pytest.mark.parametrize("mode,axis", [("group", 0), ("channel", 1)])
 def test_any_axis_unaligned_view(mode, axis):
     """A view whose data pointer is not 16-byte aligned takes the scalar

@@ -34,7 +34,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     L = _lib()
     names = declared_symbols()
-    assert len(names) == 22
+    assert len(names) == 24
     for n in names:
         assert hasattr(L, n), n
     from cublade_amd import _abi
@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_slot():
     L = _lib()
-    assert L.cbq_abi_version() == 105
+    assert L.cbq_abi_version() == 106
     assert L.cbq_last_error() in (b"",) or isinstance(L.cbq_last_error(), bytes)
 
 
@@ -140,19 +140,31 @@ def test_nd_entry_points_validate_and_size():
     assert L.cbq_quant_int8_channel_nd_ws_bytes(2, 3, 512) == C + 4 * (2 * 3 + 3)
     F16 = _abi.DTYPE_CODE[torch.float16]
     dummy = ctypes.c_void_p(16)
-    _einval(L.cbq_quant_int8_group_nd(dummy, F16, 2, 100, 3, 32, 1e-12, dummy, dummy, None),
-            "must divide")
-    _einval(L.cbq_quant_int8_group_nd(dummy, F16, 2, 96, 3, 0, 1e-12, dummy, dummy, None),
-            "group_size")
+    _einval(L.cbq_quant_int8_group_nd(dummy, F16, 2, 100, 3, 32, 1e-12, None, 0, dummy, dummy,
+                                      None), "must divide")
+    _einval(L.cbq_quant_int8_group_nd(dummy, F16, 2, 96, 3, 0, 1e-12, None, 0, dummy, dummy,
+                                      None), "group_size")
+    # group-major scale scratch: 4 bytes per scale when the tiled path can use
+    # it (inner % 8 == 0, more than one group along len), else the control block
+    assert L.cbq_quant_int8_group_nd_ws_bytes(1, 16384, 14336, 128) == C + 4 * 128 * 14336
+    assert L.cbq_quant_int8_group_nd_ws_bytes(3, 96, 16, 32) == C + 4 * 3 * 3 * 16
+    assert L.cbq_quant_int8_group_nd_ws_bytes(3, 96, 12, 32) == C     # inner % 8 != 0
+    assert L.cbq_quant_int8_group_nd_ws_bytes(3, 96, 16, 96) == C     # one group along len
+    assert L.cbq_quant_int8_group_nd_ws_bytes(3, 96, 1, 32) == C      # contiguous groups
+    assert L.cbq_quant_int8_group_nd_ws_bytes(3, 100, 16, 32) == C    # not a divisor
     _einval(L.cbq_quant_int8_channel_nd(dummy, 9, 2, 3, 4, 1e-12, None, 0, dummy, dummy, None),
             "dtype")
     _einval(L.cbq_quant_int8_channel_nd(dummy, F16, 2, 3, 4, 1e-12, None, 0, dummy, dummy, None),
             "workspace")
-    _einval(L.cbq_dequant_int8_group_nd(dummy, dummy, 2, 100, 3, 32, dummy, F16, None),
+    _einval(L.cbq_dequant_int8_group_nd(dummy, dummy, 2, 100, 3, 32, None, 0, dummy, F16, None),
             "must divide")
+    for n in ("cbq_quant_int8_group_nd_ws_bytes", "cbq_dequant_int8_group_nd_ws_bytes"):
+        f = getattr(L, n)
+        assert f(2, 96, 16, 32) == C + 4 * 2 * 3 * 16 and f(2, 96, 16, 96) == C
     _einval(L.cbq_dequant_int8_channel_nd(dummy, dummy, 2, 3, 4, dummy, 0, None), "out_dtype")
     # empty shapes are no-ops
-    assert L.cbq_quant_int8_group_nd(None, F16, 0, 64, 3, 32, 1e-12, None, None, None) == 0
+    assert L.cbq_quant_int8_group_nd(None, F16, 0, 64, 3, 32, 1e-12, None, 0, None, None,
+                                     None) == 0
     assert L.cbq_dequant_int8_channel_nd(None, None, 5, 0, 3, None, F16, None) == 0
 
 
