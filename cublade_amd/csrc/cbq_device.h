@@ -318,6 +318,26 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t nb) {
   return b < (per << 3) ? (b & 7) * per + (b >> 3) : b;
 }
 
+// Per-channel values of 8 adjacent columns c .. c + 7 of a [rows, channels *
+// inner] view (channel = column / inner) with at most one 64-bit division:
+// inner == 1, every column its own channel; inner >= 8, at most one channel
+// boundary among the 8. (Eight divisions per thread cost more than the
+// loads they serve once a thread's row block is short.)
+__device__ __forceinline__ void channel_vals8(const float* __restrict__ v, int64_t c,
+                                              int64_t inner, float (&out)[8]) {
+  if (inner == 1) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) out[k] = v[c + k];
+  } else if (inner >= 8) {
+    const int64_t ch0 = c / inner, rem = c - ch0 * inner;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) out[k] = v[ch0 + (rem + k >= inner ? 1 : 0)];
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) out[k] = v[(c + k) / inner];
+  }
+}
+
 // fp32 transpose of outer stacked matrices, src [R, C] -> dst [C, R] each
 // (the group scale orders: group-major [ng, inner] and the movedim order
 // [inner, ng]): 64 x 64 tiles through LDS (row stride 65 floats: no bank

@@ -707,8 +707,7 @@ __global__ __launch_bounds__(kBlock) void k_cast_cols(
     const int64_t c = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * 8;
     if (c >= cols) return;
     float inv[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) inv[k] = inv_c[(c + k) / inner];
+    channel_vals8(inv_c, c, inner, inv);
     int64_t r = r0;
     for (; r + 4 <= r1; r += 4) {
       Raw8<DT> raw[4];
@@ -1167,8 +1166,10 @@ size_t col_ws_bytes(int64_t rows, int64_t cols) {
 // Row blocking of the column cast (and of nothing else: the cast only needs
 // the [cols] multipliers, so its geometry is independent of the partial
 // maxima's). Short blocks keep many workgroups in flight; measured on
-// MI355X, walks of ~100 rows per thread lose ~25% of the bandwidth.
-constexpr int64_t kCastRB = 16;
+// MI355X at [28672, 8192] bf16: blocks of 4 rows (one batch of 4 loads per
+// thread) 110.8 us, 2 rows 112.8, 8 rows 117.0, 16 rows 119.2, 1 row 127.9;
+// walks of ~100 rows per thread lose ~25% of the bandwidth.
+constexpr int64_t kCastRB = 4;
 dim3 cast_grid(int64_t rows, int64_t col_blocks, int64_t& RB) {
   RB = kCastRB;
   if (cdiv(rows, RB) > 65535) RB = cdiv(rows, 65535);
