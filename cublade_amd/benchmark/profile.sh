@@ -14,9 +14,11 @@
 #    of configs 1-5 (every suite kernel's HBM bytes per dispatch)
 # 4. rocprof's derived MfmaUtil counter (MFMA busy cycles over active cycles
 #    x SIMDs) for the MFMA kernels: W8A16 (config 5) and the dense GEMM (f4)
+# 5. bare stream ceilings (cublade_amd/benchmark/stream_ceiling.hip)
 # Summaries: OUTDIR/bench_c2_kernels.txt, OUTDIR/quant_int8_c2_traffic.json,
 # OUTDIR/dequant_int8_c2_traffic.json, OUTDIR/suite_kernels.txt,
-# OUTDIR/suite_traffic.txt, OUTDIR/suite_configs.json, OUTDIR/mfma_util.txt. Raw
+# OUTDIR/suite_traffic.txt, OUTDIR/suite_configs.json, OUTDIR/mfma_util.txt,
+# OUTDIR/stream_ceiling.txt. Raw
 # databases go to RAWDIR (default OUTDIR/raw; they total about 80 MiB), the
 # programs' output to OUTDIR/logs.
 # Run from the repository root on a GPU machine. Every GPU step has its own
@@ -63,6 +65,11 @@ step "counter MfmaUtil: suite configs c5,f4"
 timeout -s KILL 300 rocprofv3 --pmc MfmaUtil --kernel-trace -d "$RAW/mfma" -o suite -- \
   $PY -m cublade_amd.benchmark.suite --configs c5,f4 --reps 3 --warmup 1 > "$LOGS/mfma.log" 2>&1 || exit $?
 
+step "bare stream ceilings (stream_ceiling.hip)"
+/opt/rocm/bin/hipcc --offload-arch=gfx950 -O3 -std=c++17 -Xclang -target-feature -Xclang -packed-fp32-ops \
+  cublade_amd/benchmark/stream_ceiling.hip -o "$RAW/stream_ceiling" > "$LOGS/stream_ceiling_build.log" 2>&1 || exit $?
+timeout -k 10 120 "$RAW/stream_ceiling" > "$LOGS/stream_ceiling.log" 2>&1 || exit $?
+
 step "summaries"
 CAL="$RAW/cal_fetch/calib_results.db $RAW/cal_write/calib_results.db 262144"
 {
@@ -101,4 +108,10 @@ traffic_json "k_deq_tensor<false, 1, 2>" 201326596 "$OUT/dequant_int8_c2_traffic
   echo "# command: rocprofv3 --pmc MfmaUtil --kernel-trace -d RAW/mfma -o suite -- python -u -m cublade_amd.benchmark.suite --configs c5,f4 --reps 3 --warmup 1"
   $R counters "$RAW/mfma/suite_results.db" | grep -E "k_gemm_dma|k_stream|k_skinny|k_gemm<|k_mm_dma|Cijk"
 } > "$OUT/mfma_util.txt" || exit $?
+{
+  echo "# bare HBM streams with the quant / dequant access mixes (no arithmetic): the ceilings the"
+  echo "# kernels' roofline fractions are read against"
+  echo "# command: hipcc --offload-arch=gfx950 -O3 -std=c++17 -Xclang -target-feature -Xclang -packed-fp32-ops cublade_amd/benchmark/stream_ceiling.hip -o RAW/stream_ceiling && RAW/stream_ceiling"
+  cat "$LOGS/stream_ceiling.log"
+} > "$OUT/stream_ceiling.txt" || exit $?
 step "done"
