@@ -532,7 +532,10 @@ def test_channel_any_axis(code, shape, axis):
     # tiled: 8 / 4 / 2 / 1 waves per group, groups held in registers (<= 16
     # positions per wave) or read twice, partial inner tiles
     ((256, 64), 0, 32), ((6, 96, 520), 1, 96), ((512, 1024), 0, 128), ((2, 384, 16), 1, 384),
-    ((136, 8), 0, 136), ((3, 10, 24), 1, 5), ((4, 36, 8), 1, 6), ((2, 12, 1032), 1, 12)])
+    ((136, 8), 0, 136), ((3, 10, 24), 1, 5), ((4, 36, 8), 1, 6), ((2, 12, 1032), 1, 12),
+    # group-major scale scratch with 8 waves per group and a walk that is not a
+    # power of two (3 and 12 positions, clamped to 4 and 16), partial inner tile
+    ((3, 48, 8), 1, 24), ((2, 192, 520), 1, 96), ((5, 64, 16), 1, 8)])
 def test_group_any_axis(code, shape, axis, G):
     from cublade_amd.quantization import dequantize_tensor, quantize_tensor
     x = rand_bits(shape, code, seed=sum(shape) * 3 + axis + G)
