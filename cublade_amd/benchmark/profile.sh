@@ -110,7 +110,7 @@ traffic_json "k_deq_tensor<false, 1, 2>" 201326596 "$OUT/dequant_int8_c2_traffic
 } > "$OUT/mfma_util.txt" || exit $?
 {
   echo "# bare HBM streams with the quant / dequant access mixes (no arithmetic): the ceilings the"
-  echo "# kernels' roofline fractions are read against"
+  echo "# kernels' roofline fractions are read against; first the timing floor of one launch"
   echo "# command: hipcc --offload-arch=gfx950 -O3 -std=c++17 -Xclang -target-feature -Xclang -packed-fp32-ops cublade_amd/benchmark/stream_ceiling.hip -o RAW/stream_ceiling && RAW/stream_ceiling"
   cat "$LOGS/stream_ceiling.log"
 } > "$OUT/stream_ceiling.txt" || exit $?

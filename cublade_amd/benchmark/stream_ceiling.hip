@@ -6,8 +6,10 @@
 //   dequant mix  8-byte loads, 16-byte stores
 //   read only    16-byte loads (the amax / column-max passes)
 //
-// Each is timed as a one-shot grid (one 16-byte chunk per thread and step,
-// U steps per thread, all loads issued first) and as a persistent grid-stride
+// First the timing floor: an event pair with nothing between and an empty
+// kernel, after the same sweep. Each stream is timed as a one-shot grid (one
+// 16-byte chunk per thread and step, U steps per thread, all loads issued
+// first) and as a persistent grid-stride
 // loop, with non-temporal or ordinary stores, after a read-only ("clean") and
 // a write ("dirty") 512 MiB sweep that evicts the 256 MB Infinity Cache. Sizes:
 // BASELINE configs 2 (64 Mi fp16 elements) and 3 (28672 x 8192 bf16).
@@ -103,6 +105,12 @@ __global__ __launch_bounds__(256) void k_r1(const u32x4* __restrict__ x, long n1
   if (h == 0x9e3779b9u) sink[0] = h;
 }
 
+// near-empty kernel: the event / dispatch floor of a single timed launch
+template <int B>
+__global__ __launch_bounds__(B) void k_empty(unsigned* sink, int never) {
+  if (static_cast<int>(blockIdx.x) == never) sink[0] = threadIdx.x;
+}
+
 __global__ void k_sweep_read(const u32x4* p, long n16, unsigned* sink) {
   unsigned h = 0;
   for (long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x; i < n16;
@@ -158,6 +166,12 @@ int main() {
   };
   struct Size { const char* name; size_t elems; };
   const Size sizes[] = {{"C2 64Mi x 2B", size_t(8192) * 8192}, {"C3 28672x8192 x 2B", size_t(28672) * 8192}};
+  std::printf("# timing floor of one launch between two events after a sweep (median of 20)\n");
+  std::printf("%-44s %9.2f us\n", "event pair, nothing between", timeit(false, [&] {}));
+  std::printf("%-44s %9.2f us\n", "empty kernel, 256 x 1024 threads",
+              timeit(false, [&] { k_empty<1024><<<256, 1024>>>(sink, -1); }));
+  std::printf("%-44s %9.2f us\n", "empty kernel, 8192 x 256 threads",
+              timeit(false, [&] { k_empty<256><<<8192, 256>>>(sink, -1); }));
   std::printf("# bare streams, median of 20 launches after a 512 MiB sweep; frac = bytes / time / 8 TB/s\n");
   std::printf("%-20s %-34s %-6s %9s %9s %6s\n", "size", "kernel", "sweep", "us", "GB/s", "frac");
   for (const Size& sz : sizes) {
