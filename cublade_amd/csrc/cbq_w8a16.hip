@@ -119,6 +119,7 @@ struct GemmArgs {
   int tiles_m, tiles_n;
   int splits, split_steps;  // split-K: number of k-ranges, 64-k steps per range
   int full_tiles;           // split-K: tiles [0, full_tiles) run whole, the rest split
+  const uint16_t* x2;       // k_gemm_dma<.., PLANES>: the second x plane (split 1 reads it)
 };
 
 // Workgroup b of n goes to XCD b % 8; renumbered so that each XCD takes a
@@ -476,7 +477,7 @@ __device__ __forceinline__ void outlier_mfma(const uint8_t* so, int wm, int wn, 
 // the others split the remaining tiles over `splits` k-ranges, workgroup
 // full_tiles + b covering tail tile b % rest of k-range b / rest (after the
 // XCD renumbering, so the workgroups of one XCD share a k-range of x).
-template <int ACT, bool SPLIT, int TM>
+template <int ACT, bool SPLIT, int TM, bool PLANES = false>
 __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
   constexpr int BM = 64 * TM, BN = 256, BK = 64, NS = 3;
   constexpr int XB = BM * BK * 2;          // x stage bytes (32 / 24 / 16 KiB)
@@ -514,8 +515,9 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
     decode_tile(blockIdx.x, a, tm, tn);
   }
   const int m0 = tm * BM, n0 = tn * BN;
-  const int kb = partial ? split * a.split_steps : 0;          // first 64-k step
-  const int nk = partial ? min(a.split_steps, a.K / BK - kb) : a.K / BK;
+  const int kb = (partial && !PLANES) ? split * a.split_steps : 0;   // first 64-k step
+  const int nk = (partial && !PLANES) ? min(a.split_steps, a.K / BK - kb) : a.K / BK;
+  const uint16_t* const xsrc = (PLANES && split == 1) ? a.x2 : a.x;
   const uint32_t sbase = __builtin_amdgcn_readfirstlane(lds_addr(smem));
 
   // Per-lane DMA source offsets (bytes from the k0 column of the tile). x
@@ -541,7 +543,7 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
   // DMA instruction u (0..XL+WL-1) of tile t into `stage`.
   auto issue_one = [&](int t, int stage, int u) {
     if (u < XL)
-      lds_dma16(xo[u], uniform_ptr(a.x + (kb + t) * BK), sbase + stage * SB + wave * 1024 + u * 8192);
+      lds_dma16(xo[u], uniform_ptr(xsrc + (kb + t) * BK), sbase + stage * SB + wave * 1024 + u * 8192);
     else
       lds_dma16(wo[u - XL], uniform_ptr(a.wq + (kb + t) * BK),
                 sbase + stage * SB + XB + wave * 1024 + (u - XL) * 8192);
@@ -923,6 +925,84 @@ __global__ __launch_bounds__(kBlock) void k_splitk_reduce(GemmArgs a) {
     const int m = tm * 64 * TM + (wave & 1) * 32 * TM + j * 32 + (lane & 31);
     const int nb = tn * 256 + (wave >> 1) * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
     splitk_finish<ACT>(a, sum[u], src + a.splits * per_split + u * kBlock, m, nb);
+  }
+}
+
+// fp32 activations on the matrix cores. The weights are int8, exact in
+// bf16, so x . w = hi . w + lo . w + r . w with hi = x truncated to bf16
+// (never rounds up to inf), lo = bf16(x - hi) (x - hi is exact: the low 16
+// bits of x's significand) and |r| <= 2^-16 |x|: each bf16 x int8 product is
+// exact in the fp32 accumulators, and x keeps 16 significant bits (the
+// reference's fp32 Triton dot runs at TF32 precision, 11 bits). Non-finite x:
+// hi carries it (NaN canonical), lo = 0. k_f32_planes writes the two planes;
+// k_gemm_dma<BF16, true, TM, true> then runs every tile twice over the whole
+// of K (split s reads plane s), and k_planes_reduce adds the two
+// partial planes in order and applies the fp32 scale and bias.
+__global__ __launch_bounds__(kBlock) void k_f32_planes(const float* __restrict__ x, int64_t n4,
+                                                     uint16_t* __restrict__ xh,
+                                                     uint16_t* __restrict__ xl) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= n4) return;
+  const f4 v = reinterpret_cast<const f4*>(x)[i];
+  uint32_t hb[4];
+  float lo[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t b = __float_as_uint(v[r]);
+    const bool fin = (b & 0x7f800000u) != 0x7f800000u;
+    const bool nan = !fin && (b & 0x007fffffu) != 0;
+    hb[r] = nan ? 0x7fc0u : (b >> 16);
+    lo[r] = fin ? v[r] - __uint_as_float(hb[r] << 16) : 0.0f;
+  }
+  reinterpret_cast<uint2*>(xh)[i] = make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
+  reinterpret_cast<uint2*>(xl)[i] =
+      make_uint2(pack2_out<kBF16>(lo[0], lo[1]), pack2_out<kBF16>(lo[2], lo[3]));
+}
+
+// The two partial planes of every tile (layout as in k_splitk_reduce, all
+// tiles split, plane 0 then plane 1) -> y = fp32((p0 + p1) * s[n] + bias[n]).
+// Each thread takes two partial f4, kBlock apart.
+template <int TM>
+__global__ __launch_bounds__(kBlock) void k_planes_reduce(GemmArgs a, const float* __restrict__ sc,
+                                                          const float* __restrict__ bias,
+                                                          float* __restrict__ y) {
+  constexpr int kWaveF4 = kDmaTN * TM * 4 * 64;
+  constexpr int kTileF4 = 8 * kWaveF4;
+  static_assert(kTileF4 % (kBlock * 2) == 0, "a thread's f4 share a tile");
+  const int tiles = a.tiles_m * a.tiles_n;
+  const int64_t per_plane = static_cast<int64_t>(tiles) * kTileF4;
+  const int64_t idx0 = static_cast<int64_t>(blockIdx.x) * (kBlock * 2) + threadIdx.x;
+  if (idx0 >= per_plane) return;
+  const f4* src = reinterpret_cast<const f4*>(a.part) + idx0;
+  const f4 p00 = src[0], p01 = src[kBlock], p10 = src[per_plane], p11 = src[per_plane + kBlock];
+  const f4 sum[2] = {p00 + p10, p01 + p11};
+  int tm, tn;
+  group_tile(static_cast<int>(idx0 / kTileF4), a, tm, tn);
+  const bool vec = (a.N % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int w = static_cast<int>((idx0 + u * kBlock) % kWaveF4);
+    const int lane = w & 63, q = (w >> 6) & 3, j = (w >> 8) % TM, i = (w >> 8) / TM;
+    const int wave = static_cast<int>(((idx0 + u * kBlock) / kWaveF4) & 7);
+    const int m = tm * 64 * TM + (wave & 1) * 32 * TM + j * 32 + (lane & 31);
+    const int nb = tn * 256 + (wave >> 1) * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
+    if (m >= a.M || nb >= a.N) continue;
+    f4 v;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = nb + r < a.N ? sum[u][r] * sc[nb + r] : 0.0f;
+    if (bias) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (nb + r < a.N) v[r] += bias[nb + r];
+    }
+    float* dst = y + static_cast<int64_t>(m) * a.N + nb;
+    if (vec && nb + 3 < a.N) {
+      *reinterpret_cast<f4*>(dst) = v;
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (nb + r < a.N) dst[r] = v[r];
+    }
   }
 }
 
@@ -1712,6 +1792,88 @@ int64_t general_split_bytes(int64_t M, int64_t N, int64_t K) {
   return sp > 1 ? static_cast<int64_t>(sp) * M * N * 4 : 0;
 }
 
+// Two-plane fp32 path (see k_f32_planes): M > 64, no outlier columns, the
+// DMA kernel's shape limits. The x-tile height with the fewest modelled step
+// units over both planes' workgroups: rounds of workgroups on the CUs times
+// the full-occupancy cost of a 64-k step (dma_plan's model: 1.12 / 1.46 /
+// 1.85 us for 128 / 192 / 256-row tiles).
+bool planes_ok(int64_t M, int64_t N, int64_t K, int64_t n_out) {
+  return M > 64 && n_out == 0 && dma_ok(M, N, K) && 2 * cdiv(M, 128) * cdiv(N, 256) < (1LL << 30);
+}
+
+int planes_tm(int64_t M, int64_t N) {
+  const int64_t cus = device_cus();
+  const double cost[5] = {0.0, 0.0, 1.12, 1.46, 1.85};
+  int best_tm = 4;
+  double best = 1e300;
+  for (int tm = 2; tm <= 4; ++tm) {
+    const int64_t wgs = 2 * cdiv(M, static_cast<int64_t>(64 * tm)) * cdiv(N, static_cast<int64_t>(256));
+    const double t = static_cast<double>(cdiv(wgs, cus)) * cost[tm];
+    if (t < best - 1e-9) {
+      best = t;
+      best_tm = tm;
+    }
+  }
+  return best_tm;
+}
+
+// Bytes after the control block: the two bf16 planes (each 256-byte
+// aligned), then the fp32 partial tiles of both planes.
+int64_t planes_x_bytes(int64_t M, int64_t K) { return cdiv(M * K * 2, static_cast<int64_t>(256)) * 256; }
+
+int64_t planes_bytes(int64_t M, int64_t N, int64_t K) {
+  const int tm = planes_tm(M, N);
+  const int64_t tiles = cdiv(M, static_cast<int64_t>(64 * tm)) * cdiv(N, static_cast<int64_t>(256));
+  return 2 * planes_x_bytes(M, K) + tiles * 2 * (64 * tm) * 256 * 4;
+}
+
+template <int TM>
+void launch_planes(GemmArgs a, const float* sc, const float* bias, float* y, hipStream_t s) {
+  a.tiles_m = static_cast<int>(cdiv(a.M, 64 * TM));
+  a.tiles_n = static_cast<int>(cdiv(a.N, 256));
+  a.full_tiles = 0;
+  a.splits = 2;
+  a.split_steps = a.K / 64;
+  const int tiles = a.tiles_m * a.tiles_n;
+  k_gemm_dma<kBF16, true, TM, true><<<dim3(static_cast<unsigned>(2 * tiles)), dim3(kDmaThreads), 0,
+                                      s>>>(a);
+  const int64_t n4 = static_cast<int64_t>(tiles) * 8 * kDmaTN * TM * 4 * 64;
+  k_planes_reduce<TM><<<dim3(static_cast<unsigned>(cdiv(n4, kBlock * 2))), dim3(kBlock), 0, s>>>(
+      a, sc, bias, y);
+}
+
+// The two-plane path when it applies (returns its status), else -1.
+int w8a16_f32_planes(const void* x, const int8_t* wq, const void* scales, const void* bias,
+                     int64_t n_out, int64_t M, int64_t N, int64_t K, void* ws, size_t ws_bytes,
+                     void* y, hipStream_t s) {
+  if (!planes_ok(M, N, K, n_out) || !ws || !aligned(x, 16) || !aligned(wq, 16) ||
+      ws_bytes < static_cast<size_t>(CBQ_WS_CTRL_BYTES + planes_bytes(M, N, K)))
+    return -1;
+  uint8_t* base = static_cast<uint8_t*>(ws) + CBQ_WS_CTRL_BYTES;
+  uint16_t* xh = reinterpret_cast<uint16_t*>(base);
+  uint16_t* xl = reinterpret_cast<uint16_t*>(base + planes_x_bytes(M, K));
+  const int64_t n4 = M * K / 4;   // K % 64 == 0
+  k_f32_planes<<<dim3(static_cast<unsigned>(cdiv(n4, static_cast<int64_t>(kBlock)))), dim3(kBlock),
+                 0, s>>>(static_cast<const float*>(x), n4, xh, xl);
+  GemmArgs a{};
+  a.x = xh;
+  a.x2 = xl;
+  a.wq = wq;
+  a.part = reinterpret_cast<float*>(base + 2 * planes_x_bytes(M, K));
+  a.M = static_cast<int>(M);
+  a.N = static_cast<int>(N);
+  a.K = static_cast<int>(K);
+  const float* sc = static_cast<const float*>(scales);
+  const float* bs = static_cast<const float*>(bias);
+  float* yo = static_cast<float*>(y);
+  switch (planes_tm(M, N)) {
+    case 2: launch_planes<2>(a, sc, bs, yo, s); break;
+    case 3: launch_planes<3>(a, sc, bs, yo, s); break;
+    default: launch_planes<4>(a, sc, bs, yo, s); break;
+  }
+  return launch_status("cbq_w8a16_linear");
+}
+
 template <int ACT>
 int w8a16_general(const void* x, const int8_t* wq, const void* scales, const void* bias,
                   const int64_t* oc, int64_t n_out, const void* w_out, int64_t M, int64_t N,
@@ -1799,7 +1961,10 @@ extern "C" size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_
   // kernel; with this size it then runs without a split (same results).
   const bool mfma = (act_dtype == kF16 || act_dtype == kBF16) && K % 16 == 0;
   const int64_t bytes =
-      mfma ? splitk_bytes(M, N, split_plan(M, N, K), n_out) : general_split_bytes(M, N, K);
+      mfma ? splitk_bytes(M, N, split_plan(M, N, K), n_out)
+      : (act_dtype == kF32 && planes_ok(M, N, K, n_out))
+          ? std::max(planes_bytes(M, N, K), general_split_bytes(M, N, K))
+          : general_split_bytes(M, N, K);
   return CBQ_WS_CTRL_BYTES + static_cast<size_t>(bytes);
 }
 
@@ -1831,9 +1996,13 @@ extern "C" int cbq_w8a16_linear(const void* x, int act_dtype, const int8_t* wq,
                                : w8a16_general<kBF16>(x, wq, scales, bias, nullptr, 0, nullptr, M,
                                                      N, K, nullptr, 0, y, s);
   }
-  if (act_dtype == kF32)
+  if (act_dtype == kF32) {
+    const int rc = w8a16_f32_planes(x, wq, scales, bias, n_out, M, N, K, ws, ws_bytes, y,
+                                    as_stream(stream));
+    if (rc >= 0) return rc;
     return w8a16_general<kF32>(x, wq, scales, bias, outlier_cols, n_out, w_out, M, N, K, ws,
                               ws_bytes, y, as_stream(stream));
+  }
   return act_dtype == kF16
              ? w8a16_t<kF16>(x, wq, scales, bias, outlier_cols, n_out, w_out, M, N, K, ws,
                              ws_bytes, y, as_stream(stream))

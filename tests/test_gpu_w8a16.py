@@ -2,8 +2,9 @@
 against the oracle's exact-accumulation W8A16 (float64) and the golden
 vectors. Gate (north star): rtol 1e-2 / atol 1e-2.
 
-Covers the MFMA path (fp16 / bf16, M / N / K tails), the general path (fp32
-activations, K not a multiple of 16, unaligned activations), bias, the
+Covers the MFMA path (fp16 / bf16, M / N / K tails), fp32 activations on the
+matrix cores as two bf16 planes (M > 64, K % 64 == 0), the general path (other
+fp32 shapes, K not a multiple of 16, unaligned activations), bias, the
 outlier side-GEMM, quantize_model on an MLP, state_dict round trips (own and
 reference compact layout) and the BASELINE config-5 shapes (row subsets
 against the oracle, full output against a GPU fp32 matmul of the same
@@ -154,6 +155,67 @@ def test_general_path_fp32_tiles(M, K, N):
     run_and_check(M, K, N, torch.float32, seed=M + K, bias=True, n_out=3 if K > 3 else 0,
                   rows=list(range(0, M, max(1, M // 7))))
     run_and_check(M, K, N, torch.bfloat16, seed=M + K + 1, x_offset=1 if K % 2 else 0)
+
+
+@pytest.mark.parametrize("M,K,N", [(65, 64, 40), (300, 1024, 700), (1100, 256, 520),
+                                   (2137, 2048, 8192)])
+def test_fp32_two_plane_path(M, K, N):
+    """fp32 activations with M > 64, K % 64 == 0 and no outlier columns run on
+    the matrix cores as two bf16 planes of x (hi truncated, lo = bf16(x - hi))
+    against the int8 weights. Sampled rows against the oracle; the whole
+    output against a float64 product within 2^-14 of sum_k |x w s| (x keeps
+    16 significant bits; dropping the lo plane would leave only 8); with
+    outlier columns the VALU kernel runs, also against the oracle."""
+    from cublade_amd import _abi
+    assert _abi.lib().cbq_w8a16_ws_bytes(M, N, K, 0, _abi.DTYPE_CODE[torch.float32]) > \
+        _abi.WS_CTRL_BYTES + 2 * M * K * 2
+    print(f"[w8a16 fp32 planes] M={M} K={K} N={N}", flush=True)
+    rows = [0, M // 3, M - 1]
+    y = run_and_check(M, K, N, torch.float32, seed=M + 7, bias=True, rows=rows)
+    x, wq, s, b, _, _ = make_case(M, K, N, torch.float32, M + 7, True, 0)
+    xd, wd, sd, bd = (t.to(DEV) for t in (x, wq, s, b))
+    prod = xd.double() @ wd.double().t().contiguous()
+    ref = prod * sd.double() + bd.double()
+    bound = (xd.double().abs() @ wd.double().abs().t().contiguous()) * sd.double() * 2.0 ** -14
+    err = (y.double() - ref).abs()
+    assert bool((err <= bound + 1e-6).all()), float((err - bound).max())
+    run_and_check(M, K, N, torch.float32, seed=M + 8, n_out=2, rows=rows)
+
+
+def test_fp32_two_plane_path_special_values():
+    """NaN, +-inf and huge finite activations: the two-plane path and the VALU
+    kernel (forced by a control-block-only workspace) give the same NaN and
+    inf pattern and close finite values."""
+    from cublade_amd import _abi
+    M, K, N = 130, 256, 96
+    x, wq, s, _, _, _ = make_case(M, K, N, torch.float32, 31, False, 0)
+    x[3, 5] = float("nan")
+    x[7, 9] = float("inf")
+    x[8, 1] = -float("inf")
+    x[9, :] = 1e30
+    x[10, 2] = 3.0e38
+    x[11, :] = 1e-40              # fp32 subnormals
+    xd, wd, sd = x.to(DEV), wq.to(DEV), s.to(DEV)
+    L = _abi.lib()
+    f32 = _abi.DTYPE_CODE[torch.float32]
+    outs = []
+    for nb in (L.cbq_w8a16_ws_bytes(M, N, K, 0, f32), _abi.WS_CTRL_BYTES):
+        ws = torch.zeros(nb, dtype=torch.uint8, device=DEV)
+        y = torch.empty(M, N, dtype=torch.float32, device=DEV)
+        rc = L.cbq_w8a16_linear(_abi.ptr(xd), f32, _abi.ptr(wd), _abi.ptr(sd), None, None, 0,
+                                None, M, N, K, _abi.ptr(ws), nb, _abi.ptr(y),
+                                _abi.stream_handle(xd.device))
+        _abi.check(rc, "w8a16 fp32")
+        outs.append(y)
+    torch.cuda.synchronize()
+    yp, yg = outs
+    assert torch.equal(torch.isnan(yp), torch.isnan(yg))
+    assert torch.equal(torch.isinf(yp), torch.isinf(yg))
+    fin = torch.isfinite(yg)
+    assert torch.equal(torch.sign(yp[torch.isinf(yg)]), torch.sign(yg[torch.isinf(yg)]))
+    xa = torch.where(torch.isfinite(xd), xd, torch.zeros((), device=DEV)).double().abs()
+    bound = (xa @ wd.double().abs().t().contiguous()) * sd.double() * 2.0 ** -14 + 1e-30
+    assert bool(((yp.double() - yg.double()).abs()[fin] <= bound[fin]).all())
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
