@@ -45,27 +45,29 @@ def _check_replays(static_in, make_input, fn, g, out, n=3):
                                w.view(torch.uint8) if w.dtype.itemsize == 1 else w), f"replay {seed}"
 
 
-@pytest.mark.parametrize("M", [16, 256, 4096])
-def test_graph_w8a16_layer(M):
+@pytest.mark.parametrize("M,dt", [(16, torch.float16), (256, torch.float16),
+                                  (4096, torch.float16), (256, torch.float32)])
+def test_graph_w8a16_layer(M, dt):
     """The W8A16 layer at a decode shape (weight streaming), at M = 256
-    (split-K: fp32 partials in the workspace, reused by every replay) and at
+    (split-K: fp32 partials in the workspace, reused by every replay), at
     M = 4096 (256-row MFMA tiles, whose kernel keeps a few spilled registers
-    in scratch memory)."""
+    in scratch memory), and with fp32 activations at M = 256 (three launches:
+    the bf16 planes of x and the partial planes in the workspace)."""
     from cublade_amd.quantization import cuBladeW8A16LinearLayer
     N, K = 4096, 2048
     g0 = torch.Generator().manual_seed(M)
-    layer = cuBladeW8A16LinearLayer(K, N, bias=True, dtype=torch.float16)
-    layer.quantize((0.02 * torch.randn(N, K, generator=g0)).half().to(DEV))
+    layer = cuBladeW8A16LinearLayer(K, N, bias=True, dtype=dt)
+    layer.quantize((0.02 * torch.randn(N, K, generator=g0)).to(dt).to(DEV))
     with torch.no_grad():
-        layer.bias.copy_((0.1 * torch.randn(N, generator=g0)).half())
+        layer.bias.copy_((0.1 * torch.randn(N, generator=g0)).to(dt))
     layer = layer.to(DEV)   # the bias parameter too: a captured call copies nothing from the host
-    x = torch.randn(M, K, generator=g0).half().to(DEV)
+    x = torch.randn(M, K, generator=g0).to(dt).to(DEV)
     s = torch.cuda.Stream()
     with torch.no_grad():
         fn = lambda: layer(x)
         g, out = _capture(fn, s)
         _check_replays(x, lambda i: torch.randn(M, K, generator=torch.Generator().manual_seed(100 + i))
-                       .half().to(DEV), fn, g, out)
+                       .to(dt).to(DEV), fn, g, out)
 
 
 def test_graph_quant_dequant_per_tensor():
