@@ -12,7 +12,8 @@
 // first) and as a persistent grid-stride
 // loop, with non-temporal or ordinary stores, after a read-only ("clean") and
 // a write ("dirty") 512 MiB sweep that evicts the 256 MB Infinity Cache. Sizes:
-// BASELINE configs 2 (64 Mi fp16 elements) and 3 (28672 x 8192 bf16).
+// BASELINE configs 1 (16 Mi bf16 elements), 2 (64 Mi fp16 elements) and 3
+// (28672 x 8192 bf16).
 // Fractions are of 8 TB/s over the bytes moved.
 //
 //   hipcc --offload-arch=gfx950 -O3 -std=c++17 stream_ceiling.hip -o stream_ceiling
@@ -165,7 +166,8 @@ int main() {
     return v[v.size() / 2];
   };
   struct Size { const char* name; size_t elems; };
-  const Size sizes[] = {{"C2 64Mi x 2B", size_t(8192) * 8192}, {"C3 28672x8192 x 2B", size_t(28672) * 8192}};
+  const Size sizes[] = {{"C1 16Mi x 2B", size_t(4096) * 4096}, {"C2 64Mi x 2B", size_t(8192) * 8192},
+                        {"C3 28672x8192 x 2B", size_t(28672) * 8192}};
   std::printf("# timing floor of one launch between two events after a sweep (median of 20)\n");
   std::printf("%-44s %9.2f us\n", "event pair, nothing between", timeit(false, [&] {}));
   std::printf("%-44s %9.2f us\n", "empty kernel, 256 x 1024 threads",
