@@ -119,7 +119,7 @@ struct GemmArgs {
   int tiles_m, tiles_n;
   int splits, split_steps;  // split-K: number of k-ranges, 64-k steps per range
   int full_tiles;           // split-K: tiles [0, full_tiles) run whole, the rest split
-  const uint16_t* x2;       // k_gemm_dma<.., PLANES>: the second x plane (split 1 reads it)
+  const uint16_t* x2;       // k_gemm_dma<.., PLANES>: the second x plane (splits >= splits / 2)
 };
 
 // Workgroup b of n goes to XCD b % 8; renumbered so that each XCD takes a
@@ -515,9 +515,12 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
     decode_tile(blockIdx.x, a, tm, tn);
   }
   const int m0 = tm * BM, n0 = tn * BN;
-  const int kb = (partial && !PLANES) ? split * a.split_steps : 0;   // first 64-k step
-  const int nk = (partial && !PLANES) ? min(a.split_steps, a.K / BK - kb) : a.K / BK;
-  const uint16_t* const xsrc = (PLANES && split == 1) ? a.x2 : a.x;
+  // PLANES: splits = 2 KS, split s runs k-range s % KS of x plane s / KS
+  const int ks = PLANES ? a.splits / 2 : 1;
+  const int krange = PLANES ? split % ks : split;
+  const int kb = partial ? krange * a.split_steps : 0;   // first 64-k step
+  const int nk = partial ? min(a.split_steps, a.K / BK - kb) : a.K / BK;
+  const uint16_t* const xsrc = (PLANES && split >= ks) ? a.x2 : a.x;
   const uint32_t sbase = __builtin_amdgcn_readfirstlane(lds_addr(smem));
 
   // Per-lane DMA source offsets (bytes from the k0 column of the tile). x
@@ -935,9 +938,10 @@ __global__ __launch_bounds__(kBlock) void k_splitk_reduce(GemmArgs a) {
 // exact in the fp32 accumulators, and x keeps 16 significant bits (the
 // reference's fp32 Triton dot runs at TF32 precision, 11 bits). Non-finite x:
 // hi carries it (NaN canonical), lo = 0. k_f32_planes writes the two planes;
-// k_gemm_dma<BF16, true, TM, true> then runs every tile twice over the whole
-// of K (split s reads plane s), and k_planes_reduce adds the two
-// partial planes in order and applies the fp32 scale and bias.
+// k_gemm_dma<BF16, true, TM, true> then runs every tile once per plane and
+// k-range (KS ranges per plane: 1, or up to 8 for M <= 64) into fp32 partial
+// tiles, and k_planes_reduce adds them in order and applies the fp32 scale
+// and bias.
 __global__ __launch_bounds__(kBlock) void k_f32_planes(const float* __restrict__ x, int64_t n4,
                                                      uint16_t* __restrict__ xh,
                                                      uint16_t* __restrict__ xl) {
@@ -959,9 +963,10 @@ __global__ __launch_bounds__(kBlock) void k_f32_planes(const float* __restrict__
       make_uint2(pack2_out<kBF16>(lo[0], lo[1]), pack2_out<kBF16>(lo[2], lo[3]));
 }
 
-// The two partial planes of every tile (layout as in k_splitk_reduce, all
-// tiles split, plane 0 then plane 1) -> y = fp32((p0 + p1) * s[n] + bias[n]).
-// Each thread takes two partial f4, kBlock apart.
+// The 2 KS partial planes of every tile (layout as in k_splitk_reduce, all
+// tiles split: the k-ranges of x plane hi, then those of plane lo), summed in
+// that order -> y = fp32(sum * s[n] + bias[n]). Each thread takes two
+// partial f4, kBlock apart.
 template <int TM>
 __global__ __launch_bounds__(kBlock) void k_planes_reduce(GemmArgs a, const float* __restrict__ sc,
                                                           const float* __restrict__ bias,
@@ -974,8 +979,13 @@ __global__ __launch_bounds__(kBlock) void k_planes_reduce(GemmArgs a, const floa
   const int64_t idx0 = static_cast<int64_t>(blockIdx.x) * (kBlock * 2) + threadIdx.x;
   if (idx0 >= per_plane) return;
   const f4* src = reinterpret_cast<const f4*>(a.part) + idx0;
-  const f4 p00 = src[0], p01 = src[kBlock], p10 = src[per_plane], p11 = src[per_plane + kBlock];
-  const f4 sum[2] = {p00 + p10, p01 + p11};
+  f4 sum[2] = {src[0], src[kBlock]};
+#pragma unroll 4
+  for (int p = 1; p < a.splits; ++p) {
+    const f4* q = src + p * per_plane;
+    sum[0] += q[0];
+    sum[1] += q[kBlock];
+  }
   int tm, tn;
   group_tile(static_cast<int>(idx0 / kTileF4), a, tm, tn);
   const bool vec = (a.N % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
@@ -1792,13 +1802,19 @@ int64_t general_split_bytes(int64_t M, int64_t N, int64_t K) {
   return sp > 1 ? static_cast<int64_t>(sp) * M * N * 4 : 0;
 }
 
-// Two-plane fp32 path (see k_f32_planes): M > 64, no outlier columns, the
-// DMA kernel's shape limits. The x-tile height with the fewest modelled step
-// units over both planes' workgroups: rounds of workgroups on the CUs times
-// the full-occupancy cost of a 64-k step (dma_plan's model: 1.12 / 1.46 /
-// 1.85 us for 128 / 192 / 256-row tiles).
+// Two-plane fp32 path (see k_f32_planes): no outlier columns, the DMA
+// kernel's shape limits, and for M <= 64 a weight of at least 8 MB (below
+// that the general kernel's single launch is as fast). The x-tile height
+// with the fewest modelled step units over both planes' workgroups: rounds
+// of workgroups on the CUs times the full-occupancy cost of a 64-k step
+// (dma_plan's model: 1.12 / 1.46 / 1.85 us for 128 / 192 / 256-row tiles).
+// For M <= 64 (one row of 128-row tiles) K is also split into KS ranges, so
+// that the 2 KS planes' workgroups fill the CUs (at most 8 ranges of at
+// least four 64-k steps): fp32 x at M = 16, N = 11008, K = 4096 takes two
+// ranges, 172 workgroups.
 bool planes_ok(int64_t M, int64_t N, int64_t K, int64_t n_out) {
-  return M > 64 && n_out == 0 && dma_ok(M, N, K) && 2 * cdiv(M, 128) * cdiv(N, 256) < (1LL << 30);
+  return n_out == 0 && dma_ok(M, N, K) && 2 * cdiv(M, 128) * cdiv(N, 256) < (1LL << 30) &&
+         (M > 64 || N * K >= (8LL << 20));
 }
 
 int planes_tm(int64_t M, int64_t N) {
@@ -1817,26 +1833,41 @@ int planes_tm(int64_t M, int64_t N) {
   return best_tm;
 }
 
+struct PlanesPlan {
+  int tm, ks, steps;   // x-tile height / 64, k-ranges per plane, 64-k steps per range
+};
+
+PlanesPlan planes_plan(int64_t M, int64_t N, int64_t K) {
+  const int tm = planes_tm(M, N);
+  const int64_t tiles = cdiv(M, static_cast<int64_t>(64 * tm)) * cdiv(N, static_cast<int64_t>(256));
+  const int64_t nk = K / 64;
+  int64_t ks = 1;
+  if (M <= 64) ks = std::max<int64_t>(1, std::min<int64_t>({device_cus() / (2 * tiles), 8, nk / 4}));
+  const int64_t steps = cdiv(nk, ks);
+  return {tm, static_cast<int>(cdiv(nk, steps)), static_cast<int>(steps)};   // no empty ranges
+}
+
 // Bytes after the control block: the two bf16 planes (each 256-byte
-// aligned), then the fp32 partial tiles of both planes.
+// aligned), then the fp32 partial tiles of every plane and k-range.
 int64_t planes_x_bytes(int64_t M, int64_t K) { return cdiv(M * K * 2, static_cast<int64_t>(256)) * 256; }
 
 int64_t planes_bytes(int64_t M, int64_t N, int64_t K) {
-  const int tm = planes_tm(M, N);
-  const int64_t tiles = cdiv(M, static_cast<int64_t>(64 * tm)) * cdiv(N, static_cast<int64_t>(256));
-  return 2 * planes_x_bytes(M, K) + tiles * 2 * (64 * tm) * 256 * 4;
+  const PlanesPlan p = planes_plan(M, N, K);
+  const int64_t tiles = cdiv(M, static_cast<int64_t>(64 * p.tm)) * cdiv(N, static_cast<int64_t>(256));
+  return 2 * planes_x_bytes(M, K) + tiles * 2 * p.ks * (64 * p.tm) * 256 * 4;
 }
 
 template <int TM>
-void launch_planes(GemmArgs a, const float* sc, const float* bias, float* y, hipStream_t s) {
+void launch_planes(GemmArgs a, const PlanesPlan& p, const float* sc, const float* bias, float* y,
+                   hipStream_t s) {
   a.tiles_m = static_cast<int>(cdiv(a.M, 64 * TM));
   a.tiles_n = static_cast<int>(cdiv(a.N, 256));
   a.full_tiles = 0;
-  a.splits = 2;
-  a.split_steps = a.K / 64;
+  a.splits = 2 * p.ks;
+  a.split_steps = p.steps;
   const int tiles = a.tiles_m * a.tiles_n;
-  k_gemm_dma<kBF16, true, TM, true><<<dim3(static_cast<unsigned>(2 * tiles)), dim3(kDmaThreads), 0,
-                                      s>>>(a);
+  k_gemm_dma<kBF16, true, TM, true><<<dim3(static_cast<unsigned>(a.splits * tiles)),
+                                      dim3(kDmaThreads), 0, s>>>(a);
   const int64_t n4 = static_cast<int64_t>(tiles) * 8 * kDmaTN * TM * 4 * 64;
   k_planes_reduce<TM><<<dim3(static_cast<unsigned>(cdiv(n4, kBlock * 2))), dim3(kBlock), 0, s>>>(
       a, sc, bias, y);
@@ -1866,10 +1897,11 @@ int w8a16_f32_planes(const void* x, const int8_t* wq, const void* scales, const 
   const float* sc = static_cast<const float*>(scales);
   const float* bs = static_cast<const float*>(bias);
   float* yo = static_cast<float*>(y);
-  switch (planes_tm(M, N)) {
-    case 2: launch_planes<2>(a, sc, bs, yo, s); break;
-    case 3: launch_planes<3>(a, sc, bs, yo, s); break;
-    default: launch_planes<4>(a, sc, bs, yo, s); break;
+  const PlanesPlan p = planes_plan(M, N, K);
+  switch (p.tm) {
+    case 2: launch_planes<2>(a, p, sc, bs, yo, s); break;
+    case 3: launch_planes<3>(a, p, sc, bs, yo, s); break;
+    default: launch_planes<4>(a, p, sc, bs, yo, s); break;
   }
   return launch_status("cbq_w8a16_linear");
 }

@@ -215,10 +215,11 @@ int cbq_dequant_int8_group_nd(const int8_t* q, const float* scale,
  * (ranges x tail tiles x 256 / 192 / 128 KiB for tiles of 256 / 192 / 128 x
  * 256; at most 16 ranges and at most one partial tile per CU, i.e. <= 64 MiB
  * on MI355X), with n_out > 0 one more tile per tail tile for the outlier
- * side-GEMM block, else nothing. CBQ_F32 with M > 64, K % 64 == 0 and no
- * outlier columns (matrix-core path, see cbq_w8a16_linear): two bf16 planes
- * of x (4 M K bytes) and the fp32 partial tiles of both planes (8 bytes per
- * output of the padded tiles; 360 MB at M = 4096, N = 11008). Other CBQ_F32
+ * side-GEMM block, else nothing. CBQ_F32 on the matrix-core path (see
+ * cbq_w8a16_linear): two bf16 planes of x (4 M K bytes) and the fp32
+ * partial tiles of both planes (8 bytes per output of the padded tiles; 360
+ * MB at M = 4096, N = 11008; for M <= 64 times the k-ranges per plane, at
+ * most 8: 32 MB at M = 16, N = 4096, K = 11008). Other CBQ_F32
  * shapes and K % 16 != 0 (general kernel): fp32 partial sums, up to 16 x M x
  * N x 4 bytes when its tiles give fewer than two workgroups per CU. The
  * reference allocates its temporaries inside the forward (linear.py:105-131). */
@@ -235,8 +236,9 @@ size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_out, int ac
  * with fp32 accumulation and one final round-to-nearest-even to T.
  * x: [M,K] and y: [M,N] in act_dtype, row-major. CBQ_F16 / CBQ_BF16 run
  * on MFMA. CBQ_F32 (the reference's fp32 Triton path, TF32 precision on its
- * hardware) with M > 64, K % 64 == 0, no outlier columns and a workspace of
- * cbq_w8a16_ws_bytes also runs on MFMA: x is split into two bf16 planes
+ * hardware) with K % 64 == 0, no outlier columns, M > 64 or a weight of at
+ * least 8 MB, and a workspace of cbq_w8a16_ws_bytes also runs on MFMA (for
+ * M <= 64 with K split into up to 8 ranges): x is split into two bf16 planes
  * (hi = x truncated, lo = bf16(x - hi): 16 significant bits of x, exact
  * products with the int8 weights, fp32 accumulation); other CBQ_F32 calls,
  * K % 16 != 0 and unaligned operands run a tiled fp32-FMA kernel. K == 0

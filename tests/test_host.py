@@ -93,10 +93,15 @@ def test_workspace_sizes():
     big = L.cbq_quant_int8_channel_ws_bytes(28672, 8192, 1)
     assert big >= C + 8192 * 4 * 2 and big < 64 << 20
     F16, F32 = _abi.F16, _abi.F32
-    # M <= 16, fp16: the weight-streaming kernel, no partials; fp32 activations
-    # take the general kernel: 16 k-ranges of [16, 11008] fp32 partial sums
+    # M <= 16, fp16: the weight-streaming kernel, no partials. fp32 activations:
+    # the larger of the two-plane path's needs (two bf16 planes of x, then 2
+    # planes x 2 k-ranges x 43 tiles of 128 x 256 fp32 partials) and the
+    # general kernel's (16 k-ranges of [16, 11008] fp32 partial sums)
     assert L.cbq_w8a16_ws_bytes(16, 11008, 4096, 0, F16) == C
-    assert L.cbq_w8a16_ws_bytes(16, 11008, 4096, 0, F32) == C + 16 * 16 * 11008 * 4
+    planes16 = 2 * 16 * 4096 * 2 + 2 * 2 * 43 * 128 * 256 * 4
+    assert L.cbq_w8a16_ws_bytes(16, 11008, 4096, 0, F32) == C + max(planes16, 16 * 16 * 11008 * 4)
+    # a weight under 8 MB keeps the general kernel at M <= 64
+    assert L.cbq_w8a16_ws_bytes(16, 1024, 4096, 0, F32) == C + 16 * 16 * 1024 * 4
     assert L.cbq_w8a16_ws_bytes(4096, 11008, 4096, 0, F16) == C
     # split-K tile path, 256 CUs (also the CPU-only fallback count): 2 k-ranges
     # x 86 tiles of 128 x 256 (128 KiB of fp32 partials each)
@@ -111,9 +116,13 @@ def test_workspace_sizes():
     # 24 < M <= 64 with K > 8192: the split MFMA path (11 ranges x 16 tiles of 128 x 256)
     assert L.cbq_w8a16_ws_bytes(64, 4096, 11008, 0, F16) == C + 11 * 16 * 128 * 1024
     assert L.cbq_w8a16_ws_bytes(32, 4096, 11008, 0, F16) == C + 11 * 16 * 128 * 1024
-    # M = 24: k_stream<2>, no MFMA partials; fp32: 16 ranges of [24, 4096] fp32
+    # M = 24: k_stream<2>, no MFMA partials; fp32: the two-plane path (bf16
+    # planes, then 2 planes x 8 k-ranges x 16 tiles of 128 x 256 fp32), larger
+    # than the general kernel's 16 ranges of [24, 4096] fp32
     assert L.cbq_w8a16_ws_bytes(24, 4096, 11008, 0, F16) == C
-    assert L.cbq_w8a16_ws_bytes(24, 4096, 11008, 0, F32) == C + 16 * 24 * 4096 * 4
+    planes24 = 2 * 24 * 11008 * 2 + 2 * 8 * 16 * 128 * 256 * 4
+    assert planes24 > 16 * 24 * 4096 * 4
+    assert L.cbq_w8a16_ws_bytes(24, 4096, 11008, 0, F32) == C + planes24
     # K % 16 != 0 takes the general kernel whatever the dtype
     assert L.cbq_w8a16_ws_bytes(16, 11008, 4090, 0, F16) == L.cbq_w8a16_ws_bytes(
         16, 11008, 4090, 0, F32)
