@@ -5,7 +5,7 @@
 // precision table:
 //   int8  x int8  -> int32   v_mfma_i32_32x32x32_i8
 //   uint8 x uint8 -> int32   the same on u ^ 0x80 (= u - 128), corrected exactly
-//                            by k_u8_fix:
+//                            in the epilogue (or the split-K reduce):
 //        sum_k ua ub = sum_k sa sb + 128 (sum_k sa + sum_k sb) + 16384 K
 //   fp16  x fp16  -> fp32    v_mfma_f32_32x32x16_f16
 //   fp16  x fp16  -> fp16    fp32 accumulation, one rounding at the end (the
@@ -282,11 +282,40 @@ __global__ __launch_bounds__(MmGeom<T>::kThreads) void k_mm_dma(MmArgs a) {
   // range stores its raw 4-byte sums to its plane of the partial buffer.
   typedef typename std::conditional<IN == kInI8, int, float>::type PartT;
   constexpr int ES_OUT = (OUT == kOutF16 && !SPLIT) ? 2 : 4;
+  // uint8 inputs (col_sum set): the correction 128 (row_sum[m] + col_sum[n])
+  // + 16384 K of the offset operands' product, added before the store (int32
+  // wrap-around). M and N are multiples of 16, so each lane's four row sums
+  // of a group (rows m .. m + 3, m % 4 == 0) are one 16-byte load.
+  constexpr bool kFix = (OUT == kOutI32) && !SPLIT;
+  const bool u8fix = kFix && a.col_sum != nullptr;
+  uint32_t ccol[2] = {0u, 0u};
+  if (u8fix) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      ccol[i] = 128u * static_cast<uint32_t>(a.col_sum[min(nw + 32 * i + r32, a.N - 1)]) +
+                16384u * static_cast<uint32_t>(a.K);
+  }
   uint8_t* cw = SPLIT ? static_cast<uint8_t*>(a.part) +
                             ((static_cast<int64_t>(split) * a.M + mw) * a.N + nw) * ES_OUT
                       : static_cast<uint8_t*>(a.c) + (static_cast<int64_t>(mw) * a.N + nw) * ES_OUT;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
+    uint32_t crow[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) crow[v] = 0u;
+    if (u8fix) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int mb = mw + 32 * j + 8 * g + 4 * h;
+        if (mb < a.M) {
+          const int4 r = *reinterpret_cast<const int4*>(a.row_sum + mb);
+          crow[4 * g] = 128u * static_cast<uint32_t>(r.x);
+          crow[4 * g + 1] = 128u * static_cast<uint32_t>(r.y);
+          crow[4 * g + 2] = 128u * static_cast<uint32_t>(r.z);
+          crow[4 * g + 3] = 128u * static_cast<uint32_t>(r.w);
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int nl = 32 * i + r32;
@@ -299,7 +328,8 @@ __global__ __launch_bounds__(MmGeom<T>::kThreads) void k_mm_dma(MmArgs a) {
             if constexpr (SPLIT)
               *reinterpret_cast<PartT*>(cw + off) = acc[j][i][v];
             else if constexpr (OUT == kOutI32)
-              *reinterpret_cast<int*>(cw + off) = acc[j][i][v];
+              *reinterpret_cast<uint32_t*>(cw + off) =
+                  static_cast<uint32_t>(acc[j][i][v]) + (u8fix ? crow[v] + ccol[i] : 0u);
             else if constexpr (OUT == kOutF32)
               *reinterpret_cast<float*>(cw + off) = acc[j][i][v];
             else
@@ -313,8 +343,9 @@ __global__ __launch_bounds__(MmGeom<T>::kThreads) void k_mm_dma(MmArgs a) {
 }
 
 // Split-K finish: C = the sum of the ranges' partial planes, in range order
-// (int32 wrap-around for integer inputs, fp32 for float inputs, then one
-// rounding for fp16 outputs). One thread per output.
+// (int32 wrap-around for integer inputs, plus the uint8 correction when
+// col_sum is set; fp32 for float inputs, then one rounding for fp16 outputs).
+// One thread per output.
 template <int IN, int OUT>
 __global__ __launch_bounds__(kBlock) void k_mm_reduce(MmArgs a) {
   const int64_t mn = static_cast<int64_t>(a.M) * a.N;
@@ -324,6 +355,11 @@ __global__ __launch_bounds__(kBlock) void k_mm_reduce(MmArgs a) {
     const uint32_t* p = static_cast<const uint32_t*>(a.part) + idx;
     uint32_t sum = p[0];
     for (int s = 1; s < a.splits; ++s) sum += p[s * mn];
+    if (a.col_sum) {
+      const int64_t m = idx / a.N, n = idx - m * a.N;
+      sum += 128u * (static_cast<uint32_t>(a.row_sum[m]) + static_cast<uint32_t>(a.col_sum[n])) +
+             16384u * static_cast<uint32_t>(a.K);
+    }
     static_cast<uint32_t*>(a.c)[idx] = sum;
   } else {
     const float* p = static_cast<const float*>(a.part) + idx;
@@ -439,27 +475,6 @@ __global__ __launch_bounds__(kBlock) void k_row_sums(const uint8_t* __restrict__
     __syncthreads();
     if (threadIdx.x == 0) sums[r] = red[0] + red[1] + red[2] + red[3];
     __syncthreads();
-  }
-}
-
-// uint8 correction, after the int8 GEMM on the offset operands:
-// C[m][n] += 128 (row_sum[m] + col_sum[n]) + 16384 K (int32 wrap-around).
-// N % 16 == 0 and C 16-byte aligned: four outputs per thread.
-__global__ __launch_bounds__(kBlock) void k_u8_fix(int* __restrict__ c, int64_t M, int64_t N,
-                                                   const int* __restrict__ row_sum,
-                                                   const int* __restrict__ col_sum, int64_t K) {
-  const int64_t n4 = N >> 2, total = M * n4;
-  const uint32_t kk = static_cast<uint32_t>(K) * 16384u;
-  for (int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; t < total;
-       t += static_cast<int64_t>(gridDim.x) * kBlock) {
-    const int64_t m = t / n4, n = (t % n4) * 4;
-    u32x4 v = *reinterpret_cast<const u32x4*>(c + m * N + n);
-    const uint32_t r = static_cast<uint32_t>(row_sum[m]) * 128u + kk;
-    v.x += r + static_cast<uint32_t>(col_sum[n]) * 128u;
-    v.y += r + static_cast<uint32_t>(col_sum[n + 1]) * 128u;
-    v.z += r + static_cast<uint32_t>(col_sum[n + 2]) * 128u;
-    v.w += r + static_cast<uint32_t>(col_sum[n + 3]) * 128u;
-    *reinterpret_cast<u32x4*>(c + m * N + n) = v;
   }
 }
 
@@ -672,12 +687,7 @@ extern "C" int cbq_mm(const void* A, const void* B, int in_dtype, int b_layout, 
     a.row_sum = rs;
     a.col_sum = cs;
   }
-  if (p.in == kInI8) {
-    launch_mm<kInI8, kOutI32>(a, p.tile, s);
-    if (a.col_sum)
-      k_u8_fix<<<grid_for(M * (N / 4), kBlock), kBlock, 0, s>>>(static_cast<int*>(C), M, N,
-                                                               a.row_sum, a.col_sum, K);
-  }
+  if (p.in == kInI8) launch_mm<kInI8, kOutI32>(a, p.tile, s);
   else if (p.in == kInF16 && out_dtype == CBQ_F16) launch_mm<kInF16, kOutF16>(a, p.tile, s);
   else if (p.in == kInF16) launch_mm<kInF16, kOutF32>(a, p.tile, s);
   else launch_mm<kInBF16, kOutF32>(a, p.tile, s);
