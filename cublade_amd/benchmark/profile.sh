@@ -14,11 +14,12 @@
 #    of configs 1-5 (every suite kernel's HBM bytes per dispatch)
 # 4. rocprof's derived MfmaUtil counter (MFMA busy cycles over active cycles
 #    x SIMDs) for the MFMA kernels: W8A16 (config 5) and the dense GEMM (f4)
-# 5. bare stream ceilings (cublade_amd/benchmark/stream_ceiling.hip)
+# 5. bare stream ceilings (cublade_amd/benchmark/stream_ceiling.hip) and the
+#    MFMA-only matrix-core rate (cublade_amd/benchmark/mfma_ceiling.hip)
 # Summaries: OUTDIR/bench_c2_kernels.txt, OUTDIR/quant_int8_c2_traffic.json,
 # OUTDIR/dequant_int8_c2_traffic.json, OUTDIR/suite_kernels.txt,
 # OUTDIR/suite_traffic.txt, OUTDIR/suite_configs.json, OUTDIR/mfma_util.txt,
-# OUTDIR/stream_ceiling.txt. Raw
+# OUTDIR/stream_ceiling.txt, OUTDIR/mfma_ceiling.txt. Raw
 # databases go to RAWDIR (default OUTDIR/raw; they total about 80 MiB), the
 # programs' output to OUTDIR/logs.
 # Run from the repository root on a GPU machine. Every GPU step has its own
@@ -69,6 +70,10 @@ step "bare stream ceilings (stream_ceiling.hip)"
 /opt/rocm/bin/hipcc --offload-arch=gfx950 -O3 -std=c++17 -Xclang -target-feature -Xclang -packed-fp32-ops \
   cublade_amd/benchmark/stream_ceiling.hip -o "$RAW/stream_ceiling" > "$LOGS/stream_ceiling_build.log" 2>&1 || exit $?
 timeout -k 10 120 "$RAW/stream_ceiling" > "$LOGS/stream_ceiling.log" 2>&1 || exit $?
+step "MFMA-only rate (mfma_ceiling.hip)"
+/opt/rocm/bin/hipcc --offload-arch=gfx950 -O3 -std=c++17 -Xclang -target-feature -Xclang -packed-fp32-ops \
+  cublade_amd/benchmark/mfma_ceiling.hip -o "$RAW/mfma_ceiling" > "$LOGS/mfma_ceiling_build.log" 2>&1 || exit $?
+timeout -k 10 120 "$RAW/mfma_ceiling" > "$LOGS/mfma_ceiling.log" 2>&1 || exit $?
 
 step "summaries"
 CAL="$RAW/cal_fetch/calib_results.db $RAW/cal_write/calib_results.db 262144"
@@ -114,4 +119,10 @@ traffic_json "k_deq_tensor<false, 1, 2>" 201326596 "$OUT/dequant_int8_c2_traffic
   echo "# command: hipcc --offload-arch=gfx950 -O3 -std=c++17 -Xclang -target-feature -Xclang -packed-fp32-ops cublade_amd/benchmark/stream_ceiling.hip -o RAW/stream_ceiling && RAW/stream_ceiling"
   cat "$LOGS/stream_ceiling.log"
 } > "$OUT/stream_ceiling.txt" || exit $?
+{
+  echo "# matrix-core rate with nothing but MFMAs in flight: the ceiling the GEMM kernels' TFLOP/s"
+  echo "# are read against (the clock falls under MFMA load, and further with random operands)"
+  echo "# command: hipcc --offload-arch=gfx950 -O3 -std=c++17 -Xclang -target-feature -Xclang -packed-fp32-ops cublade_amd/benchmark/mfma_ceiling.hip -o RAW/mfma_ceiling && RAW/mfma_ceiling"
+  cat "$LOGS/mfma_ceiling.log"
+} > "$OUT/mfma_ceiling.txt" || exit $?
 step "done"
