@@ -28,10 +28,12 @@
 // writes each range's raw int32 / fp32 sums to the workspace and k_mm_reduce
 // adds the ranges in order (int32 wrap-around: bit-exact; fp32:
 // deterministic).
-// Both operands are K-contiguous rows: A [M, K] as given
-// and B as B^T [N, K]. A B that is stored [N, K] (B = W^T, the usual weight
-// layout) is read in place; a [K, N] B is transposed into the workspace
-// first (k_stage_bt). uint8 operands and row lengths that are not a multiple
+// A is read as K-contiguous rows [M, K]. A B that is stored [N, K] (B = W^T,
+// the usual weight layout) is read in place as B^T rows; a contiguous
+// [K, N] B whose K fills whole 64-byte k-steps is read in place too, as
+// k-rows, its fragments assembled by gfx950's transposing LDS reads
+// (k_mm_dma<.., BKN>). Otherwise a [K, N] B is transposed into the workspace
+// first (k_stage_bt); uint8 operands and row lengths that are not a multiple
 // of 64 bytes are staged too (k_stage_rows: offset to int8, zero padding).
 //
 // LDS layout of a stage: A rows (64 B each) then B^T rows; 16-byte chunk c of
@@ -59,6 +61,9 @@ typedef __bf16 b8 __attribute__((ext_vector_type(8)));
 typedef float f16x __attribute__((ext_vector_type(16)));
 typedef int i4v __attribute__((ext_vector_type(4)));
 typedef int i16x __attribute__((ext_vector_type(16)));
+typedef int v2i32_t __attribute__((ext_vector_type(2)));
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef short v8i16_t __attribute__((ext_vector_type(8)));
 
 // Input kinds of the kernels (the C ABI's dtype codes map onto these).
 enum : int { kInI8 = 0, kInF16 = 1, kInBF16 = 2 };
@@ -84,7 +89,8 @@ __device__ __forceinline__ typename AccOf<IN>::type mfma32(const u32x4& a, const
 
 struct MmArgs {
   const uint8_t* a;      // [M, ldk] bytes, K-contiguous rows
-  const uint8_t* bt;     // [N, ldk] bytes (B^T)
+  const uint8_t* bt;     // [N, ldk] bytes (B^T); k_mm_dma<.., BKN>: B itself, [K, ldb] bytes
+  int ldb;               // k_mm_dma<.., BKN>: B's row pitch in bytes (N x element bytes)
   void* c;               // [M, N] row-major, OUT elements
   const int* row_sum;    // uint8 correction: sum_k of each signed A row [M]
   const int* col_sum;    // and of each signed B^T row [N] (null: none)
@@ -131,7 +137,28 @@ template <int T> struct MmGeom {
   static_assert(kL == 2 && T / (kWaves / 2) == 64, "two DMA rows per thread, 64-column wave tiles");
 };
 
-template <int IN, int OUT, bool SPLIT, int T>
+// XOR swizzle (in 16-byte chunks) of k-row r of a [K, N]-layout B tile in
+// LDS: the 16 (row, chunk) pairs that a transposing fragment read touches
+// per 32 lanes (8 rows x 2 chunks for int8, 4 rows x 4 chunks for 16-bit
+// elements) fall in distinct 16-byte bank groups.
+template <int IN, int T>
+__device__ __forceinline__ int kn_swizzle(int r) {
+  if constexpr (IN != kInI8) return 4 * (r & 3);
+  else if constexpr (T == 256) return 2 * (r & 7);
+  else return 2 * ((r >> 1) & 3);
+}
+
+// BKN: B is read in place as [K, N] (row pitch a.ldb), without the
+// transposing staging pass: its k-step tile is held in LDS as k-rows of T
+// columns (swizzled, see kn_swizzle), and each B^T fragment (16 consecutive
+// bytes of k for one column) is assembled by two transposing reads,
+// ds_read_b64_tr_b8 / ds_read_b64_tr_b16. Measured on MI355X: lane i of a
+// 16-lane group receives element i % EV of the 8-byte vectors that lanes
+// i / EV + (16 / EV) j address (EV = 8 / element bytes, j = 0 .. EV - 1), so
+// lanes that address k-rows k0 + sl / (16 / EV) at columns c + EV (sl %
+// (16 / EV)) give lane i column c + i, k-rows k0 .. k0 + EV - 1 in order.
+// Needs K to fill whole 64-byte k-steps (no padding).
+template <int IN, int OUT, bool SPLIT, int T, bool BKN = false>
 __global__ __launch_bounds__(MmGeom<T>::kThreads) void k_mm_dma(MmArgs a) {
   typedef typename AccOf<IN>::type Acc;
   typedef MmGeom<T> G;
@@ -159,13 +186,25 @@ __global__ __launch_bounds__(MmGeom<T>::kThreads) void k_mm_dma(MmArgs a) {
   // 16 + lane / 4, chunk slot lane % 4, which holds source chunk slot ^ swizzle.
   // Rows past M or N are clamped to the last row; their products land in
   // outputs that are never stored.
+  constexpr int ES = IN == kInI8 ? 1 : 2;     // element bytes
+  constexpr int KCPR = T * ES / 16;            // BKN: 16-byte chunks per k-row of the B tile
+  constexpr int KRPI = 64 / KCPR;              // BKN: k-rows per wave DMA instruction
   uint32_t ao[kMmL], bo[kMmL];
 #pragma unroll
   for (int u = 0; u < kMmL; ++u) {
     const int row = (u * G::kWaves + wave) * 16 + (lane >> 2);
     const int c = (lane & 3) ^ ((row >> 2) & 3);
     ao[u] = static_cast<uint32_t>(min(m0 + row, a.M - 1)) * static_cast<uint32_t>(a.ldk) + c * 16u;
-    bo[u] = static_cast<uint32_t>(min(n0 + row, a.N - 1)) * static_cast<uint32_t>(a.ldk) + c * 16u;
+    if constexpr (BKN) {
+      // k-row kr of the tile, slot lane % KCPR holding chunk slot ^ swizzle;
+      // columns past N are clamped to the row's last chunk
+      const int kr = (u * G::kWaves + wave) * KRPI + lane / KCPR;
+      const int kc = (lane % KCPR) ^ kn_swizzle<IN, T>(kr);
+      const int col = min(n0 * ES + kc * 16, a.N * ES - 16);
+      bo[u] = static_cast<uint32_t>(kr) * static_cast<uint32_t>(a.ldb) + static_cast<uint32_t>(col);
+    } else {
+      bo[u] = static_cast<uint32_t>(min(n0 + row, a.N - 1)) * static_cast<uint32_t>(a.ldk) + c * 16u;
+    }
   }
   // DMA instruction u (0 .. 2 kMmL - 1: A rows, then B^T rows) of tile t.
   auto issue_one = [&](int t, int stage, int u) {
@@ -173,7 +212,9 @@ __global__ __launch_bounds__(MmGeom<T>::kThreads) void k_mm_dma(MmArgs a) {
     if (u < kMmL)
       lds_dma16(ao[u], uniform_ptr(a.a + (kb + t) * 64), dst + u * G::kWaves * 1024);
     else
-      lds_dma16(bo[u - kMmL], uniform_ptr(a.bt + (kb + t) * 64),
+      lds_dma16(bo[u - kMmL],
+                uniform_ptr(BKN ? a.bt + static_cast<int64_t>(kb + t) * (64 / ES) * a.ldb
+                                : a.bt + (kb + t) * 64),
                 dst + kMmHalf + (u - kMmL) * G::kWaves * 1024);
   };
   auto issue = [&](int t, int stage) {
@@ -191,6 +232,28 @@ __global__ __launch_bounds__(MmGeom<T>::kThreads) void k_mm_dma(MmArgs a) {
     ar[s] = (wm * G::kWM + r32) * 64 + slot;
     br[s] = kMmHalf + (wn * 64 + r32) * 64 + slot;
   }
+  // BKN: LDS offsets of the two transposing reads (p) of B tile i, substep
+  // s. Substep s of lane half h takes k-chunk 2 h + s (16 bytes of k). A read
+  // gives each lane EV = 8 / ES consecutive k of its column: source lane sl
+  // (of 16) addresses k-row k0 + sl / LPR, bytes 8 (sl % LPR) past the
+  // group's first column (LPR = 16 / EV lanes per k-row); lanes 16 g .. 16 g
+  // + 15 of the half take columns 16 g .. 16 g + 15 of the 32-column tile.
+  uint32_t bkr[2][2][2];   // [i][s][p]
+  if constexpr (BKN) {
+    constexpr int EV = 8 / ES, LPR = 16 / EV;
+    const int sl = lane & 15, g = (lane >> 4) & 1;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const int kr = ((2 * h + s) * 16) / ES + p * EV + sl / LPR;
+          const int cb = (wn * 64 + i * 32 + 16 * g) * ES + 8 * (sl % LPR);
+          const int chunk = (cb >> 4) ^ kn_swizzle<IN, T>(kr);
+          bkr[i][s][p] = kMmHalf + kr * (T * ES) + chunk * 16 + (cb & 15);
+        }
+  }
 
   const int mw = m0 + wm * G::kWM, nw = n0 + wn * 64;
   Acc acc[J][2];   // [j: m-tile][i: n-tile]
@@ -207,8 +270,25 @@ __global__ __launch_bounds__(MmGeom<T>::kThreads) void k_mm_dma(MmArgs a) {
   };
   auto read_one = [&](int stage, int s, Frags& f, int r) {
     const uint8_t* st = smem + stage * kMmSB;
-    if (r < J) f.x[r] = *reinterpret_cast<const u32x4*>(st + ar[s] + r * 2048);
-    else f.w[r - J] = *reinterpret_cast<const u32x4*>(st + br[s] + (r - J) * 2048);
+    if (r < J) {
+      f.x[r] = *reinterpret_cast<const u32x4*>(st + ar[s] + r * 2048);
+    } else if constexpr (BKN) {
+      const int i = r - J;
+      typedef __attribute__((address_space(3))) v2i32_t* lp2;
+      if constexpr (ES == 1) {
+        const v2i32_t lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lp2)(st + bkr[i][s][0]));
+        const v2i32_t hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lp2)(st + bkr[i][s][1]));
+        f.w[i] = u32x4{static_cast<uint32_t>(lo.x), static_cast<uint32_t>(lo.y),
+                       static_cast<uint32_t>(hi.x), static_cast<uint32_t>(hi.y)};
+      } else {
+        typedef __attribute__((address_space(3))) v4i16_t* lp4;
+        const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp4)(st + bkr[i][s][0]));
+        const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp4)(st + bkr[i][s][1]));
+        f.w[i] = __builtin_bit_cast(u32x4, v8i16_t{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w});
+      }
+    } else {
+      f.w[r - J] = *reinterpret_cast<const u32x4*>(st + br[s] + (r - J) * 2048);
+    }
   };
   auto read = [&](int stage, int s, Frags& f) {
 #pragma unroll
@@ -486,6 +566,7 @@ struct MmPlan {
   bool u8;
   int64_t kb, ldk;     // row bytes, padded row bytes
   bool stage_a, stage_b;
+  bool kn_direct;      // [K, N] B read in place by k_mm_dma<.., BKN>
   int tile;            // output tile edge (256 or 128)
   int splits;          // k-ranges (1: no split-K)
   size_t a_off, b_off, rs_off, cs_off, part_off, bytes;
@@ -537,7 +618,8 @@ bool mm_plan(int64_t M, int64_t N, int64_t K, int in_dtype, int b_layout, MmPlan
   p.ldk = cdiv(p.kb, 64) * 64;
   const bool padded = p.ldk != p.kb;
   p.stage_a = p.u8 || padded;
-  p.stage_b = p.u8 || padded || b_layout == CBQ_MM_B_KN;
+  p.kn_direct = b_layout == CBQ_MM_B_KN && !p.u8 && !padded;
+  p.stage_b = p.u8 || padded || (b_layout == CBQ_MM_B_KN && !p.kn_direct);
   size_t off = CBQ_WS_CTRL_BYTES;
   p.a_off = off;
   if (p.stage_a) off = align256(off + static_cast<size_t>(M) * p.ldk);
@@ -556,24 +638,30 @@ bool mm_plan(int64_t M, int64_t N, int64_t K, int in_dtype, int b_layout, MmPlan
   return true;
 }
 
-template <int IN, int OUT, int T>
+template <int IN, int OUT, int T, bool BKN>
 void launch_mm_t(const MmArgs& a, hipStream_t s) {
   const unsigned tiles = static_cast<unsigned>(a.tiles_m * a.tiles_n);
   const dim3 b(MmGeom<T>::kThreads);
   if (a.splits > 1) {
-    k_mm_dma<IN, OUT, true, T><<<dim3(tiles * a.splits), b, 0, s>>>(a);
+    k_mm_dma<IN, OUT, true, T, BKN><<<dim3(tiles * a.splits), b, 0, s>>>(a);
     const int64_t mn = static_cast<int64_t>(a.M) * a.N;
     k_mm_reduce<IN, OUT><<<dim3(static_cast<unsigned>(cdiv(mn, kBlock))), dim3(kBlock), 0, s>>>(a);
   } else {
-    k_mm_dma<IN, OUT, false, T><<<dim3(tiles), b, 0, s>>>(a);
+    k_mm_dma<IN, OUT, false, T, BKN><<<dim3(tiles), b, 0, s>>>(a);
   }
 }
 
-// a.tiles_m / a.tiles_n must be counted in tiles of `tile`.
+// a.tiles_m / a.tiles_n must be counted in tiles of `tile`; kn: a.bt is B
+// as [K, N] (row pitch a.ldb), else B^T as [N, ldk].
 template <int IN, int OUT>
-void launch_mm(const MmArgs& a, int tile, hipStream_t s) {
-  if (tile == 128) launch_mm_t<IN, OUT, 128>(a, s);
-  else launch_mm_t<IN, OUT, 256>(a, s);
+void launch_mm(const MmArgs& a, int tile, bool kn, hipStream_t s) {
+  if (kn) {
+    if (tile == 128) launch_mm_t<IN, OUT, 128, true>(a, s);
+    else launch_mm_t<IN, OUT, 256, true>(a, s);
+  } else {
+    if (tile == 128) launch_mm_t<IN, OUT, 128, false>(a, s);
+    else launch_mm_t<IN, OUT, 256, false>(a, s);
+  }
 }
 
 unsigned grid_for(int64_t work, int64_t per_block) {
@@ -646,6 +734,7 @@ extern "C" int cbq_mm(const void* A, const void* B, int in_dtype, int b_layout, 
   a.M = static_cast<int>(M);
   a.N = static_cast<int>(N);
   a.ldk = static_cast<int>(p.ldk);
+  a.ldb = static_cast<int>(N * p.es);
   a.nk = static_cast<int>(p.ldk / 64);
   a.K = static_cast<int>(K);
   a.tiles_m = static_cast<int>(cdiv(M, p.tile));
@@ -687,9 +776,10 @@ extern "C" int cbq_mm(const void* A, const void* B, int in_dtype, int b_layout, 
     a.row_sum = rs;
     a.col_sum = cs;
   }
-  if (p.in == kInI8) launch_mm<kInI8, kOutI32>(a, p.tile, s);
-  else if (p.in == kInF16 && out_dtype == CBQ_F16) launch_mm<kInF16, kOutF16>(a, p.tile, s);
-  else if (p.in == kInF16) launch_mm<kInF16, kOutF32>(a, p.tile, s);
-  else launch_mm<kInBF16, kOutF32>(a, p.tile, s);
+  const bool kn = p.kn_direct && K > 0;
+  if (p.in == kInI8) launch_mm<kInI8, kOutI32>(a, p.tile, kn, s);
+  else if (p.in == kInF16 && out_dtype == CBQ_F16) launch_mm<kInF16, kOutF16>(a, p.tile, kn, s);
+  else if (p.in == kInF16) launch_mm<kInF16, kOutF32>(a, p.tile, kn, s);
+  else launch_mm<kInBF16, kOutF32>(a, p.tile, kn, s);
   return launch_status(what);
 }

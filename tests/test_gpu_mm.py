@@ -201,6 +201,36 @@ def test_mm_tile_and_split_paths(M, N, K, dt, path):
         np.testing.assert_array_equal(got, ref)
 
 
+@pytest.mark.parametrize("M,N,K,dt", [
+    (4096, 4096, 128, torch.int8), (256, 8192, 16384, torch.int8), (1024, 1024, 1024, torch.int8),
+    (16, 11008, 4096, torch.int8), (256, 1040, 512, torch.int8), (2048, 4096, 4096, torch.float16),
+    (1024, 4096, 4096, torch.float16), (256, 1040, 512, torch.float16), (512, 768, 1024, torch.bfloat16),
+])
+def test_mm_kn_in_place_paths(M, N, K, dt):
+    """B given as a contiguous [K, N] with K filling whole 64-byte k-steps is
+    read in place (transposing LDS reads, no staging pass) on each tile and
+    split path, including column tiles past N: sampled rows against an exact
+    numpy product (int64 modulo 2^32, or the fp32 accumulation bound)."""
+    print(f"[mm] {dt} M={M} N={N} K={K} (B [K, N] in place)", flush=True)
+    if dt in (torch.float16, torch.bfloat16):
+        g = torch.Generator().manual_seed(M + N + K)
+        A, B = torch.randn(M, K, generator=g).to(dt), torch.randn(K, N, generator=g).to(dt)
+    else:
+        A, B = rand_int((M, K), dt, seed=M + K), rand_int((K, N), dt, seed=N + K)
+    C = H().wmma_gemm(A.to(DEV), B.to(DEV))
+    rows = np.unique(np.array([0, 1, M // 3, M // 2, M - 1]))
+    if dt in (torch.float16, torch.bfloat16):
+        a64 = A[rows].float().numpy().astype(np.float64)
+        b64 = B.float().numpy().astype(np.float64)
+        ref = a64 @ b64
+        err = np.abs(np_of(C)[rows].astype(np.float64) - ref)
+        assert (err <= float_bound(a64, b64, K, False, ref)).all()
+    else:
+        ref = (np_of(A)[rows].astype(np.int64) @ np_of(B).astype(np.int64)) % (1 << 32)
+        got = np_of(C)[rows].astype(np.int64) % (1 << 32)
+        np.testing.assert_array_equal(got, ref)
+
+
 def test_mm_repeated_calls_share_workspace():
     """Back-to-back calls with different staging needs on one workspace."""
     wm = H().wmma_gemm
