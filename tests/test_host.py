@@ -191,8 +191,11 @@ def test_mm_entry_point_validates_and_sizes():
 
     # int8, B stored [N, K], K * 1 % 64 == 0: both operands read in place
     assert L.cbq_mm_ws_bytes(8192, 8192, 8192, I8, NK) == C
-    # B [K, N]: transposed copy of B (N rows of K bytes)
-    assert L.cbq_mm_ws_bytes(512, 256, 128, I8, KN) == a256(C + 256 * 128)
+    # B [K, N] with K * 1 % 64 == 0: read in place by the transposing LDS reads
+    assert L.cbq_mm_ws_bytes(512, 256, 128, I8, KN) == C
+    assert L.cbq_mm_ws_bytes(512, 256, 128, F16, KN) == C
+    # B [K, N] with K * 1 % 64 != 0: A padded, B^T staged (N rows of 128 bytes)
+    assert L.cbq_mm_ws_bytes(512, 256, 80, I8, KN) == a256(a256(C + 512 * 128) + 256 * 128)
     # K * 1 % 64 != 0: both operands padded to 64-byte rows
     assert L.cbq_mm_ws_bytes(32, 48, 80, I8, NK) == a256(a256(C + 32 * 128) + 48 * 128)
     # uint8: offset copies of both plus int32 row / column sums
