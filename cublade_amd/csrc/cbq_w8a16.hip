@@ -1329,28 +1329,30 @@ __global__ __launch_bounds__(64 * kStreamWaves) void k_stream(GemmArgs a) {
   }
 }
 
-// k_stream1<ACT> (M <= 16): weight streaming with row-contiguous loads.
+// k_stream1<ACT, RT> (M <= 16): weight streaming with row-contiguous loads.
 //
-// One 16-wave workgroup owns 3 consecutive row tiles (48 weight rows).
-// Every wave issues all of its weight loads at once, as 1 KiB row-contiguous
-// requests (wave w: rows 3 w .. 3 w + 2, step by step; 64 lanes x 16 bytes
-// per request), which stream from HBM far faster than MFMA-shaped requests
+// One 16-wave workgroup owns RT consecutive row tiles (16 RT weight rows;
+// RT = 3, or 4 when 48-row workgroups would outnumber the CUs). Every wave
+// issues all of its weight loads at once, as 1 KiB row-contiguous requests
+// (wave w: rows RT w .. RT w + RT - 1, step by step; 64 lanes x 16 bytes per
+// request), which stream from HBM far faster than MFMA-shaped requests
 // (16 rows x 64 bytes). Per 1024-k step the rows are written to a
 // padded LDS stage (row stride 1040 bytes: the 16 rows of a fragment read
 // fall in distinct bank groups), one barrier, and read back in the MFMA
-// layout: wave w takes 64-k block w of the step for all 3 tiles, with its
+// layout: wave w takes 64-k block w of the step for all RT tiles, with its
 // x fragments loaded from L2 up front. k order within a block as in
 // k_stream. The 16 partial tiles are summed in wave order (deterministic).
 // Requirements (host): K % 1024 == 0, K <= 4096, 16-byte aligned x and wq,
 // M <= 16.
-constexpr int kStream1Rows = 48;
 constexpr int kStream1Stride = 1040;
 constexpr int kStream1MaxSteps = 4;
+constexpr int kStream1MaxRT = 4;   // two stages of 64 rows: 130 KiB of LDS
 
-template <int ACT>
+template <int ACT, int RT>
 __global__ __launch_bounds__(1024) void k_stream1(GemmArgs a) {
-  constexpr int RT = 3, SB = kStream1Rows * kStream1Stride, NST = kStream1MaxSteps;
-  static_assert(2 * SB <= 2 * 49920, "two LDS stages");
+  constexpr int ROWS = 16 * RT, SB = ROWS * kStream1Stride, NST = kStream1MaxSteps;
+  static_assert(RT >= 3 && RT <= kStream1MaxRT, "3 or 4 row tiles");
+  static_assert(2 * SB <= 160 * 1024, "two LDS stages");
   static_assert(16 * RT * 64 * 16 <= 2 * SB, "reduction fits in the stages");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * SB];
 
@@ -1358,7 +1360,7 @@ __global__ __launch_bounds__(1024) void k_stream1(GemmArgs a) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int row = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * kStream1Rows;
+  const int n0 = blockIdx.x * ROWS;
   const int nsteps = a.K / 1024;
 
   // Scale and bias of this lane's outputs (wave r < 3 finishes tile r).
@@ -1392,7 +1394,7 @@ __global__ __launch_bounds__(1024) void k_stream1(GemmArgs a) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
-      const int n = min(n0 + 3 * wave + i, a.N - 1);
+      const int n = min(n0 + RT * wave + i, a.N - 1);
       wr[s][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
           a.wq + static_cast<int64_t>(n) * a.K + sc * 1024 + lane * 16));
     }
@@ -1410,7 +1412,7 @@ __global__ __launch_bounds__(1024) void k_stream1(GemmArgs a) {
     // s - 2) ended before the barrier of step s - 1.
 #pragma unroll
     for (int i = 0; i < RT; ++i)
-      *reinterpret_cast<u32x4*>(st + (3 * wave + i) * kStream1Stride + lane * 16) = wr[s][i];
+      *reinterpret_cast<u32x4*>(st + (RT * wave + i) * kStream1Stride + lane * 16) = wr[s][i];
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
@@ -1457,10 +1459,24 @@ __global__ __launch_bounds__(1024) void k_stream1(GemmArgs a) {
   }
 }
 
+// Row tiles per k_stream1 workgroup: 3 while 48-row workgroups fit on the
+// CUs at once, else 4 (0: neither fits; the host picks another kernel).
+// Measured on MI355X, M = 16, K = 4096, N = 14336: 299 workgroups of 48 rows
+// do not fit, and the kernel it then fell back to (k_skinny) took 30.0 us;
+// 224 workgroups of 64 rows took 23.8 us.
+int stream1_tiles(int64_t N) {
+  const int64_t cus = device_cus();
+  if (cdiv(N, 48) <= cus) return 3;
+  if (cdiv(N, 16 * kStream1MaxRT) <= cus) return kStream1MaxRT;
+  return 0;
+}
+
 template <int ACT>
 void launch_stream1(GemmArgs a, hipStream_t s) {
-  const unsigned grid = static_cast<unsigned>(cdiv(a.N, kStream1Rows));
-  k_stream1<ACT><<<dim3(grid), dim3(1024), 0, s>>>(a);
+  const int rt = stream1_tiles(a.N);
+  const unsigned grid = static_cast<unsigned>(cdiv(a.N, 16 * rt));
+  if (rt == 3) k_stream1<ACT, 3><<<dim3(grid), dim3(1024), 0, s>>>(a);
+  else k_stream1<ACT, kStream1MaxRT><<<dim3(grid), dim3(1024), 0, s>>>(a);
 }
 
 template <int ACT, int TM>
@@ -1633,8 +1649,8 @@ __global__ __launch_bounds__(kBlock) void k_general_reduce(GenArgs a) {
 // ---------------------------------------------------------------------------
 // Kernel choice by M (measured on MI355X at N = 11008, K = 4096):
 //   M <= 16       k_stream1 when the weight is at least 8 MB, K % 1024 == 0,
-//                 K <= 4096 and the 48-row groups fit one wave of
-//                 workgroups; else k_skinny (TM = 1)
+//                 K <= 4096 and the 48-row (else 64-row) groups fit one
+//                 wave of workgroups; else k_skinny (TM = 1)
 //   M <= 64       k_stream<2 or 4> under the same size rules (3 row tiles
 //                 per workgroup); else k_skinny, TM = ceil(M / 16); for
 //                 M > 24 and K > 8192 the split k_gemm_dma plan below first
@@ -1733,7 +1749,7 @@ Kind choose(int64_t M, int64_t N, int64_t K, int64_t n_out, size_t ws_bytes, Dma
   const int64_t cus = device_cus();
   const bool stream = stream_ok(M, N, K);
   if (M <= 16)
-    return (stream && K <= 4096 && cdiv(N, kStream1Rows) <= cus) ? kStream1 : kSkinny1;
+    return (stream && K <= 4096 && stream1_tiles(N) > 0) ? kStream1 : kSkinny1;
   const bool tiles_fit = cdiv(N, 16) <= kStreamMaxTiles * cus;
   const Kind narrow = M <= 32 ? ((stream && tiles_fit) ? kStream2 : kSkinny2)
                               : ((stream && tiles_fit) ? kStream4 : kSkinny4);

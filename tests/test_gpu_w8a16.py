@@ -120,6 +120,7 @@ def test_golden(meta, arr):
                                    (1031, 192, 1000), (1024, 64, 256), (1290, 448, 520),
                                    (1024, 80, 300), (1100, 208, 264),              # K % 64 != 0
                                    (7, 2048, 8200), (1, 4096, 4000), (13, 1024, 9000),  # k_stream1
+                                   (16, 1024, 14336), (5, 2048, 16384), (16, 4096, 12301),  # 64 rows
                                    (24, 4096, 5000), (64, 2048, 6000), (40, 1024, 9000),  # k_stream
                                    (200, 4096, 1000), (700, 1024, 3000), (500, 2048, 2600),  # split-K
                                    (800, 256, 3000)])                               # DMA, M < 1024
