@@ -535,7 +535,9 @@ def test_channel_any_axis(code, shape, axis):
     ((136, 8), 0, 136), ((3, 10, 24), 1, 5), ((4, 36, 8), 1, 6), ((2, 12, 1032), 1, 12),
     # group-major scale scratch with 8 waves per group and a walk that is not a
     # power of two (3 and 12 positions, clamped to 4 and 16), partial inner tile
-    ((3, 48, 8), 1, 24), ((2, 192, 520), 1, 96), ((5, 64, 16), 1, 8)])
+    ((3, 48, 8), 1, 24), ((2, 192, 520), 1, 96), ((5, 64, 16), 1, 8),
+    # 16 waves per group (G > 128): held in registers up to 256, read twice beyond
+    ((512, 520), 0, 256), ((2, 480, 24), 1, 160), ((1024, 64), 0, 512)])
 def test_group_any_axis(code, shape, axis, G):
     from cublade_amd.quantization import dequantize_tensor, quantize_tensor
     x = rand_bits(shape, code, seed=sum(shape) * 3 + axis + G)
