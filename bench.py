@@ -31,7 +31,7 @@ rocprofv3 FETCH_SIZE and WRITE_SIZE runs of this script, calibrated on a
 Extras, timed in the same run (HIP events around each op after a clean
 sweep, median of EXTRA_REPS): every other BASELINE config (C1 FP8 per
 tensor, C3 per channel on both axes, C4 per group, W8A16 at M = 16, 256 and
-4096). Their inputs follow the configs' distributions but are drawn on the
+4096, each next to an fp16 F.linear of the dequantized weight). Their inputs follow the configs' distributions but are drawn on the
 GPU (torch's device generator), which makes no difference to the timing of
 these data-independent kernels; the parity tests use the CPU-seeded recipes.
 
@@ -211,14 +211,22 @@ def extras(torch, dev, no_w8a16):
             layer.quantize(w.to(dev))
             xd = xa.to(dev)
             us = statistics.median(time_op(lambda: layer(xd), EXTRA_REPS, 2, flush))
+            # the same product with the dequantized weight as an fp16 F.linear
+            # (the runtime's GEMM library), timed the same way
+            wd = (layer.int8_weights.half() * layer.scales[:, None]).contiguous()
+            us_fp16 = statistics.median(time_op(lambda: torch.nn.functional.linear(xd, wd),
+                                                EXTRA_REPS, 2, flush))
             flops = 2.0 * M * N * K
             bytes_ = N * K + 2 * N + 2 * M * K + 2 * M * N
             out[f"c5_w8a16_m{M}"] = {"us": round(us, 2), "tflops": round(flops / us / 1e6, 2),
                                      "mfma_frac": round(flops / (us * 1e-6) / FP16_PEAK, 4),
                                      "gbs": round(bytes_ / us / 1e3, 1),
-                                     "hbm_frac": round(bytes_ / (us * 1e-6) / HBM_PEAK, 4)}
-            print(f"[bench] w8a16 M={M}: {us:.1f} us", file=sys.stderr, flush=True)
-            del layer, xd
+                                     "hbm_frac": round(bytes_ / (us * 1e-6) / HBM_PEAK, 4),
+                                     "fp16_linear_us": round(us_fp16, 2),
+                                     "speedup_vs_fp16_linear": round(us_fp16 / us, 3)}
+            print(f"[bench] w8a16 M={M}: {us:.1f} us (fp16 F.linear {us_fp16:.1f} us)",
+                  file=sys.stderr, flush=True)
+            del layer, xd, wd
     return out
 
 
