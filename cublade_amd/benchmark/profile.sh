@@ -74,9 +74,9 @@ if want suite; then
   step "counter WRITE_SIZE: suite configs c1-c5"
   timeout -s KILL 300 rocprofv3 --pmc WRITE_SIZE --kernel-trace -d "$RAW/swrite" -o suite -- \
     $PY -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5 --reps 3 --warmup 1 > "$LOGS/swrite.log" 2>&1 || exit $?
-  step "counter MfmaUtil: suite configs c5,f4"
+  step "counter MfmaUtil: suite configs c5,c5m,f4"
   timeout -s KILL 300 rocprofv3 --pmc MfmaUtil --kernel-trace -d "$RAW/mfma" -o suite -- \
-    $PY -m cublade_amd.benchmark.suite --configs c5,f4 --reps 3 --warmup 1 > "$LOGS/mfma.log" 2>&1 || exit $?
+    $PY -m cublade_amd.benchmark.suite --configs c5,c5m,f4 --reps 3 --warmup 1 > "$LOGS/mfma.log" 2>&1 || exit $?
 
 fi
 if want ceil; then
@@ -127,8 +127,9 @@ if want suite; then
   {
     echo "# rocprof derived counter MfmaUtil = sum(SQ_VALU_MFMA_BUSY_CYCLES) / (max(GRBM_GUI_ACTIVE) * SIMDs) * 100,"
     echo "# per kernel: mean and median over dispatches, then the values in dispatch order (the first is the"
-    echo "# suite's warm-up call): W8A16 (suite config c5, M = 16 / 256 / 768 / 1536 / 4096) and the dense GEMM (f4, 8192^3)"
-    echo "# command: rocprofv3 --pmc MfmaUtil --kernel-trace -d RAW/mfma -o suite -- python -u -m cublade_amd.benchmark.suite --configs c5,f4 --reps 3 --warmup 1"
+    echo "# suite's warm-up call): W8A16 (suite configs c5 and c5m, M = 16 / 256 / 768 / 1536 / 4096 and"
+    echo "# 1024 / 2048 / 3072) and the dense GEMM (f4, 8192^3)"
+    echo "# command: rocprofv3 --pmc MfmaUtil --kernel-trace -d RAW/mfma -o suite -- python -u -m cublade_amd.benchmark.suite --configs c5,c5m,f4 --reps 3 --warmup 1"
     $R counters "$RAW/mfma/suite_results.db" | grep -E "k_gemm_dma|k_stream|k_skinny|k_gemm<|k_mm_dma|Cijk"
   } > "$OUT/mfma_util.txt" || exit $?
 fi

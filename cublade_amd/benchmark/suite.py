@@ -10,7 +10,7 @@ every quant (x read once, codes and scales written), N + 4 * scales read +
 FLOPs (int8 GEMMs against the 5.0 POP/s dense int8 peak, the fp32-activation
 W8A16 against the 157.3 TFLOP/s fp32 peak).
 
-    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5,c5o,c5f32,f1,f3,f4,f4s [--json out.json]
+    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5,c5m,c5o,c5f32,f1,f3,f4,f4s [--json out.json]
 """
 from __future__ import annotations
 
@@ -94,6 +94,21 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
             us = time_op(lambda: layer(xd), reps, warmup, flush)
             bytes_ = N * K + 2 * N + 2 * M * K + 2 * M * N
             r = _rec("c5", f"w8a16_m{M}", us, bytes_, 2.0 * M * N * K)
+            out.append(r)
+            print(json.dumps(r), flush=True)
+            del layer, xd
+    if "c5m" in selected:
+        # the north star's M >= 1024 range of config 5's layer (every tile
+        # plan the dispatcher uses there: whole waves, split tails)
+        for M in (1024, 2048, 3072):
+            x, w = configs.c5_w8a16(M)
+            N, K = w.shape
+            layer = cuBladeW8A16LinearLayer(K, N, bias=False, dtype=torch.float16)
+            layer.quantize(w.to(dev))
+            xd = x.to(dev)
+            us = time_op(lambda: layer(xd), reps, warmup, flush)
+            bytes_ = N * K + 2 * N + 2 * M * K + 2 * M * N
+            r = _rec("c5m", f"w8a16_m{M}", us, bytes_, 2.0 * M * N * K)
             out.append(r)
             print(json.dumps(r), flush=True)
             del layer, xd
@@ -299,7 +314,7 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,c5o,c5f32,f1,f3,f4,f4s")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,c5m,c5o,c5f32,f1,f3,f4,f4s")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--json", default=None)
