@@ -1035,7 +1035,15 @@ int tensor_quant_t(const void* x, int64_t n, float eps, float* partial, char* ct
   const char* what = fp8 ? "cbq_quant_fp8_tensor" : "cbq_quant_int8_tensor";
   if (vec && n >= kFusedMinElems && device_cus() <= kMaxFusedGrid &&
       (fp8 ? fused_fits<DT, true>() : fused_fits<DT, false>())) {
-    const dim3 g(static_cast<unsigned>(device_cus())), b(kFusedBlock);
+    // One workgroup per CU, or fewer when x has fewer 4096-chunk steps than
+    // there are CUs (below 2^23 elements): the workgroups that would find no
+    // chunk of x only lengthen the launch and the exchange. Measured on
+    // MI355X (back-to-back launches): [1024, 4096] fp16 9.76 -> 8.67 us,
+    // [1024, 1024] bf16 FP8 9.10 -> 8.21 us. Below 2^20 elements the two-pass
+    // path's smaller workgroups spread a small x over more CUs: [16, 4096]
+    // bf16 FP8 6.5 us against 7.6 us for one 1024-thread workgroup.
+    const int64_t steps = cdiv(n >> 3, static_cast<int64_t>(kFusedBlock) * kFusedU);
+    const dim3 g(static_cast<unsigned>(std::min<int64_t>(steps, device_cus()))), b(kFusedBlock);
     if (fp8)
       k_quant_tensor_1pass<DT, true><<<g, b, 0, s>>>(x, n, eps, q, scale, ctl, fused_spin_limit());
     else
