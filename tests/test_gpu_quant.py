@@ -500,8 +500,12 @@ def test_config4_int8_group_full():
     ((6, 40, 24), 1), ((3, 5, 7, 8), 2), ((3, 5, 7, 8), 1), ((64, 3, 5), 1), ((2, 300, 3), 1),
     ((5, 1, 9), 1),
     # inner >= 512: one wave per contiguous segment (vector and scalar loads)
-    ((3, 17, 512), 1), ((2, 5, 1000), 1), ((4, 3, 1001), 1), ((2, 64, 4096), 1),
-    ((3, 2, 600, 2), 1)])
+    ((3, 17, 512), 1), ((2, 5, 1000), 1), ((4, 3, 1001), 1), ((3, 2, 600, 2), 1),
+    ((9, 2, 8192), 1),
+    # 512 .. 8192 chunks of 8 per channel: one workgroup per channel, held in
+    # registers (1, 2, 3 -> 4, 14 -> 16 and 16 chunks per thread)
+    ((2, 8, 2048), 1), ((2, 64, 4096), 1), ((3, 10, 2048), 1), ((2, 9, 3, 1600), 1),
+    ((7, 6, 8192), 1), ((16, 3, 4096), 1)])
 def test_channel_any_axis(code, shape, axis):
     from cublade_amd.quantization import dequantize_tensor, quantize_tensor
     x = rand_bits(shape, code, seed=sum(shape) + axis)
