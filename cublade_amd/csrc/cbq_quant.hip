@@ -26,8 +26,9 @@
 //                   quantize_int8.cu:307-371, short per-channel rows :173-297)
 //   k_rows_wg       fused single-pass quant of rows of 4096..16384 elements,
 //                   one workgroup per row held in registers (per-channel)
-//   k_rows_generic  any row length (two passes over the row; the second read
-//                   hits L2)
+//   k_rows_generic  row lengths no kernel above takes (two passes over the
+//                   row; the second read hits L2); aligned rows of 256 to
+//                   8192 chunks of 8 elements take k_chan_wg (below) instead
 //   k_colmax / k_col_finalize / k_cast_cols
 //                   per-column (axis 1) quant: partial column maxima per row
 //                   block, one finalize pass, then the cast with each
@@ -1153,6 +1154,46 @@ void launch_rows_sub(const void* x, int64_t rows, float eps, int8_t* q, float* s
       x, rows, eps, q, scale);
 }
 
+// The one-pass channel kernel (k_chan_wg) for channels of 256 to 8192
+// chunks of 8 elements: 256 threads with up to 8 chunks each up to 2048
+// chunks, else 512 threads with up to 16. It takes the N-D channel path
+// (a middle axis of [outer, channels, inner]) and rows whose length has no
+// fixed-shape kernel (outer = 1). Measured on MI355X, bf16, against the
+// paths it replaced: [7, 4096, 8192] axis 1 201.7 -> 133.6 us; [2, 8192,
+// 4096] 64.2 -> 41.9 us; rows [4096, 11008] 43.2 -> 29.6 us, [4096, 14336]
+// 52.4 -> 34.4 us, [4096, 28672] 103.5 -> 63.1 us, [8192, 5120] 37.0 ->
+// 30.2 us (k_rows_generic reads each row twice). 512 threads for every
+// channel size: [8192, 5120] 37.0 us, [16, 4096, 512] 30.6 against 26.1 us.
+constexpr int kChanWgThreads = 512;
+constexpr int kChanWgMaxV = 16;
+constexpr int kChanWgSmall = 2048;   // chunks: 256 threads up to here
+
+bool chan_wg_applies(const void* x, const void* q, int64_t outer, int64_t inner) {
+  const int64_t chunks = outer * (inner >> 3);
+  return inner % 8 == 0 && aligned(x, 16) && aligned(q, 8) && chunks >= 256 &&
+         chunks <= static_cast<int64_t>(kChanWgThreads) * kChanWgMaxV;
+}
+
+template <int DT>
+int chan_wg_quant_t(const void* x, int64_t outer, int64_t channels, int64_t inner, float eps,
+                    int8_t* q, float* scale, hipStream_t s, const char* what) {
+  const int nchunks = static_cast<int>(outer * (inner >> 3));
+  const dim3 g(static_cast<unsigned>(channels));
+  if (nchunks <= kChanWgSmall) {
+    const int v = static_cast<int>(cdiv(nchunks, 256));
+    const dim3 b(256);
+    if (v <= 2) k_chan_wg<DT, 2, 256><<<g, b, 0, s>>>(x, channels, inner, nchunks, eps, q, scale);
+    else if (v <= 4) k_chan_wg<DT, 4, 256><<<g, b, 0, s>>>(x, channels, inner, nchunks, eps, q, scale);
+    else k_chan_wg<DT, 8, 256><<<g, b, 0, s>>>(x, channels, inner, nchunks, eps, q, scale);
+    return launch_status(what);
+  }
+  const int v = static_cast<int>(cdiv(nchunks, kChanWgThreads));
+  const dim3 b(kChanWgThreads);
+  if (v <= 8) k_chan_wg<DT, 8, kChanWgThreads><<<g, b, 0, s>>>(x, channels, inner, nchunks, eps, q, scale);
+  else k_chan_wg<DT, kChanWgMaxV, kChanWgThreads><<<g, b, 0, s>>>(x, channels, inner, nchunks, eps, q, scale);
+  return launch_status(what);
+}
+
 template <int DT>
 int rows_quant_t(const void* x, int64_t rows, int64_t L, float eps, int8_t* q, float* scale,
                  hipStream_t s, const char* what) {
@@ -1180,6 +1221,9 @@ int rows_quant_t(const void* x, int64_t rows, int64_t L, float eps, int8_t* q, f
         return launch_status(what);
       default: break;
     }
+    // other lengths of 256 to 8192 chunks: one workgroup per row, in registers
+    if (chan_wg_applies(x, q, 1, L) && rows <= 0x7fffffffLL)
+      return chan_wg_quant_t<DT>(x, 1, rows, L, eps, q, scale, s, what);
   }
   k_rows_generic<DT><<<dim3(wg_rows_grid(rows)), dim3(kBlock), 0, s>>>(
       x, rows, L, vec ? 1 : 0, eps, q, scale);
@@ -1369,35 +1413,6 @@ size_t seg_ws_bytes(int64_t outer, int64_t channels) {
 
 size_t channel_nd_ws_bytes(int64_t outer, int64_t channels, int64_t inner) {
   return inner >= kSegInner ? seg_ws_bytes(outer, channels) : col_ws_bytes(outer, channels * inner);
-}
-
-// The one-pass N-D channel kernel (k_chan_wg): 512 threads, up to 16 chunks
-// each, so a channel of at most 65536 elements in whole 8-element chunks.
-// Measured on MI355X (bf16, against the two-pass column path it replaces at
-// these shapes): [7, 4096, 8192] axis 1 201.7 -> 133.0 us; [2, 8192, 4096]
-// 64.2 -> 45.2 us; [8, 4096, 4096] 122.5 -> 90.9 us. 1024 threads with up to
-// 8 chunks: 139.5 / 58.6 / 94.0 us.
-constexpr int kChanWgThreads = 512;
-constexpr int kChanWgMaxV = 16;
-
-bool chan_wg_applies(const void* x, const void* q, int64_t outer, int64_t inner) {
-  const int64_t chunks = outer * (inner >> 3);
-  return inner % 8 == 0 && aligned(x, 16) && aligned(q, 8) && chunks >= kChanWgThreads &&
-         chunks <= static_cast<int64_t>(kChanWgThreads) * kChanWgMaxV;
-}
-
-template <int DT>
-int chan_wg_quant_t(const void* x, int64_t outer, int64_t channels, int64_t inner, float eps,
-                    int8_t* q, float* scale, hipStream_t s, const char* what) {
-  const int nchunks = static_cast<int>(outer * (inner >> 3));
-  const int v = static_cast<int>(cdiv(nchunks, kChanWgThreads));
-  const dim3 g(static_cast<unsigned>(channels)), b(kChanWgThreads);
-  if (v <= 1) k_chan_wg<DT, 1, kChanWgThreads><<<g, b, 0, s>>>(x, channels, inner, nchunks, eps, q, scale);
-  else if (v <= 2) k_chan_wg<DT, 2, kChanWgThreads><<<g, b, 0, s>>>(x, channels, inner, nchunks, eps, q, scale);
-  else if (v <= 4) k_chan_wg<DT, 4, kChanWgThreads><<<g, b, 0, s>>>(x, channels, inner, nchunks, eps, q, scale);
-  else if (v <= 8) k_chan_wg<DT, 8, kChanWgThreads><<<g, b, 0, s>>>(x, channels, inner, nchunks, eps, q, scale);
-  else k_chan_wg<DT, kChanWgMaxV, kChanWgThreads><<<g, b, 0, s>>>(x, channels, inner, nchunks, eps, q, scale);
-  return launch_status(what);
 }
 
 template <int DT>
