@@ -26,8 +26,11 @@
 //                   quantize_int8.cu:307-371, short per-channel rows :173-297)
 //   k_rows_wg       fused single-pass quant of rows of 4096..16384 elements,
 //                   one workgroup per row held in registers (per-channel)
+//   k_rows_sub_any  rows / groups of any multiple of 8 below 4096 elements
+//                   without a fixed-shape kernel (k_rows_sub's layout with
+//                   masked chunk slots)
 //   k_rows_generic  row lengths no kernel above takes (two passes over the
-//                   row; the second read hits L2); aligned rows of 256 to
+//                   row; the second read hits L2); aligned rows of 512 to
 //                   8192 chunks of 8 elements take k_chan_wg (below) instead
 //   k_colmax / k_col_finalize / k_cast_cols
 //                   per-column (axis 1) quant: partial column maxima per row
@@ -504,6 +507,63 @@ __global__ __launch_bounds__(kBlock) void k_rows_sub(
 #pragma unroll
       for (int v = 0; v < VPL; ++v)
         stg8(q + row * L + (v * LPR + lr) * 8, pack8_int8(f[v], inv));
+      if (lr == 0) scale[row] = 1.0f / inv;
+    }
+  }
+}
+
+// Rows (groups) of cg chunks of 8 elements for any cg < 512 without a
+// fixed-shape kernel (e.g. groups of 56, 112, 224 elements): the layout of
+// k_rows_sub with LPR * VPL >= cg chunk slots per row, chunk j = v * LPR + lr
+// in slot (v, lr); slots past cg load the row's first chunk (in bounds), stay
+// out of the maximum and store nothing.
+template <int DT, int LPR, int VPL, int RI>
+__global__ __launch_bounds__(kBlock) void k_rows_sub_any(
+    const void* __restrict__ x, int64_t rows, int cg, float eps, int8_t* __restrict__ q,
+    float* __restrict__ scale) {
+  constexpr int RPW = kWave / LPR;
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int sub = lane / LPR;
+  const int lr = lane % LPR;
+  const int64_t L = static_cast<int64_t>(cg) * 8;
+  const int64_t row0 =
+      (static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + wave) * (RI * RPW) + sub;
+
+  Raw8<DT> r[RI][VPL];
+#pragma unroll
+  for (int it = 0; it < RI; ++it) {
+    const int64_t row = row0 + static_cast<int64_t>(it) * RPW;
+    if (row < rows) {
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const int j = v * LPR + lr;
+        r[it][v] = ld8<DT>(x, row * L + (j < cg ? j : 0) * 8);
+      }
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < RI; ++it) {
+    const int64_t row = row0 + static_cast<int64_t>(it) * RPW;
+    const bool ok = row < rows;
+    float f[VPL][8];
+    float m = 0.0f;
+    if (ok) {
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        cvt8<DT>(r[it][v], f[v]);
+        const float mv = absmax8(f[v], 0.0f);
+        m = v * LPR + lr < cg ? fmaxf(m, mv) : m;
+      }
+    }
+    m = group_max<LPR>(m);   // every lane participates
+    const float inv = inv_scale(m, eps, kQmaxInt8);
+    if (ok) {
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const int j = v * LPR + lr;
+        if (j < cg) stg8(q + row * L + j * 8, pack8_int8(f[v], inv));
+      }
       if (lr == 0) scale[row] = 1.0f / inv;
     }
   }
@@ -1194,6 +1254,39 @@ int chan_wg_quant_t(const void* x, int64_t outer, int64_t channels, int64_t inne
   return launch_status(what);
 }
 
+// Rows of cg < 512 chunks without a fixed-shape kernel: LPR lanes (a power
+// of two, at most 64) x VPL chunks per row, the fewest slots that cover cg.
+// Measured on MI355X, groups along the last axis of [16384, 14336] bf16,
+// against k_rows_generic (a 256-thread workgroup per group, two reads):
+// G = 56 3096.6 -> 114.4 us, G = 112 1624.7 -> 115.1 us, G = 224 869.6 ->
+// 117.8 us, G = 896 285.0 -> 113.9 us, G = 1792 189.1 -> 113.5 us (G = 128:
+// 112.7 us); G = 3584 117.5 us against 134.2 us in k_chan_wg, rows of 2056
+// 24.7 against 35.5 us.
+constexpr int kRowsAnyMaxChunks = 512;
+template <int DT, int LPR, int VPL>
+void launch_rows_sub_any(const void* x, int64_t rows, int cg, float eps, int8_t* q, float* scale,
+                         hipStream_t s) {
+  constexpr int RI = (LPR * VPL >= 64) ? 2 : 4;
+  constexpr int64_t rows_per_wg = static_cast<int64_t>(kBlock / kWave) * RI * (kWave / LPR);
+  k_rows_sub_any<DT, LPR, VPL, RI><<<dim3(static_cast<unsigned>(cdiv(rows, rows_per_wg))),
+                                     dim3(kBlock), 0, s>>>(x, rows, cg, eps, q, scale);
+}
+
+template <int DT>
+void rows_quant_any(const void* x, int64_t rows, int cg, float eps, int8_t* q, float* scale,
+                    hipStream_t s) {
+  if (cg <= 1) launch_rows_sub_any<DT, 1, 1>(x, rows, cg, eps, q, scale, s);
+  else if (cg <= 2) launch_rows_sub_any<DT, 2, 1>(x, rows, cg, eps, q, scale, s);
+  else if (cg <= 4) launch_rows_sub_any<DT, 4, 1>(x, rows, cg, eps, q, scale, s);
+  else if (cg <= 8) launch_rows_sub_any<DT, 8, 1>(x, rows, cg, eps, q, scale, s);
+  else if (cg <= 16) launch_rows_sub_any<DT, 16, 1>(x, rows, cg, eps, q, scale, s);
+  else if (cg <= 32) launch_rows_sub_any<DT, 32, 1>(x, rows, cg, eps, q, scale, s);
+  else if (cg <= 64) launch_rows_sub_any<DT, 64, 1>(x, rows, cg, eps, q, scale, s);
+  else if (cg <= 128) launch_rows_sub_any<DT, 64, 2>(x, rows, cg, eps, q, scale, s);
+  else if (cg <= 256) launch_rows_sub_any<DT, 64, 4>(x, rows, cg, eps, q, scale, s);
+  else launch_rows_sub_any<DT, 64, 8>(x, rows, cg, eps, q, scale, s);
+}
+
 template <int DT>
 int rows_quant_t(const void* x, int64_t rows, int64_t L, float eps, int8_t* q, float* scale,
                  hipStream_t s, const char* what) {
@@ -1221,8 +1314,13 @@ int rows_quant_t(const void* x, int64_t rows, int64_t L, float eps, int8_t* q, f
         return launch_status(what);
       default: break;
     }
-    // other lengths of 256 to 8192 chunks: one workgroup per row, in registers
-    if (chan_wg_applies(x, q, 1, L) && rows <= 0x7fffffffLL)
+    // other lengths: below 512 chunks several rows per wave, up to 8192 one
+    // workgroup per row, in registers either way
+    if ((L >> 3) < kRowsAnyMaxChunks) {
+      rows_quant_any<DT>(x, rows, static_cast<int>(L >> 3), eps, q, scale, s);
+      return launch_status(what);
+    }
+    if (chan_wg_applies(x, q, 1, L))
       return chan_wg_quant_t<DT>(x, 1, rows, L, eps, q, scale, s, what);
   }
   k_rows_generic<DT><<<dim3(wg_rows_grid(rows)), dim3(kBlock), 0, s>>>(

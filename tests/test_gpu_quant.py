@@ -290,8 +290,10 @@ def test_tensor_fp32_int8(n):
 
 
 ROW_LENGTHS = [8, 16, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192, 16384,   # fast shapes
-               2056, 3000, 5120, 11008, 14336, 28672, 65536,                     # one workgroup
-               1, 3, 7, 40, 96, 136, 1000, 2040, 3004, 65544]                    # generic
+               24, 40, 56, 96, 112, 136, 224, 448, 896, 1000, 1792, 2040, 2056,  # masked slots
+               3000, 3584,
+               4104, 5120, 11008, 14336, 28672, 65536,                           # one workgroup
+               1, 3, 7, 3004, 65544]                                             # generic
 
 
 @pytest.mark.parametrize("L", ROW_LENGTHS)
