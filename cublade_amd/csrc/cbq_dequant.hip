@@ -8,8 +8,10 @@
 //   k_deq_rows_sub   rows of 8..2048 codes (per-group, short per-channel rows)
 //                    owned by power-of-two lane groups; 8-byte loads, 16-byte
 //                    stores (dequantize_int8.cu:118-134, :70-109)
-//   k_deq_rows_wg    one workgroup per row of any length that is a multiple
-//                    of 8 (long per-channel rows)
+//   k_deq_rows_sub_any rows of any multiple of 8 below 4096 codes without a
+//                    fixed-shape kernel: k_deq_rows_sub's layout, masked slots
+//   k_deq_rows_wg    one workgroup per row of any longer length that is a
+//                    multiple of 8 (long per-channel rows)
 //   k_deq_rows_scalar any row length, element at a time
 //   k_deq_cols       per-column scales (axis 1), and per-channel scales of an
 //                    N-D tensor seen as [outer, channels * inner]: each thread
@@ -137,6 +139,54 @@ __global__ __launch_bounds__(kBlock) void k_deq_rows_sub(
 #pragma unroll
         for (int k = 0; k < 8; ++k) f[k] *= s[it];
         st8<OUT>(y, row * L + (v * LPR + lr) * 8, f);
+      }
+    }
+  }
+}
+
+// Rows of cg chunks of 8 codes for any cg < 512 without a fixed-shape
+// kernel (group sizes such as 56 or 112): the layout of k_deq_rows_sub with
+// LPR * VPL >= cg chunk slots per row, slots past cg idle.
+template <int OUT, int LPR, int VPL, int RI>
+__global__ __launch_bounds__(kBlock) void k_deq_rows_sub_any(
+    const int8_t* __restrict__ q, const float* __restrict__ scale, int64_t rows, int cg,
+    void* __restrict__ y) {
+  constexpr int RPW = kWave / LPR;
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int sub = lane / LPR;
+  const int lr = lane % LPR;
+  const int64_t L = static_cast<int64_t>(cg) * 8;
+  const int64_t row0 =
+      (static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + wave) * (RI * RPW) + sub;
+  uint2 r[RI][VPL];
+  float s[RI];
+#pragma unroll
+  for (int it = 0; it < RI; ++it) {
+    const int64_t row = row0 + static_cast<int64_t>(it) * RPW;
+    if (row < rows) {
+      s[it] = scale[row];
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const int j = v * LPR + lr;
+        r[it][v] = ldg8(q + row * L + (j < cg ? j : 0) * 8);
+      }
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < RI; ++it) {
+    const int64_t row = row0 + static_cast<int64_t>(it) * RPW;
+    if (row < rows) {
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const int j = v * LPR + lr;
+        if (j >= cg) continue;
+        float f[8];
+        int8x4_to_f32(r[it][v].x, f);
+        int8x4_to_f32(r[it][v].y, f + 4);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) f[k] *= s[it];
+        st8<OUT>(y, row * L + j * 8, f);
       }
     }
   }
@@ -382,6 +432,32 @@ void launch_deq_rows_sub(const int8_t* q, const float* scale, int64_t rows, void
                                        dim3(kBlock), 0, s>>>(q, scale, rows, y);
 }
 
+template <int OUT, int LPR, int VPL>
+void launch_deq_rows_sub_any(const int8_t* q, const float* scale, int64_t rows, int cg, void* y,
+                             hipStream_t s) {
+  constexpr int RI = (LPR * VPL >= 64) ? 2 : 4;
+  constexpr int64_t rows_per_wg = static_cast<int64_t>(kBlock / kWave) * RI * (kWave / LPR);
+  k_deq_rows_sub_any<OUT, LPR, VPL, RI><<<dim3(static_cast<unsigned>(cdiv(rows, rows_per_wg))),
+                                           dim3(kBlock), 0, s>>>(q, scale, rows, cg, y);
+}
+
+// Rows of cg < 512 chunks without a fixed-shape kernel (k_deq_rows_wg would
+// give each short row a workgroup of its own): LPR lanes x VPL chunks.
+template <int OUT>
+void deq_rows_any(const int8_t* q, const float* scale, int64_t rows, int cg, void* y,
+                  hipStream_t s) {
+  if (cg <= 1) launch_deq_rows_sub_any<OUT, 1, 1>(q, scale, rows, cg, y, s);
+  else if (cg <= 2) launch_deq_rows_sub_any<OUT, 2, 1>(q, scale, rows, cg, y, s);
+  else if (cg <= 4) launch_deq_rows_sub_any<OUT, 4, 1>(q, scale, rows, cg, y, s);
+  else if (cg <= 8) launch_deq_rows_sub_any<OUT, 8, 1>(q, scale, rows, cg, y, s);
+  else if (cg <= 16) launch_deq_rows_sub_any<OUT, 16, 1>(q, scale, rows, cg, y, s);
+  else if (cg <= 32) launch_deq_rows_sub_any<OUT, 32, 1>(q, scale, rows, cg, y, s);
+  else if (cg <= 64) launch_deq_rows_sub_any<OUT, 64, 1>(q, scale, rows, cg, y, s);
+  else if (cg <= 128) launch_deq_rows_sub_any<OUT, 64, 2>(q, scale, rows, cg, y, s);
+  else if (cg <= 256) launch_deq_rows_sub_any<OUT, 64, 4>(q, scale, rows, cg, y, s);
+  else launch_deq_rows_sub_any<OUT, 64, 8>(q, scale, rows, cg, y, s);
+}
+
 template <int OUT>
 int deq_rows_t(const int8_t* q, const float* scale, int64_t rows, int64_t L, void* y,
                hipStream_t s, const char* what) {
@@ -399,6 +475,10 @@ int deq_rows_t(const int8_t* q, const float* scale, int64_t rows, int64_t L, voi
       case 1024: launch_deq_rows_sub<OUT, 64, 2>(q, scale, rows, y, s); return launch_status(what);
       case 2048: launch_deq_rows_sub<OUT, 64, 4>(q, scale, rows, y, s); return launch_status(what);
       default:
+        if ((L >> 3) < 512) {
+          deq_rows_any<OUT>(q, scale, rows, static_cast<int>(L >> 3), y, s);
+          return launch_status(what);
+        }
         k_deq_rows_wg<OUT><<<dim3(rows_grid(rows)), dim3(kBlock), 0, s>>>(q, scale, rows, L, y);
         return launch_status(what);
     }
