@@ -17,6 +17,8 @@
 //                    N-D tensor seen as [outer, channels * inner]: each thread
 //                    keeps the scales of its eight columns in registers while
 //                    walking rows
+//   k_deq_cols_narrow the same for rows of at most 1024 codes: several rows
+//                    per workgroup pass, so every thread has a chunk
 //   k_deq_group_tile groups along a non-last axis (the reference moves the
 //                    axis last with two copies, dequantizers.py:58-72): 1-2
 //                    waves per group and 512 inner positions, in place
@@ -290,6 +292,47 @@ __global__ __launch_bounds__(kBlock) void k_deq_cols(
   }
 }
 
+// Narrow columns (cols % 8 == 0, u = cols / 8 <= kBlock / 2 chunks per row,
+// e.g. [262144, 64]): k_deq_cols would leave all but u threads of a
+// workgroup idle; here thread t takes chunk t % u of rows r0 + t / u,
+// stepping by rpi = kBlock / u rows.
+template <int OUT>
+__global__ __launch_bounds__(kBlock) void k_deq_cols_narrow(
+    const int8_t* __restrict__ q, const float* __restrict__ scale, int64_t rows, int64_t cols,
+    int64_t RB, int u, int rpi, int64_t inner, void* __restrict__ y) {
+  const int sub = static_cast<int>(threadIdx.x) / u, cu = static_cast<int>(threadIdx.x) - sub * u;
+  if (sub >= rpi) return;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * RB;
+  const int64_t r1 = r0 + RB < rows ? r0 + RB : rows;
+  const int64_t c = static_cast<int64_t>(cu) * 8;
+  float s[8];
+  channel_vals8(scale, c, inner, s);
+  int64_t r = r0 + sub;
+  for (; r + 3 * rpi < r1; r += 4 * rpi) {
+    uint2 raw[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) raw[k] = ldg8(q + (r + k * rpi) * cols + c);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float f[8];
+      int8x4_to_f32(raw[k].x, f);
+      int8x4_to_f32(raw[k].y, f + 4);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] *= s[e];
+      st8<OUT>(y, (r + k * rpi) * cols + c, f);
+    }
+  }
+  for (; r < r1; r += rpi) {
+    const uint2 raw = ldg8(q + r * cols + c);
+    float f[8];
+    int8x4_to_f32(raw.x, f);
+    int8x4_to_f32(raw.y, f + 4);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] *= s[e];
+    st8<OUT>(y, r * cols + c, f);
+  }
+}
+
 // Groups along a non-last axis ([outer, len, inner], groups of G along len):
 // one thread per group (o, g, i), i fastest; scale index in the reference's
 // movedim layout, (o * inner + i) * (len / G) + g (dequantizers.py:61-72).
@@ -493,10 +536,22 @@ int deq_rows(const int8_t* q, const float* scale, int64_t rows, int64_t L, void*
                      : deq_rows_t<kBF16>(q, scale, rows, L, y, s, what);
 }
 
+constexpr int64_t kDeqNarrowRows = 8;
+
 template <int OUT>
 int deq_cols_t(const int8_t* q, const float* scale, int64_t rows, int64_t cols, int64_t inner,
                void* y, hipStream_t s, const char* what) {
   const bool vec = (cols % 8 == 0) && aligned(q, 8) && aligned(y, 16);
+  const int64_t u = cols >> 3;
+  if (vec && u <= kBlock / 2) {
+    // narrow rows: kDeqNarrowRows rows per thread, rpi threads per chunk
+    const int rpi = kBlock / static_cast<int>(u);
+    int64_t RB = rpi * kDeqNarrowRows;
+    if (cdiv(rows, RB) > 65535) RB = cdiv(cdiv(rows, 65535), rpi) * rpi;
+    k_deq_cols_narrow<OUT><<<dim3(1, static_cast<unsigned>(cdiv(rows, RB))), dim3(kBlock), 0, s>>>(
+        q, scale, rows, cols, RB, static_cast<int>(u), rpi, inner, y);
+    return launch_status(what);
+  }
   const int64_t col_blocks = vec ? cdiv(cdiv(cols, 8), kBlock) : cdiv(cols, kBlock);
   // Short row blocks (16 rows per thread): many workgroups in flight;
   // measured on MI355X, walks of ~60 rows per thread lose ~5-20%, and

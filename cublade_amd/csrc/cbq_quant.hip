@@ -32,10 +32,17 @@
 //   k_rows_generic  row lengths no kernel above takes (two passes over the
 //                   row; the second read hits L2); aligned rows of 512 to
 //                   8192 chunks of 8 elements take k_chan_wg (below) instead
+//   k_rows_split_max / k_rows_split_cast
+//                   few long rows (fewer than about two per CU): each row cut
+//                   into slices over the CUs, one partial maximum per slice
+//                   in the workspace, then the cast of each slice
 //   k_colmax / k_col_finalize / k_cast_cols
 //                   per-column (axis 1) quant: partial column maxima per row
 //                   block, one finalize pass, then the cast with each
 //                   thread's eight column multipliers held in registers
+//   k_colmax_narrow / k_cast_cols_narrow
+//                   the same for rows of at most 1024 columns: several rows
+//                   per workgroup pass, so every thread has a chunk
 //   k_chan_wg       per-channel quant of an N-D tensor seen as
 //                   [outer, channels, inner] in one pass: one workgroup per
 //                   channel holding its outer segments (512 .. 65536
@@ -569,6 +576,80 @@ __global__ __launch_bounds__(kBlock) void k_rows_sub_any(
   }
 }
 
+// Few long rows (e.g. per-channel axis 0 of [64, 1024, 1024]): each row is
+// cut into `splits` slices of sc chunks and workgroup (row, slice) = blockIdx
+// (y, x) works on one slice, so the grid fills the CUs however few the rows.
+// k_rows_split_max writes one partial maximum per slice; k_rows_split_cast
+// reduces its row's partials (L2) while its first loads are in flight, then
+// casts its slice. L % 8 == 0, 16-byte aligned x, 8-byte aligned q.
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_rows_split_max(
+    const void* __restrict__ x, int64_t L, int64_t sc, float* __restrict__ partial) {
+  __shared__ float red[kBlock / kWave];
+  const int64_t row = blockIdx.y, n8 = L >> 3;
+  const int64_t c_end = min((static_cast<int64_t>(blockIdx.x) + 1) * sc, n8);
+  const int64_t base = row * L;
+  float m = 0.0f;
+  for (int64_t c0 = static_cast<int64_t>(blockIdx.x) * sc + threadIdx.x; c0 < c_end;
+       c0 += kU * kBlock) {
+    Raw8<DT> r[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
+      if (c < c_end) r[u] = ld8<DT>(x, base + c * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
+      if (c < c_end) {
+        float f[8];
+        cvt8<DT>(r[u], f);
+        m = absmax8(f, m);
+      }
+    }
+  }
+  m = block_max(m, red);
+  if (threadIdx.x == 0) partial[row * gridDim.x + blockIdx.x] = m;
+}
+
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_rows_split_cast(
+    const void* __restrict__ x, int64_t L, int64_t sc, const float* __restrict__ partial,
+    float eps, int8_t* __restrict__ q, float* __restrict__ scale) {
+  __shared__ float red[kBlock / kWave];
+  const int64_t row = blockIdx.y, n8 = L >> 3;
+  const int64_t c_end = min((static_cast<int64_t>(blockIdx.x) + 1) * sc, n8);
+  const int64_t base = row * L;
+  int64_t c0 = static_cast<int64_t>(blockIdx.x) * sc + threadIdx.x;
+  Raw8<DT> r[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
+    if (c < c_end) r[u] = ld8<DT>(x, base + c * 8);
+  }
+  const float m = reduce_partials(partial + row * gridDim.x, static_cast<int>(gridDim.x), red);
+  const float inv = inv_scale(m, eps, kQmaxInt8);
+  if (blockIdx.x == 0 && threadIdx.x == 0) scale[row] = 1.0f / inv;
+  for (;;) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
+      if (c < c_end) {
+        float f[8];
+        cvt8<DT>(r[u], f);
+        stg8(q + base + c * 8, pack8_int8(f, inv));
+      }
+    }
+    c0 += kU * kBlock;
+    if (c0 >= c_end) break;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t c = c0 + static_cast<int64_t>(u) * kBlock;
+      if (c < c_end) r[u] = ld8<DT>(x, base + c * 8);
+    }
+  }
+}
+
 // One workgroup of B threads per row of L = B * VPL * 8 elements, held in
 // registers. Workgroups stride over rows (the row loop is uniform per
 // workgroup). Measured on MI355X, rows of 8192 bf16 (C3 axis 0): 512 threads
@@ -802,6 +883,92 @@ __global__ __launch_bounds__(kBlock) void k_cast_cols(
     const float inv = inv_c[c / inner];
     for (int64_t r = r0; r < r1; ++r)
       q[r * cols + c] = static_cast<int8_t>(q_int8(ld1<DT>(x, r * cols + c) * inv));
+  }
+}
+
+// Narrow columns (cols % 8 == 0, u = cols / 8 <= kBlock / 2 chunks per row,
+// e.g. [262144, 64] or the [outer, 512] view of a channel on the last axis):
+// the wide kernels above leave all but u threads of a workgroup idle, so
+// here thread t takes chunk t % u of rows r0 + t / u, stepping by rpi =
+// kBlock / u rows. k_colmax_narrow folds its rpi sub-rows through LDS and
+// writes the same [gridDim.y, cols] partials as k_colmax.
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_colmax_narrow(
+    const void* __restrict__ x, int64_t rows, int64_t cols, int64_t RB, int u, int rpi,
+    float* __restrict__ partial) {
+  __shared__ float4 red[kBlock][2];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * RB;
+  const int64_t r1 = r0 + RB < rows ? r0 + RB : rows;
+  const int sub = static_cast<int>(threadIdx.x) / u, cu = static_cast<int>(threadIdx.x) - sub * u;
+  const int64_t c = static_cast<int64_t>(cu) * 8;
+  float m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (sub < rpi) {
+    int64_t r = r0 + sub;
+    for (; r + 3 * rpi < r1; r += 4 * rpi) {
+      Raw8<DT> raw[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) raw[k] = ld8<DT>(x, (r + k * rpi) * cols + c);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float f[8];
+        cvt8<DT>(raw[k], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m[e] = fmaxf(m[e], __builtin_fabsf(f[e]));
+      }
+    }
+    for (; r < r1; r += rpi) {
+      float f[8];
+      cvt8<DT>(ld8<DT>(x, r * cols + c), f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m[e] = fmaxf(m[e], __builtin_fabsf(f[e]));
+    }
+  }
+  red[threadIdx.x][0] = make_float4(m[0], m[1], m[2], m[3]);
+  red[threadIdx.x][1] = make_float4(m[4], m[5], m[6], m[7]);
+  __syncthreads();
+  if (sub == 0) {
+    for (int k = 1; k < rpi; ++k) {
+      const float4 a = red[k * u + cu][0], b = red[k * u + cu][1];
+      m[0] = fmaxf(m[0], a.x); m[1] = fmaxf(m[1], a.y); m[2] = fmaxf(m[2], a.z); m[3] = fmaxf(m[3], a.w);
+      m[4] = fmaxf(m[4], b.x); m[5] = fmaxf(m[5], b.y); m[6] = fmaxf(m[6], b.z); m[7] = fmaxf(m[7], b.w);
+    }
+    float4* o = reinterpret_cast<float4*>(partial + static_cast<int64_t>(blockIdx.y) * cols + c);
+    o[0] = make_float4(m[0], m[1], m[2], m[3]);
+    o[1] = make_float4(m[4], m[5], m[6], m[7]);
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_cast_cols_narrow(
+    const void* __restrict__ x, int64_t rows, int64_t cols, int64_t RB, int u, int rpi,
+    const float* __restrict__ inv_c, int64_t inner, int8_t* __restrict__ q) {
+  const int sub = static_cast<int>(threadIdx.x) / u, cu = static_cast<int>(threadIdx.x) - sub * u;
+  if (sub >= rpi) return;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * RB;
+  const int64_t r1 = r0 + RB < rows ? r0 + RB : rows;
+  const int64_t c = static_cast<int64_t>(cu) * 8;
+  float inv[8];
+  channel_vals8(inv_c, c, inner, inv);
+  int64_t r = r0 + sub;
+  for (; r + 3 * rpi < r1; r += 4 * rpi) {
+    Raw8<DT> raw[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) raw[k] = ld8<DT>(x, (r + k * rpi) * cols + c);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float f[8];
+      cvt8<DT>(raw[k], f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] *= inv[e];
+      stg8(q + (r + k * rpi) * cols + c, pack8_int8(f, 1.0f));
+    }
+  }
+  for (; r < r1; r += rpi) {
+    float f[8];
+    cvt8<DT>(ld8<DT>(x, r * cols + c), f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] *= inv[e];
+    stg8(q + r * cols + c, pack8_int8(f, 1.0f));
   }
 }
 
@@ -1287,11 +1454,55 @@ void rows_quant_any(const void* x, int64_t rows, int cg, float eps, int8_t* q, f
   else launch_rows_sub_any<DT, 64, 8>(x, rows, cg, eps, q, scale, s);
 }
 
+// Slices per row for the split-row path: enough workgroups for about four
+// per CU, each slice at least kSplitMinChunks chunks; 1 (no split) when the
+// one-workgroup-per-row kernels have enough rows. The split reads x twice,
+// so it pays only where those kernels starve the CUs. Measured on MI355X,
+// bf16, one workgroup per row -> split: [64, 2^20] 512.5 -> 63.6 us,
+// [256, 262144] 146.7 -> 63.8 us, [8, 2^21] 1011.5 -> 21.1 us; against it
+// [512, 65536] 24.2 -> 34.6 us and [255, 8200] 8.1 -> 10.3 us.
+constexpr int64_t kSplitMinChunks = 1024;
+constexpr int64_t kSplitMaxSlices = 256;
+
+int64_t row_splits(int64_t rows, int64_t L) {
+  if (L % 8 != 0 || rows <= 0 || rows > 65535) return 1;
+  const int64_t n8 = L >> 3;
+  const int64_t most = std::min<int64_t>(n8 / kSplitMinChunks, kSplitMaxSlices);
+  if (most < 2) return 1;
+  const int64_t cus = device_cus();
+  const bool one_pass = n8 <= static_cast<int64_t>(kChanWgThreads) * kChanWgMaxV;
+  if (rows >= 2 * cus || (one_pass && rows >= cus)) return 1;
+  const int64_t sp = std::min(cdiv(4 * cus, rows), most);
+  return sp >= 2 ? sp : 1;
+}
+
+size_t row_split_ws_bytes(int64_t rows, int64_t L) {
+  const int64_t sp = row_splits(rows, L);
+  return sp > 1 ? CBQ_WS_CTRL_BYTES + static_cast<size_t>(rows * sp) * 4 : CBQ_WS_CTRL_BYTES;
+}
+
+template <int DT>
+int rows_split_quant_t(const void* x, int64_t rows, int64_t L, int64_t sp, float eps, void* ws,
+                       int8_t* q, float* scale, hipStream_t s, const char* what) {
+  float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + CBQ_WS_CTRL_BYTES);
+  const int64_t sc = cdiv(L >> 3, sp);
+  const dim3 g(static_cast<unsigned>(sp), static_cast<unsigned>(rows)), b(kBlock);
+  k_rows_split_max<DT><<<g, b, 0, s>>>(x, L, sc, partial);
+  k_rows_split_cast<DT><<<g, b, 0, s>>>(x, L, sc, partial, eps, q, scale);
+  return launch_status(what);
+}
+
 template <int DT>
 int rows_quant_t(const void* x, int64_t rows, int64_t L, float eps, int8_t* q, float* scale,
-                 hipStream_t s, const char* what) {
+                 hipStream_t s, const char* what, void* ws = nullptr, size_t ws_bytes = 0) {
   CBQ_REQUIRE(rows <= 0x7fffffffLL, "%s: too many rows (%lld)", what, (long long)rows);
   const bool vec = (L % 8 == 0) && aligned(x, 16) && aligned(q, 8);
+  if (vec && ws && aligned(ws, 16)) {
+    // few long rows: slices of each row spread over the CUs
+    const int64_t sp = row_splits(rows, L);
+    if (sp > 1 && ws_bytes >= row_split_ws_bytes(rows, L))
+      return rows_split_quant_t<DT>(x, rows, L, sp, eps, ws, q, scale, s, what);
+  }
   if (vec) {
     switch (L) {
       case 8: launch_rows_sub<DT, 1, 1>(x, rows, eps, q, scale, s); return launch_status(what);
@@ -1329,11 +1540,11 @@ int rows_quant_t(const void* x, int64_t rows, int64_t L, float eps, int8_t* q, f
 }
 
 int rows_quant(const void* x, int dt, int64_t rows, int64_t L, float eps, int8_t* q, float* scale,
-               hipStream_t s, const char* what) {
+               hipStream_t s, const char* what, void* ws = nullptr, size_t ws_bytes = 0) {
   switch (dt) {
-    case kF16: return rows_quant_t<kF16>(x, rows, L, eps, q, scale, s, what);
-    case kBF16: return rows_quant_t<kBF16>(x, rows, L, eps, q, scale, s, what);
-    default: return rows_quant_t<kF32>(x, rows, L, eps, q, scale, s, what);
+    case kF16: return rows_quant_t<kF16>(x, rows, L, eps, q, scale, s, what, ws, ws_bytes);
+    case kBF16: return rows_quant_t<kBF16>(x, rows, L, eps, q, scale, s, what, ws, ws_bytes);
+    default: return rows_quant_t<kF32>(x, rows, L, eps, q, scale, s, what, ws, ws_bytes);
   }
 }
 
@@ -1391,7 +1602,14 @@ int cols_quant_t(const void* x, int64_t rows, int64_t cols, int64_t inner, float
   float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + CBQ_WS_CTRL_BYTES);
   float* inv = partial + g.nrb * cols;
   const dim3 grid2(static_cast<unsigned>(g.col_blocks), static_cast<unsigned>(g.nrb));
-  k_colmax<DT><<<grid2, dim3(kBlock), 0, s>>>(x, rows, cols, g.RB, vec ? 1 : 0, partial);
+  const int64_t u = cols >> 3;
+  const bool narrow = vec && u <= kBlock / 2;
+  const int rpi = narrow ? kBlock / static_cast<int>(u) : 1;
+  if (narrow)
+    k_colmax_narrow<DT><<<grid2, dim3(kBlock), 0, s>>>(x, rows, cols, g.RB, static_cast<int>(u),
+                                                       rpi, partial);
+  else
+    k_colmax<DT><<<grid2, dim3(kBlock), 0, s>>>(x, rows, cols, g.RB, vec ? 1 : 0, partial);
   if (inner == 1)
     if (cols % 4 == 0)
       k_col_finalize4<<<dim3(static_cast<unsigned>(cdiv(cols, kFin4Cols))), dim3(kBlock), 0, s>>>(
@@ -1403,6 +1621,14 @@ int cols_quant_t(const void* x, int64_t rows, int64_t cols, int64_t inner, float
     k_chan_finalize<<<dim3(static_cast<unsigned>(cols / inner)), dim3(kBlock), 0, s>>>(
         partial, g.nrb, cols, inner, eps, inv, scale);
   int64_t crb;
+  if (narrow) {
+    // kCastRB rows per thread, rpi threads per column chunk
+    crb = rpi * kCastRB;
+    if (cdiv(rows, crb) > 65535) crb = cdiv(cdiv(rows, 65535), rpi) * rpi;
+    k_cast_cols_narrow<DT><<<dim3(1, static_cast<unsigned>(cdiv(rows, crb))), dim3(kBlock), 0, s>>>(
+        x, rows, cols, crb, static_cast<int>(u), rpi, inv, inner, q);
+    return launch_status(what);
+  }
   const dim3 cgrid = cast_grid(rows, g.col_blocks, crb);
   k_cast_cols<DT><<<cgrid, dim3(kBlock), 0, s>>>(x, rows, cols, crb, vec ? 1 : 0, inv, inner, q);
   return launch_status(what);
@@ -1618,8 +1844,8 @@ extern "C" int cbq_quant_int8_tensor(const void* x, int dtype, int64_t n, float 
 extern "C" size_t cbq_quant_tensor_ws_bytes(void) { return tensor_ws_bytes(); }
 
 extern "C" size_t cbq_quant_int8_channel_ws_bytes(int64_t rows, int64_t cols, int axis) {
-  if (axis != 1 || rows <= 0 || cols <= 0) return CBQ_WS_CTRL_BYTES;
-  return col_ws_bytes(rows, cols);
+  if (rows <= 0 || cols <= 0) return CBQ_WS_CTRL_BYTES;
+  return axis == 1 ? col_ws_bytes(rows, cols) : row_split_ws_bytes(rows, cols);
 }
 
 extern "C" int cbq_quant_int8_channel(const void* x, int dtype, int64_t rows, int64_t cols,
@@ -1632,7 +1858,8 @@ extern "C" int cbq_quant_int8_channel(const void* x, int dtype, int64_t rows, in
   CBQ_REQUIRE(rows >= 0 && cols >= 0, "%s: negative shape", what);
   if (rows == 0 || cols == 0) return CBQ_OK;
   CBQ_REQUIRE(x && q && scale, "%s: null pointer", what);
-  if (axis == 0) return rows_quant(x, dtype, rows, cols, eps, q, scale, as_stream(stream), what);
+  if (axis == 0)
+    return rows_quant(x, dtype, rows, cols, eps, q, scale, as_stream(stream), what, ws, ws_bytes);
   const size_t need = col_ws_bytes(rows, cols);
   CBQ_REQUIRE(ws && ws_bytes >= need && aligned(ws, 16),
               "%s: axis 1 needs a 16-byte aligned workspace of %zu bytes, got %zu", what, need,
@@ -1646,7 +1873,8 @@ extern "C" int cbq_quant_int8_channel(const void* x, int dtype, int64_t rows, in
 
 extern "C" size_t cbq_quant_int8_channel_nd_ws_bytes(int64_t outer, int64_t channels,
                                                      int64_t inner) {
-  if (outer <= 1 || channels <= 0 || inner <= 0) return CBQ_WS_CTRL_BYTES;
+  if (outer <= 0 || channels <= 0 || inner <= 0) return CBQ_WS_CTRL_BYTES;
+  if (outer == 1) return row_split_ws_bytes(channels, inner);
   return channel_nd_ws_bytes(outer, channels, inner);
 }
 
@@ -1661,7 +1889,8 @@ extern "C" int cbq_quant_int8_channel_nd(const void* x, int dtype, int64_t outer
   if (outer == 0 || channels == 0 || inner == 0) return CBQ_OK;
   CBQ_REQUIRE(x && q && scale, "%s: null pointer", what);
   if (outer == 1)   // channel axis leading: one row per channel
-    return rows_quant(x, dtype, channels, inner, eps, q, scale, as_stream(stream), what);
+    return rows_quant(x, dtype, channels, inner, eps, q, scale, as_stream(stream), what, ws,
+                      ws_bytes);
   const size_t need = channel_nd_ws_bytes(outer, channels, inner);
   CBQ_REQUIRE(ws && ws_bytes >= need && aligned(ws, 16),
               "%s: needs a 16-byte aligned workspace of %zu bytes, got %zu", what, need, ws_bytes);

@@ -306,8 +306,29 @@ def test_rows_every_length(L, code):
         check_int8_group(x, code, L, what=f"group G={L}")
 
 
+# Few long rows (per-channel axis 0): each row is cut into slices spread over
+# the CUs and the slices' maxima combined; an outlier planted at a different
+# position of each row lands in different slices.
+@pytest.mark.parametrize("shape", [(1, 1 << 20), (4, 1 << 17), (5, 20000), (16, 16384),
+                                   (3, 3 * 65536 + 8), (300, 65544)])
+@pytest.mark.parametrize("code", [oracle.BF16, oracle.F16, oracle.F32])
+def test_rows_split(shape, code):
+    R, L = shape
+    x = rand_bits(shape, code, seed=R + L + code, rowfac=True)
+    v = oracle.to_f32(x.reshape(shape), code)
+    for r in range(R):
+        v[r, (r * 7919 * 8 + L - 1) % L] *= 30.0
+    x2 = oracle.from_f32(v, code).reshape(shape) if code != oracle.F32 else v
+    check_int8_channel(x2, code, 0, what=f"split rows {shape}")
+
+
 @pytest.mark.parametrize("shape", [(5, 8), (37, 29), (64, 2048), (1000, 24), (3, 16384),
-                                   (4097, 136), (300, 1)])
+                                   (4097, 136), (300, 1),
+                                   # narrow rows (cols / 8 <= 128 chunks): several rows
+                                   # per workgroup pass, 2 .. 32 threads per chunk
+                                   (20000, 64), (4096, 256), (3000, 1000), (50000, 8),
+                                   (7, 64), (10001, 24), (2048, 40), (1000, 1016),
+                                   (70000, 16)])
 @pytest.mark.parametrize("code", [oracle.BF16, oracle.F16, oracle.F32])
 def test_columns(shape, code):
     x = rand_bits(shape, code, seed=sum(shape) + code)
@@ -508,7 +529,11 @@ def test_config4_int8_group_full():
     # 512 .. 8192 chunks of 8 per channel: one workgroup per channel, held in
     # registers (1, 2, 3 -> 4, 14 -> 16 and 16 chunks per thread)
     ((2, 8, 2048), 1), ((2, 64, 4096), 1), ((3, 10, 2048), 1), ((2, 9, 3, 1600), 1),
-    ((7, 6, 8192), 1), ((16, 3, 4096), 1)])
+    ((7, 6, 8192), 1), ((16, 3, 4096), 1),
+    # leading axis with few long channels: rows cut into slices over the CUs
+    ((4, 64, 1024), 0), ((2, 3, 70000), 0),
+    # narrow [outer, C * inner] views: several rows per workgroup pass
+    ((64, 30, 64), 2), ((100, 4, 16), 1), ((3000, 2, 8), 1)])
 def test_channel_any_axis(code, shape, axis):
     from cublade_amd.quantization import dequantize_tensor, quantize_tensor
     x = rand_bits(shape, code, seed=sum(shape) + axis)

@@ -89,6 +89,15 @@ def test_workspace_sizes():
     from cublade_amd import _abi
     C = _abi.WS_CTRL_BYTES
     assert L.cbq_quant_int8_channel_ws_bytes(100, 100, 0) == C
+    # few long rows on axis 0: one partial maximum per slice of each row (no
+    # device here: 256 CUs assumed, 4 workgroups per CU, slices >= 8192
+    # elements, at most 256 per row)
+    assert L.cbq_quant_int8_channel_ws_bytes(64, 1 << 20, 0) == C + 4 * 64 * 16
+    assert L.cbq_quant_int8_channel_ws_bytes(8, 1 << 21, 0) == C + 4 * 8 * 128
+    assert L.cbq_quant_int8_channel_ws_bytes(256, 262144, 0) == C + 4 * 256 * 4
+    assert L.cbq_quant_int8_channel_ws_bytes(512, 65536, 0) == C     # enough rows
+    assert L.cbq_quant_int8_channel_ws_bytes(255, 8200, 0) == C      # rows too short
+    assert L.cbq_quant_int8_channel_nd_ws_bytes(1, 4, 65536) == C + 4 * 4 * 8
     assert L.cbq_quant_tensor_ws_bytes() == C + 4 * 2048
     big = L.cbq_quant_int8_channel_ws_bytes(28672, 8192, 1)
     assert big >= C + 8192 * 4 * 2 and big < 64 << 20
