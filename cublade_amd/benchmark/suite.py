@@ -10,7 +10,10 @@ every quant (x read once, codes and scales written), N + 4 * scales read +
 FLOPs (int8 GEMMs against the 5.0 POP/s dense int8 peak, the fp32-activation
 W8A16 against the 157.3 TFLOP/s fp32 peak).
 
-    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5,c5m,c5o,c5f32,f1,f3,f4,f4s [--json out.json]
+    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5,c5m,c5o,c5f32,f1,f3,fx,f4,f4s [--json out.json]
+
+fx is a set of shapes off the configs (odd group sizes, few long rows,
+narrow rows).
 """
 from __future__ import annotations
 
@@ -251,6 +254,31 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
         out.append(r)
         print(json.dumps(r), flush=True)
         del x
+    if "fx" in selected:
+        # Shapes off the configs, bf16 (random values; the bytes are the same
+        # 2N + N + 4 * scales / N + 2N + 4 * scales as above): group sizes
+        # that are not powers of two, rows of common LLM widths, few long
+        # rows and narrow rows per channel.
+        g = torch.Generator(device=dev).manual_seed(0)
+        shapes = [
+            ("_group56", (16384, 14336), dict(mode="group", group_size=56, ch_axis=1), 14336 // 56 * 16384),
+            ("_group112", (16384, 14336), dict(mode="group", group_size=112, ch_axis=1),
+             14336 // 112 * 16384),
+            ("_channel_axis0_rows11008", (4096, 11008), dict(mode="channel", ch_axis=0), 4096),
+            ("_channel_axis0_3d_64x1024x1024", (64, 1024, 1024), dict(mode="channel", ch_axis=0),
+             64),
+            ("_channel_axis0_256x262144", (256, 262144), dict(mode="channel", ch_axis=0), 256),
+            ("_channel_axis1_262144x64", (262144, 64), dict(mode="channel", ch_axis=1), 64),
+            ("_channel_axis1_16384x1000", (16384, 1000), dict(mode="channel", ch_axis=1), 1000),
+            ("_channel_axis2_3d_256x512x512", (256, 512, 512), dict(mode="channel", ch_axis=2),
+             512),
+        ]
+        for tag, shape, kw, nsc in shapes:
+            x = torch.randn(*shape, device=dev, generator=g).bfloat16()
+            n = x.numel()
+            q_and_dq("fx", x, dict(dtype=torch.int8, **kw), 2 * n + n + 4 * nsc,
+                     n + 2 * n + 4 * nsc, tag)
+            del x
     if "f4" in selected:
         # Dense GEMM (wmma_gemm's replacement) at 8192^3: int8 -> int32 with B
         # as an [N, K] weight (read in place) and as [K, N] (transposed into
@@ -314,7 +342,7 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,c5m,c5o,c5f32,f1,f3,f4,f4s")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,c5m,c5o,c5f32,f1,f3,fx,f4,f4s")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--json", default=None)
