@@ -322,6 +322,33 @@ def test_rows_split(shape, code):
     check_int8_channel(x2, code, 0, what=f"split rows {shape}")
 
 
+def test_rows_split_needs_its_workspace():
+    """Through the C ABI: with only the control block as workspace the
+    few-long-rows call takes the one-workgroup-per-row path, with the
+    workspace its size query names it takes the split path; both give the
+    oracle's codes and scales."""
+    from cublade_amd import _abi
+    L = _abi.lib()
+    R, Lr = 4, 1 << 17
+    code = oracle.BF16
+    x = rand_bits((R, Lr), code, seed=77, rowfac=True)
+    xt = from_bits(x.reshape(-1), code, DEV)
+    qo, so = oracle.quant_int8_channel(x.reshape(R, Lr), code, axis=0)
+    need = L.cbq_quant_int8_channel_ws_bytes(R, Lr, 0)
+    assert need > _abi.WS_CTRL_BYTES
+    h = torch.cuda.current_stream().cuda_stream
+    for nbytes in (_abi.WS_CTRL_BYTES, need):
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
+        q = torch.empty(R * Lr, dtype=torch.int8, device=DEV)
+        sc = torch.empty(R, dtype=torch.float32, device=DEV)
+        rc = L.cbq_quant_int8_channel(xt.data_ptr(), code, R, Lr, 0, 1e-12, ws.data_ptr(),
+                                      ws.numel(), q.data_ptr(), sc.data_ptr(), h)
+        assert rc == 0, L.cbq_last_error()
+        torch.cuda.synchronize()
+        assert_array_equal(bits(q).reshape(R, Lr), qo, f"ws {nbytes} q")
+        assert_scales_equal(bits(sc), so, f"ws {nbytes}")
+
+
 @pytest.mark.parametrize("shape", [(5, 8), (37, 29), (64, 2048), (1000, 24), (3, 16384),
                                    (4097, 136), (300, 1),
                                    # narrow rows (cols / 8 <= 128 chunks): several rows
@@ -533,7 +560,7 @@ def test_config4_int8_group_full():
     # leading axis with few long channels: rows cut into slices over the CUs
     ((4, 64, 1024), 0), ((2, 3, 70000), 0),
     # narrow [outer, C * inner] views: several rows per workgroup pass
-    ((64, 30, 64), 2), ((100, 4, 16), 1), ((3000, 2, 8), 1)])
+    ((64, 30, 64), 2), ((100, 4, 16), 1), ((3000, 2, 8), 1), ((500, 8, 3), 1)])
 def test_channel_any_axis(code, shape, axis):
     from cublade_amd.quantization import dequantize_tensor, quantize_tensor
     x = rand_bits(shape, code, seed=sum(shape) + axis)
