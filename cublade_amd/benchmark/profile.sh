@@ -131,6 +131,18 @@ if want suite; then
     echo "# 1024 / 2048 / 3072) and the dense GEMM (f4, 8192^3)"
     echo "# command: rocprofv3 --pmc MfmaUtil --kernel-trace -d RAW/mfma -o suite -- python -u -m cublade_amd.benchmark.suite --configs c5,c5m,f4 --reps 3 --warmup 1"
     $R counters "$RAW/mfma/suite_results.db" | grep -E "k_gemm_dma|k_stream|k_skinny|k_gemm<|k_mm_dma|Cijk"
+    echo
+    echo "# dispatches by W8A16 shape (N = 11008, K = 4096, config-5 operands; order: c5 then c5m):"
+    echo "#   M = 16    k_stream1<1, 3>                 (weight streaming, HBM-bound)"
+    echo "#   M = 256   k_gemm_dma<1, true, 2, false>   (128-row tiles, K in 2 ranges, 172 of 256 CUs)"
+    echo "#   M = 768   k_gemm_dma<1, false, 3, false>  first 4 values (172 tiles of 192 rows, one wave)"
+    echo "#   M = 1536  k_gemm_dma<1, true, 4, false>   first 4 values (256 tiles whole + 2 over 16 ranges)"
+    echo "#   M = 4096  k_gemm_dma<1, false, 4, false>  first 4 values (688 tiles, 2.69 waves)"
+    echo "#   M = 1024  k_gemm_dma<1, false, 4, false>  last 4 values (172 tiles of 256 rows, one wave)"
+    echo "#   M = 2048  k_gemm_dma<1, false, 3, false>  last 4 values (473 tiles of 192 rows)"
+    echo "#   M = 3072  k_gemm_dma<1, true, 4, false>   last 4 values (512 tiles whole + the tail split)"
+    echo "# dense GEMM (f4): k_mm_dma<0, 0, ...> int8 (B [N, K] read in place, then [K, N]), k_mm_dma<1, 1, ...>"
+    echo "# fp16 -> fp32; Cijk_* are hipBLASLt's kernels for torch._int_mm and torch.matmul on the same shapes"
   } > "$OUT/mfma_util.txt" || exit $?
 fi
 if want ceil; then
