@@ -70,7 +70,9 @@ int cbq_abi_version(void);
 size_t cbq_quant_tensor_ws_bytes(void);
 
 /* Workspace bytes needed by cbq_quant_int8_channel (axis 1 needs per-column
- * partial maxima; axis 0 needs only the control block). */
+ * partial maxima; axis 0 needs only the control block, except for few long
+ * rows, cut into slices over the CUs with one partial maximum per slice: with
+ * a smaller workspace those take the one-workgroup-per-row path). */
 size_t cbq_quant_int8_channel_ws_bytes(int64_t rows, int64_t cols, int axis);
 
 /* ---- FP8 E4M3 per tensor ------------------------------------------------ */
@@ -137,7 +139,9 @@ int cbq_quant_int8_group(const void* x, int dtype, int64_t num_groups,
  * before/after it); one fp32 scale per channel. The reference only supports
  * the leading axis (quantizers.py:116-121, quantize_int8.cu:487-509); this is
  * the same math with the channel maximum taken over outer and inner, and no
- * copies. outer == 1 runs the row kernels (no workspace). Otherwise the
+ * copies. outer == 1 runs the row kernels (the control block only, or the
+ * slices' partial maxima for few long rows, as cbq_quant_int8_channel axis 0).
+ * Otherwise the
  * workspace below holds, for inner >= 512, [outer, channels] segment maxima
  * plus [channels] multipliers; for shorter inner, the column path's partial
  * maxima over outer x (channels * inner). */
