@@ -322,6 +322,29 @@ def test_rows_split(shape, code):
     check_int8_channel(x2, code, 0, what=f"split rows {shape}")
 
 
+@pytest.mark.parametrize("shape,axis", [((6, 1 << 17), 0), ((40000, 64), 1)])
+def test_split_and_narrow_special_values(shape, axis):
+    """NaN, +-inf, all-zero and subnormal rows / columns through the split-row
+    path (few long rows, axis 0) and the narrow-column path (axis 1),
+    bit-exact against the oracle for codes, scales and the dequant."""
+    v = torch.randn(*shape, generator=torch.Generator().manual_seed(12)).bfloat16()
+    if axis == 0:
+        v[0, 70000] = float("nan")          # one NaN in a late slice
+        v[1, 5] = float("inf")
+        v[1, 130000] = -float("inf")
+        v[2, :] = 0.0
+        v[3, :] = 1e-39                      # bf16 subnormal
+        v[4, 100000:] = float("nan")         # a whole slice of NaN
+    else:
+        v[7, 3] = float("nan")
+        v[30000, 9] = float("inf")
+        v[39999, 9] = -float("inf")
+        v[:, 20] = 0.0
+        v[:, 21] = 1e-39
+        v[:20000, 40] = float("nan")
+    check_int8_channel(bits(v), oracle.BF16, axis, what=f"special {shape} axis {axis}")
+
+
 def test_rows_split_needs_its_workspace():
     """Through the C ABI: with only the control block as workspace the
     few-long-rows call takes the one-workgroup-per-row path, with the
