@@ -12,7 +12,9 @@
 //                    fixed-shape kernel: k_deq_rows_sub's layout, masked slots
 //   k_deq_rows_wg    one workgroup per row of any longer length that is a
 //                    multiple of 8 (long per-channel rows)
-//   k_deq_rows_scalar any row length, element at a time
+//   k_deq_rows_sub_any1 rows of up to 2048 codes that 8-byte loads cannot
+//                    take: k_deq_rows_sub's layout with code loads
+//   k_deq_rows_scalar any longer such row, element at a time
 //   k_deq_cols       per-column scales (axis 1), and per-channel scales of an
 //                    N-D tensor seen as [outer, channels * inner]: each thread
 //                    keeps the scales of its eight columns in registers while
@@ -245,6 +247,40 @@ __global__ __launch_bounds__(kBlock) void k_deq_rows_scalar(
     const int64_t base = row * L;
     for (int64_t i = threadIdx.x; i < L; i += kBlock)
       st1<OUT>(y, base + i, static_cast<float>(q[base + i]) * s);
+  }
+}
+
+// Rows of any length L <= 2048 that 8-byte code loads cannot take (L % 8 !=
+// 0, e.g. groups of 100, or unaligned buffers): LPR lanes per row, VPL codes
+// per lane, code j = v * LPR + lr, loads and stores contiguous across the
+// lanes of a row.
+template <int OUT, int LPR, int VPL, int RI>
+__global__ __launch_bounds__(kBlock) void k_deq_rows_sub_any1(
+    const int8_t* __restrict__ q, const float* __restrict__ scale, int64_t rows, int L,
+    void* __restrict__ y) {
+  constexpr int RPW = kWave / LPR;
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int sub = lane / LPR;
+  const int lr = lane % LPR;
+  const int64_t row0 =
+      (static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + wave) * (RI * RPW) + sub;
+#pragma unroll
+  for (int it = 0; it < RI; ++it) {
+    const int64_t row = row0 + static_cast<int64_t>(it) * RPW;
+    if (row >= rows) continue;
+    const float s = scale[row];
+    int8_t c[VPL];
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      const int j = v * LPR + lr;
+      c[v] = q[row * L + (j < L ? j : 0)];
+    }
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      const int j = v * LPR + lr;
+      if (j < L) st1<OUT>(y, row * L + j, static_cast<float>(c[v]) * s);
+    }
   }
 }
 
@@ -506,6 +542,32 @@ void deq_rows_any(const int8_t* q, const float* scale, int64_t rows, int cg, voi
   else launch_deq_rows_sub_any<OUT, 64, 8>(q, scale, rows, cg, y, s);
 }
 
+template <int OUT, int LPR, int VPL>
+void launch_deq_rows_sub_any1(const int8_t* q, const float* scale, int64_t rows, int L, void* y,
+                              hipStream_t s) {
+  constexpr int RI = VPL >= 16 ? 1 : 2;
+  constexpr int64_t rows_per_wg = static_cast<int64_t>(kBlock / kWave) * RI * (kWave / LPR);
+  k_deq_rows_sub_any1<OUT, LPR, VPL, RI><<<dim3(static_cast<unsigned>(cdiv(rows, rows_per_wg))),
+                                           dim3(kBlock), 0, s>>>(q, scale, rows, L, y);
+}
+
+template <int OUT>
+void deq_rows_any1(const int8_t* q, const float* scale, int64_t rows, int L, void* y,
+                   hipStream_t s) {
+  if (L <= 1) launch_deq_rows_sub_any1<OUT, 1, 1>(q, scale, rows, L, y, s);
+  else if (L <= 2) launch_deq_rows_sub_any1<OUT, 2, 1>(q, scale, rows, L, y, s);
+  else if (L <= 4) launch_deq_rows_sub_any1<OUT, 4, 1>(q, scale, rows, L, y, s);
+  else if (L <= 8) launch_deq_rows_sub_any1<OUT, 8, 1>(q, scale, rows, L, y, s);
+  else if (L <= 16) launch_deq_rows_sub_any1<OUT, 16, 1>(q, scale, rows, L, y, s);
+  else if (L <= 32) launch_deq_rows_sub_any1<OUT, 32, 1>(q, scale, rows, L, y, s);
+  else if (L <= 64) launch_deq_rows_sub_any1<OUT, 64, 1>(q, scale, rows, L, y, s);
+  else if (L <= 128) launch_deq_rows_sub_any1<OUT, 64, 2>(q, scale, rows, L, y, s);
+  else if (L <= 256) launch_deq_rows_sub_any1<OUT, 64, 4>(q, scale, rows, L, y, s);
+  else if (L <= 512) launch_deq_rows_sub_any1<OUT, 64, 8>(q, scale, rows, L, y, s);
+  else if (L <= 1024) launch_deq_rows_sub_any1<OUT, 64, 16>(q, scale, rows, L, y, s);
+  else launch_deq_rows_sub_any1<OUT, 64, 32>(q, scale, rows, L, y, s);
+}
+
 template <int OUT>
 int deq_rows_t(const int8_t* q, const float* scale, int64_t rows, int64_t L, void* y,
                hipStream_t s, const char* what) {
@@ -541,6 +603,10 @@ int deq_rows_t(const int8_t* q, const float* scale, int64_t rows, int64_t L, voi
         }
         return launch_status(what);
     }
+  }
+  if (L <= 2048) {
+    deq_rows_any1<OUT>(q, scale, rows, static_cast<int>(L), y, s);
+    return launch_status(what);
   }
   k_deq_rows_scalar<OUT><<<dim3(rows_grid(rows)), dim3(kBlock), 0, s>>>(q, scale, rows, L, y);
   return launch_status(what);

@@ -29,6 +29,8 @@
 //   k_rows_sub_any  rows / groups of any multiple of 8 below 4096 elements
 //                   without a fixed-shape kernel (k_rows_sub's layout with
 //                   masked chunk slots)
+//   k_rows_sub_any1 the same layout with element loads, for rows / groups of
+//                   up to 2048 elements that 16-byte loads cannot take
 //   k_rows_generic  row lengths no kernel above takes (two passes over the
 //                   row; the second read hits L2); aligned rows of 512 to
 //                   8192 chunks of 8 elements take k_chan_wg (below) instead
@@ -570,6 +572,58 @@ __global__ __launch_bounds__(kBlock) void k_rows_sub_any(
       for (int v = 0; v < VPL; ++v) {
         const int j = v * LPR + lr;
         if (j < cg) stg8(q + row * L + j * 8, pack8_int8(f[v], inv));
+      }
+      if (lr == 0) scale[row] = 1.0f / inv;
+    }
+  }
+}
+
+// Rows (groups) of any length L <= 2048 that 16-byte loads cannot take (L %
+// 8 != 0, e.g. groups of 100, or unaligned buffers): LPR lanes per row, VPL
+// elements per lane, element j = v * LPR + lr, 2- or 4-byte loads that are
+// contiguous across the lanes of a row. Slots past L load the row's first
+// element, stay out of the maximum and store nothing.
+template <int DT, int LPR, int VPL, int RI>
+__global__ __launch_bounds__(kBlock) void k_rows_sub_any1(
+    const void* __restrict__ x, int64_t rows, int L, float eps, int8_t* __restrict__ q,
+    float* __restrict__ scale) {
+  constexpr int RPW = kWave / LPR;
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int sub = lane / LPR;
+  const int lr = lane % LPR;
+  const int64_t row0 =
+      (static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + wave) * (RI * RPW) + sub;
+
+  float f[RI][VPL];
+#pragma unroll
+  for (int it = 0; it < RI; ++it) {
+    const int64_t row = row0 + static_cast<int64_t>(it) * RPW;
+    if (row < rows) {
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const int j = v * LPR + lr;
+        f[it][v] = ld1<DT>(x, row * L + (j < L ? j : 0));
+      }
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < RI; ++it) {
+    const int64_t row = row0 + static_cast<int64_t>(it) * RPW;
+    const bool ok = row < rows;
+    float m = 0.0f;
+    if (ok) {
+#pragma unroll
+      for (int v = 0; v < VPL; ++v)
+        m = v * LPR + lr < L ? fmaxf(m, __builtin_fabsf(f[it][v])) : m;
+    }
+    m = group_max<LPR>(m);   // every lane participates
+    const float inv = inv_scale(m, eps, kQmaxInt8);
+    if (ok) {
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const int j = v * LPR + lr;
+        if (j < L) q[row * L + j] = static_cast<int8_t>(q_int8(f[it][v] * inv));
       }
       if (lr == 0) scale[row] = 1.0f / inv;
     }
@@ -1454,6 +1508,34 @@ void rows_quant_any(const void* x, int64_t rows, int cg, float eps, int8_t* q, f
   else launch_rows_sub_any<DT, 64, 8>(x, rows, cg, eps, q, scale, s);
 }
 
+template <int DT, int LPR, int VPL>
+void launch_rows_sub_any1(const void* x, int64_t rows, int L, float eps, int8_t* q, float* scale,
+                          hipStream_t s) {
+  constexpr int RI = VPL >= 16 ? 1 : 2;
+  constexpr int64_t rows_per_wg = static_cast<int64_t>(kBlock / kWave) * RI * (kWave / LPR);
+  k_rows_sub_any1<DT, LPR, VPL, RI><<<dim3(static_cast<unsigned>(cdiv(rows, rows_per_wg))),
+                                      dim3(kBlock), 0, s>>>(x, rows, L, eps, q, scale);
+}
+
+constexpr int kRowsAny1Max = 2048;
+
+template <int DT>
+void rows_quant_any1(const void* x, int64_t rows, int L, float eps, int8_t* q, float* scale,
+                     hipStream_t s) {
+  if (L <= 1) launch_rows_sub_any1<DT, 1, 1>(x, rows, L, eps, q, scale, s);
+  else if (L <= 2) launch_rows_sub_any1<DT, 2, 1>(x, rows, L, eps, q, scale, s);
+  else if (L <= 4) launch_rows_sub_any1<DT, 4, 1>(x, rows, L, eps, q, scale, s);
+  else if (L <= 8) launch_rows_sub_any1<DT, 8, 1>(x, rows, L, eps, q, scale, s);
+  else if (L <= 16) launch_rows_sub_any1<DT, 16, 1>(x, rows, L, eps, q, scale, s);
+  else if (L <= 32) launch_rows_sub_any1<DT, 32, 1>(x, rows, L, eps, q, scale, s);
+  else if (L <= 64) launch_rows_sub_any1<DT, 64, 1>(x, rows, L, eps, q, scale, s);
+  else if (L <= 128) launch_rows_sub_any1<DT, 64, 2>(x, rows, L, eps, q, scale, s);
+  else if (L <= 256) launch_rows_sub_any1<DT, 64, 4>(x, rows, L, eps, q, scale, s);
+  else if (L <= 512) launch_rows_sub_any1<DT, 64, 8>(x, rows, L, eps, q, scale, s);
+  else if (L <= 1024) launch_rows_sub_any1<DT, 64, 16>(x, rows, L, eps, q, scale, s);
+  else launch_rows_sub_any1<DT, 64, 32>(x, rows, L, eps, q, scale, s);
+}
+
 // Slices per row for the split-row path: enough workgroups for about four
 // per CU, each slice at least kSplitMinChunks chunks; 1 (no split) when the
 // one-workgroup-per-row kernels have enough rows. The split reads x twice,
@@ -1533,6 +1615,10 @@ int rows_quant_t(const void* x, int64_t rows, int64_t L, float eps, int8_t* q, f
     }
     if (chan_wg_applies(x, q, 1, L))
       return chan_wg_quant_t<DT>(x, 1, rows, L, eps, q, scale, s, what);
+  } else if (L <= kRowsAny1Max) {
+    // no 16-byte loads: several rows per wave with element loads
+    rows_quant_any1<DT>(x, rows, static_cast<int>(L), eps, q, scale, s);
+    return launch_status(what);
   }
   k_rows_generic<DT><<<dim3(wg_rows_grid(rows)), dim3(kBlock), 0, s>>>(
       x, rows, L, vec ? 1 : 0, eps, q, scale);

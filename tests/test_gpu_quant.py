@@ -293,7 +293,8 @@ ROW_LENGTHS = [8, 16, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192, 16384,   # 
                24, 40, 56, 96, 112, 136, 224, 448, 896, 1000, 1792, 2040, 2056,  # masked slots
                3000, 3584,
                4104, 5120, 11008, 14336, 28672, 65536,                           # one workgroup
-               1, 3, 7, 3004, 65544]                                             # generic
+               1, 3, 7, 33, 100, 129, 1001, 2047,                                # element loads
+               3004, 65544]                                                      # generic
 
 
 @pytest.mark.parametrize("L", ROW_LENGTHS)
@@ -413,6 +414,11 @@ def test_unaligned_views(offset):
     q, s = hip().quantize_per_group_int8(xt2, L)
     qo, so = oracle.quant_int8_group(x2, code, L)
     assert_array_equal(bits(q), qo, "unaligned group")
+    qb = torch.zeros(rows * L + offset, dtype=torch.int8, device=DEV)
+    qb[offset:].copy_(q.reshape(-1))
+    y = hip().dequantize_per_group_int8(qb[offset:].view(rows, L), s, L, torch.bfloat16)
+    assert_bits_equal_16(bits(y), oracle.dequant_int8_group(qo, so, L, oracle.BF16),
+                         oracle.BF16, "unaligned group dequant")
     q, s = hip().quantize_per_channel_int8(xt2, axis=1)
     qo, so = oracle.quant_int8_channel(x2, code, axis=1)
     assert_array_equal(bits(q), qo, "unaligned cols")
