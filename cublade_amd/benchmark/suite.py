@@ -264,6 +264,8 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
             ("_group56", (16384, 14336), dict(mode="group", group_size=56, ch_axis=1), 14336 // 56 * 16384),
             ("_group112", (16384, 14336), dict(mode="group", group_size=112, ch_axis=1),
              14336 // 112 * 16384),
+            ("_group100", (16384, 14300), dict(mode="group", group_size=100, ch_axis=1),
+             14300 // 100 * 16384),
             ("_channel_axis0_rows11008", (4096, 11008), dict(mode="channel", ch_axis=0), 4096),
             ("_channel_axis0_3d_64x1024x1024", (64, 1024, 1024), dict(mode="channel", ch_axis=0),
              64),
