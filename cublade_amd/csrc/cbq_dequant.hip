@@ -254,15 +254,19 @@ __global__ __launch_bounds__(kBlock) void k_deq_rows_scalar(
 // 0, e.g. groups of 100, or unaligned buffers): LPR lanes per row, VPL codes
 // per lane, code j = v * LPR + lr, loads and stores contiguous across the
 // lanes of a row.
-template <int OUT, int LPR, int VPL, int RI>
+template <int OUT, int LPR, int VPL, int RI, int E>
 __global__ __launch_bounds__(kBlock) void k_deq_rows_sub_any1(
     const int8_t* __restrict__ q, const float* __restrict__ scale, int64_t rows, int L,
     void* __restrict__ y) {
+  // E = 2: code pairs (L even, q and y aligned to a pair): one 2-byte load
+  // and one 4-byte store per pair
+  static_assert(E == 1 || E == 2, "codes per load");
   constexpr int RPW = kWave / LPR;
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
   const int sub = lane / LPR;
   const int lr = lane % LPR;
+  const int U = L / E;
   const int64_t row0 =
       (static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + wave) * (RI * RPW) + sub;
 #pragma unroll
@@ -270,16 +274,28 @@ __global__ __launch_bounds__(kBlock) void k_deq_rows_sub_any1(
     const int64_t row = row0 + static_cast<int64_t>(it) * RPW;
     if (row >= rows) continue;
     const float s = scale[row];
-    int8_t c[VPL];
+    uint32_t c[VPL];
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
       const int j = v * LPR + lr;
-      c[v] = q[row * L + (j < L ? j : 0)];
+      const int64_t e = row * L + static_cast<int64_t>(j < U ? j : 0) * E;
+      if constexpr (E == 1) c[v] = static_cast<uint8_t>(q[e]);
+      else c[v] = *reinterpret_cast<const uint16_t*>(q + e);
     }
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
       const int j = v * LPR + lr;
-      if (j < L) st1<OUT>(y, row * L + j, static_cast<float>(c[v]) * s);
+      if (j >= U) continue;
+      const int64_t e = row * L + static_cast<int64_t>(j) * E;
+      const float a = static_cast<float>(static_cast<int8_t>(c[v] & 0xffu)) * s;
+      if constexpr (E == 1) {
+        st1<OUT>(y, e, a);
+      } else {
+        float b = static_cast<float>(static_cast<int8_t>((c[v] >> 8) & 0xffu)) * s;
+        float a2 = a;
+        asm volatile("" : "+v"(a2), "+v"(b));   // finished fp32 products, as in out1
+        *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(y) + e) = pack2_out<OUT>(a2, b);
+      }
     }
   }
 }
@@ -542,30 +558,42 @@ void deq_rows_any(const int8_t* q, const float* scale, int64_t rows, int cg, voi
   else launch_deq_rows_sub_any<OUT, 64, 8>(q, scale, rows, cg, y, s);
 }
 
-template <int OUT, int LPR, int VPL>
+template <int OUT, int LPR, int VPL, int E>
 void launch_deq_rows_sub_any1(const int8_t* q, const float* scale, int64_t rows, int L, void* y,
                               hipStream_t s) {
   constexpr int RI = VPL >= 16 ? 1 : 2;
   constexpr int64_t rows_per_wg = static_cast<int64_t>(kBlock / kWave) * RI * (kWave / LPR);
-  k_deq_rows_sub_any1<OUT, LPR, VPL, RI><<<dim3(static_cast<unsigned>(cdiv(rows, rows_per_wg))),
-                                           dim3(kBlock), 0, s>>>(q, scale, rows, L, y);
+  k_deq_rows_sub_any1<OUT, LPR, VPL, RI, E>
+      <<<dim3(static_cast<unsigned>(cdiv(rows, rows_per_wg))), dim3(kBlock), 0, s>>>(q, scale,
+                                                                                     rows, L, y);
+}
+
+template <int OUT, int E>
+void deq_rows_any1_e(const int8_t* q, const float* scale, int64_t rows, int L, void* y,
+                     hipStream_t s) {
+  const int U = L / E;
+  if (U <= 1) launch_deq_rows_sub_any1<OUT, 1, 1, E>(q, scale, rows, L, y, s);
+  else if (U <= 2) launch_deq_rows_sub_any1<OUT, 2, 1, E>(q, scale, rows, L, y, s);
+  else if (U <= 4) launch_deq_rows_sub_any1<OUT, 4, 1, E>(q, scale, rows, L, y, s);
+  else if (U <= 8) launch_deq_rows_sub_any1<OUT, 8, 1, E>(q, scale, rows, L, y, s);
+  else if (U <= 16) launch_deq_rows_sub_any1<OUT, 16, 1, E>(q, scale, rows, L, y, s);
+  else if (U <= 32) launch_deq_rows_sub_any1<OUT, 32, 1, E>(q, scale, rows, L, y, s);
+  else if (U <= 64) launch_deq_rows_sub_any1<OUT, 64, 1, E>(q, scale, rows, L, y, s);
+  else if (U <= 128) launch_deq_rows_sub_any1<OUT, 64, 2, E>(q, scale, rows, L, y, s);
+  else if (U <= 256) launch_deq_rows_sub_any1<OUT, 64, 4, E>(q, scale, rows, L, y, s);
+  else if (U <= 512) launch_deq_rows_sub_any1<OUT, 64, 8, E>(q, scale, rows, L, y, s);
+  else launch_deq_rows_sub_any1<OUT, 64, 16, E>(q, scale, rows, L, y, s);
 }
 
 template <int OUT>
 void deq_rows_any1(const int8_t* q, const float* scale, int64_t rows, int L, void* y,
                    hipStream_t s) {
-  if (L <= 1) launch_deq_rows_sub_any1<OUT, 1, 1>(q, scale, rows, L, y, s);
-  else if (L <= 2) launch_deq_rows_sub_any1<OUT, 2, 1>(q, scale, rows, L, y, s);
-  else if (L <= 4) launch_deq_rows_sub_any1<OUT, 4, 1>(q, scale, rows, L, y, s);
-  else if (L <= 8) launch_deq_rows_sub_any1<OUT, 8, 1>(q, scale, rows, L, y, s);
-  else if (L <= 16) launch_deq_rows_sub_any1<OUT, 16, 1>(q, scale, rows, L, y, s);
-  else if (L <= 32) launch_deq_rows_sub_any1<OUT, 32, 1>(q, scale, rows, L, y, s);
-  else if (L <= 64) launch_deq_rows_sub_any1<OUT, 64, 1>(q, scale, rows, L, y, s);
-  else if (L <= 128) launch_deq_rows_sub_any1<OUT, 64, 2>(q, scale, rows, L, y, s);
-  else if (L <= 256) launch_deq_rows_sub_any1<OUT, 64, 4>(q, scale, rows, L, y, s);
-  else if (L <= 512) launch_deq_rows_sub_any1<OUT, 64, 8>(q, scale, rows, L, y, s);
-  else if (L <= 1024) launch_deq_rows_sub_any1<OUT, 64, 16>(q, scale, rows, L, y, s);
-  else launch_deq_rows_sub_any1<OUT, 64, 32>(q, scale, rows, L, y, s);
+  if (L % 2 == 0 && aligned(q, 2) && aligned(y, 4))
+    deq_rows_any1_e<OUT, 2>(q, scale, rows, L, y, s);
+  else if (L <= 1024)
+    deq_rows_any1_e<OUT, 1>(q, scale, rows, L, y, s);
+  else
+    launch_deq_rows_sub_any1<OUT, 64, 32, 1>(q, scale, rows, L, y, s);
 }
 
 template <int OUT>

@@ -583,19 +583,23 @@ __global__ __launch_bounds__(kBlock) void k_rows_sub_any(
 // elements per lane, element j = v * LPR + lr, 2- or 4-byte loads that are
 // contiguous across the lanes of a row. Slots past L load the row's first
 // element, stay out of the maximum and store nothing.
-template <int DT, int LPR, int VPL, int RI>
+template <int DT, int LPR, int VPL, int RI, int E>
 __global__ __launch_bounds__(kBlock) void k_rows_sub_any1(
     const void* __restrict__ x, int64_t rows, int L, float eps, int8_t* __restrict__ q,
     float* __restrict__ scale) {
+  // E = 2: element pairs (L even, x and q aligned to a pair) in one load and
+  // one 2-byte code store
+  static_assert(E == 1 || E == 2, "elements per load");
   constexpr int RPW = kWave / LPR;
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
   const int sub = lane / LPR;
   const int lr = lane % LPR;
+  const int U = L / E;   // load units per row
   const int64_t row0 =
       (static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + wave) * (RI * RPW) + sub;
 
-  float f[RI][VPL];
+  float f[RI][VPL][E];
 #pragma unroll
   for (int it = 0; it < RI; ++it) {
     const int64_t row = row0 + static_cast<int64_t>(it) * RPW;
@@ -603,7 +607,23 @@ __global__ __launch_bounds__(kBlock) void k_rows_sub_any1(
 #pragma unroll
       for (int v = 0; v < VPL; ++v) {
         const int j = v * LPR + lr;
-        f[it][v] = ld1<DT>(x, row * L + (j < L ? j : 0));
+        const int64_t e = row * L + static_cast<int64_t>(j < U ? j : 0) * E;
+        if constexpr (E == 1) {
+          f[it][v][0] = ld1<DT>(x, e);
+        } else if constexpr (DT == kF32) {
+          const float2 w = *reinterpret_cast<const float2*>(static_cast<const float*>(x) + e);
+          f[it][v][0] = w.x;
+          f[it][v][1] = w.y;
+        } else {
+          const uint32_t w = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(x) + e);
+          if constexpr (DT == kBF16) {
+            f[it][v][0] = __uint_as_float(w << 16);
+            f[it][v][1] = __uint_as_float(w & 0xffff0000u);
+          } else {
+            f[it][v][0] = static_cast<float>(__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu)));
+            f[it][v][1] = static_cast<float>(__builtin_bit_cast(_Float16, (uint16_t)(w >> 16)));
+          }
+        }
       }
     }
   }
@@ -614,8 +634,11 @@ __global__ __launch_bounds__(kBlock) void k_rows_sub_any1(
     float m = 0.0f;
     if (ok) {
 #pragma unroll
-      for (int v = 0; v < VPL; ++v)
-        m = v * LPR + lr < L ? fmaxf(m, __builtin_fabsf(f[it][v])) : m;
+      for (int v = 0; v < VPL; ++v) {
+        float mv = __builtin_fabsf(f[it][v][0]);
+        if constexpr (E == 2) mv = fmaxf(mv, __builtin_fabsf(f[it][v][1]));
+        m = v * LPR + lr < U ? fmaxf(m, mv) : m;
+      }
     }
     m = group_max<LPR>(m);   // every lane participates
     const float inv = inv_scale(m, eps, kQmaxInt8);
@@ -623,7 +646,16 @@ __global__ __launch_bounds__(kBlock) void k_rows_sub_any1(
 #pragma unroll
       for (int v = 0; v < VPL; ++v) {
         const int j = v * LPR + lr;
-        if (j < L) q[row * L + j] = static_cast<int8_t>(q_int8(f[it][v] * inv));
+        if (j < U) {
+          if constexpr (E == 1) {
+            q[row * L + j] = static_cast<int8_t>(q_int8(f[it][v][0] * inv));
+          } else {
+            const uint32_t c0 = static_cast<uint8_t>(q_int8(f[it][v][0] * inv));
+            const uint32_t c1 = static_cast<uint8_t>(q_int8(f[it][v][1] * inv));
+            *reinterpret_cast<uint16_t*>(q + row * L + static_cast<int64_t>(j) * 2) =
+                static_cast<uint16_t>(c0 | (c1 << 8));
+          }
+        }
       }
       if (lr == 0) scale[row] = 1.0f / inv;
     }
@@ -1508,32 +1540,44 @@ void rows_quant_any(const void* x, int64_t rows, int cg, float eps, int8_t* q, f
   else launch_rows_sub_any<DT, 64, 8>(x, rows, cg, eps, q, scale, s);
 }
 
-template <int DT, int LPR, int VPL>
+template <int DT, int LPR, int VPL, int E>
 void launch_rows_sub_any1(const void* x, int64_t rows, int L, float eps, int8_t* q, float* scale,
                           hipStream_t s) {
   constexpr int RI = VPL >= 16 ? 1 : 2;
   constexpr int64_t rows_per_wg = static_cast<int64_t>(kBlock / kWave) * RI * (kWave / LPR);
-  k_rows_sub_any1<DT, LPR, VPL, RI><<<dim3(static_cast<unsigned>(cdiv(rows, rows_per_wg))),
-                                      dim3(kBlock), 0, s>>>(x, rows, L, eps, q, scale);
+  k_rows_sub_any1<DT, LPR, VPL, RI, E><<<dim3(static_cast<unsigned>(cdiv(rows, rows_per_wg))),
+                                         dim3(kBlock), 0, s>>>(x, rows, L, eps, q, scale);
 }
 
 constexpr int kRowsAny1Max = 2048;
 
+template <int DT, int E>
+void rows_quant_any1_e(const void* x, int64_t rows, int L, float eps, int8_t* q, float* scale,
+                       hipStream_t s) {
+  const int U = L / E;   // load units per row
+  if (U <= 1) launch_rows_sub_any1<DT, 1, 1, E>(x, rows, L, eps, q, scale, s);
+  else if (U <= 2) launch_rows_sub_any1<DT, 2, 1, E>(x, rows, L, eps, q, scale, s);
+  else if (U <= 4) launch_rows_sub_any1<DT, 4, 1, E>(x, rows, L, eps, q, scale, s);
+  else if (U <= 8) launch_rows_sub_any1<DT, 8, 1, E>(x, rows, L, eps, q, scale, s);
+  else if (U <= 16) launch_rows_sub_any1<DT, 16, 1, E>(x, rows, L, eps, q, scale, s);
+  else if (U <= 32) launch_rows_sub_any1<DT, 32, 1, E>(x, rows, L, eps, q, scale, s);
+  else if (U <= 64) launch_rows_sub_any1<DT, 64, 1, E>(x, rows, L, eps, q, scale, s);
+  else if (U <= 128) launch_rows_sub_any1<DT, 64, 2, E>(x, rows, L, eps, q, scale, s);
+  else if (U <= 256) launch_rows_sub_any1<DT, 64, 4, E>(x, rows, L, eps, q, scale, s);
+  else if (U <= 512) launch_rows_sub_any1<DT, 64, 8, E>(x, rows, L, eps, q, scale, s);
+  else launch_rows_sub_any1<DT, 64, 16, E>(x, rows, L, eps, q, scale, s);
+}
+
 template <int DT>
 void rows_quant_any1(const void* x, int64_t rows, int L, float eps, int8_t* q, float* scale,
                      hipStream_t s) {
-  if (L <= 1) launch_rows_sub_any1<DT, 1, 1>(x, rows, L, eps, q, scale, s);
-  else if (L <= 2) launch_rows_sub_any1<DT, 2, 1>(x, rows, L, eps, q, scale, s);
-  else if (L <= 4) launch_rows_sub_any1<DT, 4, 1>(x, rows, L, eps, q, scale, s);
-  else if (L <= 8) launch_rows_sub_any1<DT, 8, 1>(x, rows, L, eps, q, scale, s);
-  else if (L <= 16) launch_rows_sub_any1<DT, 16, 1>(x, rows, L, eps, q, scale, s);
-  else if (L <= 32) launch_rows_sub_any1<DT, 32, 1>(x, rows, L, eps, q, scale, s);
-  else if (L <= 64) launch_rows_sub_any1<DT, 64, 1>(x, rows, L, eps, q, scale, s);
-  else if (L <= 128) launch_rows_sub_any1<DT, 64, 2>(x, rows, L, eps, q, scale, s);
-  else if (L <= 256) launch_rows_sub_any1<DT, 64, 4>(x, rows, L, eps, q, scale, s);
-  else if (L <= 512) launch_rows_sub_any1<DT, 64, 8>(x, rows, L, eps, q, scale, s);
-  else if (L <= 1024) launch_rows_sub_any1<DT, 64, 16>(x, rows, L, eps, q, scale, s);
-  else launch_rows_sub_any1<DT, 64, 32>(x, rows, L, eps, q, scale, s);
+  constexpr uintptr_t pair = DT == kF32 ? 8 : 4;
+  if (L % 2 == 0 && aligned(x, pair) && aligned(q, 2))
+    rows_quant_any1_e<DT, 2>(x, rows, L, eps, q, scale, s);
+  else if (L <= 1024)
+    rows_quant_any1_e<DT, 1>(x, rows, L, eps, q, scale, s);
+  else
+    launch_rows_sub_any1<DT, 64, 32, 1>(x, rows, L, eps, q, scale, s);
 }
 
 // Slices per row for the split-row path: enough workgroups for about four
