@@ -21,6 +21,8 @@
 //                    walking rows
 //   k_deq_cols_narrow the same for rows of at most 1024 codes: several rows
 //                    per workgroup pass, so every thread has a chunk
+//   k_deq_cols_narrow1 the same with one code per thread, for rows of at most
+//                    128 codes that 8-byte loads cannot take
 //   k_deq_group_tile groups along a non-last axis (the reference moves the
 //                    axis last with two copies, dequantizers.py:58-72): 1-2
 //                    waves per group and 512 inner positions, in place
@@ -390,6 +392,29 @@ __global__ __launch_bounds__(kBlock) void k_deq_cols_narrow(
   }
 }
 
+// The same for narrow rows that 8-byte code loads cannot take (cols <=
+// kBlock / 2 with cols % 8 != 0, or unaligned buffers): one code per thread.
+template <int OUT>
+__global__ __launch_bounds__(kBlock) void k_deq_cols_narrow1(
+    const int8_t* __restrict__ q, const float* __restrict__ scale, int64_t rows, int64_t cols,
+    int64_t RB, int rpi, int64_t inner, void* __restrict__ y) {
+  const int u = static_cast<int>(cols);
+  const int sub = static_cast<int>(threadIdx.x) / u, c = static_cast<int>(threadIdx.x) - sub * u;
+  if (sub >= rpi) return;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * RB;
+  const int64_t r1 = r0 + RB < rows ? r0 + RB : rows;
+  const float s = scale[c / inner];
+  int64_t r = r0 + sub;
+  for (; r + 3 * rpi < r1; r += 4 * rpi) {
+    int8_t v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = q[(r + k * rpi) * cols + c];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) st1<OUT>(y, (r + k * rpi) * cols + c, static_cast<float>(v[k]) * s);
+  }
+  for (; r < r1; r += rpi) st1<OUT>(y, r * cols + c, static_cast<float>(q[r * cols + c]) * s);
+}
+
 // Groups along a non-last axis ([outer, len, inner], groups of G along len):
 // one thread per group (o, g, i), i fastest; scale index in the reference's
 // movedim layout, (o * inner + i) * (len / G) + g (dequantizers.py:61-72).
@@ -653,6 +678,15 @@ int deq_cols_t(const int8_t* q, const float* scale, int64_t rows, int64_t cols, 
                void* y, hipStream_t s, const char* what) {
   const bool vec = (cols % 8 == 0) && aligned(q, 8) && aligned(y, 16);
   const int64_t u = cols >> 3;
+  if (!vec && cols <= kBlock / 2) {
+    // narrow rows, one code per thread: 16 rows per thread
+    const int rpi = kBlock / static_cast<int>(cols);
+    int64_t RB = rpi * 2 * kDeqNarrowRows;
+    if (cdiv(rows, RB) > 65535) RB = cdiv(cdiv(rows, 65535), rpi) * rpi;
+    k_deq_cols_narrow1<OUT><<<dim3(1, static_cast<unsigned>(cdiv(rows, RB))), dim3(kBlock), 0, s>>>(
+        q, scale, rows, cols, RB, rpi, inner, y);
+    return launch_status(what);
+  }
   if (vec && u <= kBlock / 2) {
     // narrow rows: kDeqNarrowRows rows per thread, rpi threads per chunk
     const int rpi = kBlock / static_cast<int>(u);

@@ -45,6 +45,9 @@
 //   k_colmax_narrow / k_cast_cols_narrow
 //                   the same for rows of at most 1024 columns: several rows
 //                   per workgroup pass, so every thread has a chunk
+//   k_colmax_narrow1 / k_cast_cols_narrow1
+//                   the same with one element per thread, for rows of at
+//                   most 128 columns that 16-byte loads cannot take
 //   k_chan_wg       per-channel quant of an N-D tensor seen as
 //                   [outer, channels, inner] in one pass: one workgroup per
 //                   channel holding its outer segments (512 .. 65536
@@ -857,14 +860,18 @@ __global__ __launch_bounds__(kBlock) void k_colmax(
 // Column maxima from the partials: a workgroup covers kFinCols columns; its
 // kBlock / kFinCols thread slices stride over the row blocks, then combine
 // through LDS.
+// FC columns per workgroup: kFinCols, or 4 for narrow rows, whose few
+// columns would otherwise leave a handful of workgroups walking all the row
+// blocks.
 constexpr int kFinCols = 32;
+template <int FC>
 __global__ __launch_bounds__(kBlock) void k_col_finalize(
     const float* __restrict__ partial, int64_t nrb, int64_t cols, float eps,
     float* __restrict__ inv_out, float* __restrict__ scale) {
-  constexpr int kSlices = kBlock / kFinCols;
-  __shared__ float red[kSlices][kFinCols];
-  const int cl = threadIdx.x % kFinCols, sl = threadIdx.x / kFinCols;
-  const int64_t c = static_cast<int64_t>(blockIdx.x) * kFinCols + cl;
+  constexpr int kSlices = kBlock / FC;
+  __shared__ float red[kSlices][FC];
+  const int cl = threadIdx.x % FC, sl = threadIdx.x / FC;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * FC + cl;
   float m = 0.0f;
   if (c < cols)
     for (int64_t b = sl; b < nrb; b += kSlices) m = fmaxf(m, partial[b * cols + c]);
@@ -1056,6 +1063,60 @@ __global__ __launch_bounds__(kBlock) void k_cast_cols_narrow(
     for (int e = 0; e < 8; ++e) f[e] *= inv[e];
     stg8(q + r * cols + c, pack8_int8(f, 1.0f));
   }
+}
+
+// The same for narrow rows that 16-byte loads cannot take (cols <= kBlock /
+// 2 with cols % 8 != 0, or unaligned buffers): one element per thread, thread
+// t on column t % cols of rows r0 + t / cols, stepping by rpi = kBlock / cols.
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_colmax_narrow1(
+    const void* __restrict__ x, int64_t rows, int64_t cols, int64_t RB, int rpi,
+    float* __restrict__ partial) {
+  __shared__ float red[kBlock];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * RB;
+  const int64_t r1 = r0 + RB < rows ? r0 + RB : rows;
+  const int u = static_cast<int>(cols);
+  const int sub = static_cast<int>(threadIdx.x) / u, c = static_cast<int>(threadIdx.x) - sub * u;
+  float m = 0.0f;
+  if (sub < rpi) {
+    int64_t r = r0 + sub;
+    for (; r + 3 * rpi < r1; r += 4 * rpi) {
+      float v[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[k] = ld1<DT>(x, (r + k * rpi) * cols + c);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) m = fmaxf(m, __builtin_fabsf(v[k]));
+    }
+    for (; r < r1; r += rpi) m = fmaxf(m, __builtin_fabsf(ld1<DT>(x, r * cols + c)));
+  }
+  red[threadIdx.x] = m;
+  __syncthreads();
+  if (sub == 0) {
+    for (int k = 1; k < rpi; ++k) m = fmaxf(m, red[k * u + c]);
+    partial[static_cast<int64_t>(blockIdx.y) * cols + c] = m;
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_cast_cols_narrow1(
+    const void* __restrict__ x, int64_t rows, int64_t cols, int64_t RB, int rpi,
+    const float* __restrict__ inv_c, int64_t inner, int8_t* __restrict__ q) {
+  const int u = static_cast<int>(cols);
+  const int sub = static_cast<int>(threadIdx.x) / u, c = static_cast<int>(threadIdx.x) - sub * u;
+  if (sub >= rpi) return;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * RB;
+  const int64_t r1 = r0 + RB < rows ? r0 + RB : rows;
+  const float inv = inv_c[c / inner];
+  int64_t r = r0 + sub;
+  for (; r + 3 * rpi < r1; r += 4 * rpi) {
+    float v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = ld1<DT>(x, (r + k * rpi) * cols + c);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      q[(r + k * rpi) * cols + c] = static_cast<int8_t>(q_int8(v[k] * inv));
+  }
+  for (; r < r1; r += rpi) q[r * cols + c] = static_cast<int8_t>(q_int8(ld1<DT>(x, r * cols + c) * inv));
 }
 
 // N-D channel quant in one pass: one workgroup of B threads per channel
@@ -1734,23 +1795,38 @@ int cols_quant_t(const void* x, int64_t rows, int64_t cols, int64_t inner, float
   const dim3 grid2(static_cast<unsigned>(g.col_blocks), static_cast<unsigned>(g.nrb));
   const int64_t u = cols >> 3;
   const bool narrow = vec && u <= kBlock / 2;
-  const int rpi = narrow ? kBlock / static_cast<int>(u) : 1;
-  if (narrow)
+  const bool narrow1 = !vec && cols <= kBlock / 2;
+  const int rpi = narrow ? kBlock / static_cast<int>(u)
+                         : (narrow1 ? kBlock / static_cast<int>(cols) : 1);
+  if (narrow1)
+    k_colmax_narrow1<DT><<<grid2, dim3(kBlock), 0, s>>>(x, rows, cols, g.RB, rpi, partial);
+  else if (narrow)
     k_colmax_narrow<DT><<<grid2, dim3(kBlock), 0, s>>>(x, rows, cols, g.RB, static_cast<int>(u),
                                                        rpi, partial);
   else
     k_colmax<DT><<<grid2, dim3(kBlock), 0, s>>>(x, rows, cols, g.RB, vec ? 1 : 0, partial);
   if (inner == 1)
-    if (cols % 4 == 0)
+    if (cols <= 1024)
+      k_col_finalize<4><<<dim3(static_cast<unsigned>(cdiv(cols, 4))), dim3(kBlock), 0, s>>>(
+          partial, g.nrb, cols, eps, inv, scale);
+    else if (cols % 4 == 0)
       k_col_finalize4<<<dim3(static_cast<unsigned>(cdiv(cols, kFin4Cols))), dim3(kBlock), 0, s>>>(
           partial, g.nrb, cols, eps, inv, scale);
     else
-      k_col_finalize<<<dim3(static_cast<unsigned>(cdiv(cols, kFinCols))), dim3(kBlock), 0, s>>>(
-          partial, g.nrb, cols, eps, inv, scale);
+      k_col_finalize<kFinCols><<<dim3(static_cast<unsigned>(cdiv(cols, kFinCols))), dim3(kBlock),
+                                 0, s>>>(partial, g.nrb, cols, eps, inv, scale);
   else
     k_chan_finalize<<<dim3(static_cast<unsigned>(cols / inner)), dim3(kBlock), 0, s>>>(
         partial, g.nrb, cols, inner, eps, inv, scale);
   int64_t crb;
+  if (narrow1) {
+    // 2 kCastRB rows per thread, rpi threads per column
+    crb = rpi * 2 * kCastRB;
+    if (cdiv(rows, crb) > 65535) crb = cdiv(cdiv(rows, 65535), rpi) * rpi;
+    k_cast_cols_narrow1<DT><<<dim3(1, static_cast<unsigned>(cdiv(rows, crb))), dim3(kBlock), 0,
+                              s>>>(x, rows, cols, crb, rpi, inv, inner, q);
+    return launch_status(what);
+  }
   if (narrow) {
     // kCastRB rows per thread, rpi threads per column chunk
     crb = rpi * kCastRB;

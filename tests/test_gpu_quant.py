@@ -379,7 +379,10 @@ def test_rows_split_needs_its_workspace():
                                    # per workgroup pass, 2 .. 32 threads per chunk
                                    (20000, 64), (4096, 256), (3000, 1000), (50000, 8),
                                    (7, 64), (10001, 24), (2048, 40), (1000, 1016),
-                                   (70000, 16)])
+                                   (70000, 16),
+                                   # narrow rows without 16-byte loads: one element per
+                                   # thread, several rows per workgroup pass
+                                   (20000, 60), (5000, 37), (3000, 127), (70000, 5), (9, 100)])
 @pytest.mark.parametrize("code", [oracle.BF16, oracle.F16, oracle.F32])
 def test_columns(shape, code):
     x = rand_bits(shape, code, seed=sum(shape) + code)
@@ -589,7 +592,8 @@ def test_config4_int8_group_full():
     # leading axis with few long channels: rows cut into slices over the CUs
     ((4, 64, 1024), 0), ((2, 3, 70000), 0),
     # narrow [outer, C * inner] views: several rows per workgroup pass
-    ((64, 30, 64), 2), ((100, 4, 16), 1), ((3000, 2, 8), 1), ((500, 8, 3), 1)])
+    ((64, 30, 64), 2), ((100, 4, 16), 1), ((3000, 2, 8), 1), ((500, 8, 3), 1),
+    ((400, 5, 3), 1), ((2000, 13), 1)])
 def test_channel_any_axis(code, shape, axis):
     from cublade_amd.quantization import dequantize_tensor, quantize_tensor
     x = rand_bits(shape, code, seed=sum(shape) + axis)
