@@ -28,6 +28,8 @@ SOURCES = [
 ]
 
 WS_CTRL_BYTES = 16384
+# The library's ABI major version these signatures match (cbq_abi_version() // 100).
+ABI_MAJOR = 2
 
 F32, F16, BF16 = 0, 1, 2
 I8, U8, I32 = 3, 4, 5
@@ -46,6 +48,9 @@ SIGNATURES = {
     "cbq_quant_int8_channel_ws_bytes": (_SZ, [_I64, _I64, _I32]),
     "cbq_quant_fp8_tensor": (_I32, [_P, _I32, _I64, _F, _P, _SZ, _P, _P, _P]),
     "cbq_quant_fp8_tensor_noalloc": (_I32, [_P, _I32, _I64, _F, _P, _P, _P]),
+    "cbq_tensor_quant_status": (_I32, [_P, _P, ctypes.POINTER(ctypes.c_int)]),
+    "cbq_tensor_quant_status_clear": (_I32, [_P, _P]),
+    "cbq_set_tensor_spin_limit": (ctypes.c_uint32, [ctypes.c_uint32]),
     "cbq_dequant_fp8_tensor": (_I32, [_P, _P, _I64, _P, _I32, _P]),
     "cbq_quant_int8_tensor": (_I32, [_P, _I32, _I64, _F, _P, _SZ, _P, _P, _P]),
     "cbq_quant_int8_channel": (_I32, [_P, _I32, _I64, _I64, _I32, _F, _P, _SZ, _P, _P, _P]),
@@ -80,6 +85,13 @@ def lib() -> ctypes.CDLL:
         with _lib_lock:
             if _lib is None:
                 L = load_hip_module(LIB_NAME, SOURCES)
+                L.cbq_abi_version.restype = _I32
+                L.cbq_abi_version.argtypes = []
+                ver = L.cbq_abi_version()
+                if ver // 100 != ABI_MAJOR:
+                    raise RuntimeError(
+                        f"cublade: {LIB_NAME} has ABI version {ver}, these bindings need major "
+                        f"version {ABI_MAJOR} (rebuild the library)")
                 for name, (res, args) in SIGNATURES.items():
                     fn = getattr(L, name)
                     fn.restype = res
@@ -164,14 +176,42 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
         return buf
 
 
-def tensor_quant_status(device: torch.device) -> int:
-    """The sticky status word of the one-launch per-tensor quant in the
-    current stream's workspace (0: every exchange completed; 1: a wait timed
-    out and the workspace is poisoned until its control block is zeroed).
-    Synchronises with the device."""
+def _tensor_ws(device: torch.device):
     key = (device_index(device), stream_handle(device))
     with _ws_lock:
-        buf = _ws.get(key)
-    if buf is None:
+        return _ws.get(key)
+
+
+def tensor_quant_status(device: torch.device, noalloc: bool = False) -> int:
+    """The sticky status word of the one-launch per-tensor quant: of the
+    current stream's workspace, or with ``noalloc`` of the static array that
+    cbq_quant_fp8_tensor_noalloc uses on ``device``. 0: no exchange timed out
+    since the word was last cleared; 1: one did (that call's scale is NaN
+    unless every code it wrote is exact; later calls are exact again).
+    Synchronises the current stream."""
+    buf = None if noalloc else _tensor_ws(device)
+    if buf is None and not noalloc:
         return 0
-    return int(buf[512:516].view(torch.int32).item())
+    st = ctypes.c_int(0)
+    with on_device(device):
+        check(lib().cbq_tensor_quant_status(None if noalloc else buf.data_ptr(),
+                                            stream_handle(device), ctypes.byref(st)),
+              "cbq_tensor_quant_status")
+    return st.value
+
+
+def clear_tensor_quant_status(device: torch.device, noalloc: bool = False) -> None:
+    """Clears that status word, in stream order (no synchronisation)."""
+    buf = None if noalloc else _tensor_ws(device)
+    if buf is None and not noalloc:
+        return
+    with on_device(device):
+        check(lib().cbq_tensor_quant_status_clear(None if noalloc else buf.data_ptr(),
+                                                  stream_handle(device)),
+              "cbq_tensor_quant_status_clear")
+
+
+def set_tensor_spin_limit(polls: int) -> int:
+    """Polls before a per-tensor quant's workgroups give up waiting for each
+    other (cbq_set_tensor_spin_limit); returns the previous value."""
+    return int(lib().cbq_set_tensor_spin_limit(int(polls)))

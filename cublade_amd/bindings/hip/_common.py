@@ -7,6 +7,8 @@ RuntimeError) so that the bindings fail the same way:
 """
 from __future__ import annotations
 
+import os
+
 import torch
 
 from ... import _abi
@@ -42,3 +44,19 @@ def check_out_dtype(dtype: torch.dtype) -> int:
     if dtype not in (torch.float16, torch.bfloat16):
         raise RuntimeError("out_dtype must be torch.float16 or torch.bfloat16")
     return _abi.DTYPE_CODE[dtype]
+
+
+def check_exchange(dev: torch.device, what: str) -> None:
+    """With CUBLADE_CHECK_EXCHANGE=1 in the environment: synchronise after a
+    per-tensor quant and raise RuntimeError if its workgroups' exchange timed
+    out (the status word of the stream's workspace; cleared before raising).
+    Off by default, so that calls stay asynchronous; a timed-out call's scale
+    is NaN whenever a code is not exact, and later calls are exact either way."""
+    if os.environ.get("CUBLADE_CHECK_EXCHANGE", "") in ("", "0"):
+        return
+    if _abi.tensor_quant_status(dev):
+        _abi.clear_tensor_quant_status(dev)
+        raise RuntimeError(
+            f"{what}: the workgroups of the one-launch per-tensor quant gave up waiting for "
+            f"each other (exchange timed out; other work kept part of the grid off the GPU): "
+            f"the result is not valid, repeat the call")

@@ -5,7 +5,7 @@ from __future__ import annotations
 import torch
 
 from ... import _abi
-from ._common import check_float_input
+from ._common import check_exchange, check_float_input
 
 
 def quantize_per_tensor_fp8(
@@ -41,4 +41,5 @@ def quantize_per_tensor_fp8(
         rc = L.cbq_quant_fp8_tensor(_abi.ptr(x), code, n, float(eps), _abi.ptr(ws), ws.numel(),
                                     _abi.ptr(q), _abi.ptr(scale), _abi.stream_handle(dev))
     _abi.check(rc, "quantize_per_tensor_fp8")
+    check_exchange(dev, "quantize_per_tensor_fp8")
     return q, scale

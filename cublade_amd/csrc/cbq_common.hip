@@ -50,4 +50,4 @@ int device_cus() {
 
 extern "C" const char* cbq_last_error(void) { return cbq::g_err; }
 
-extern "C" int cbq_abi_version(void) { return 106; }
+extern "C" int cbq_abi_version(void) { return 200; }

@@ -66,6 +66,7 @@
 //
 // Numerics: see cbq_device.h. Every kernel guards its indices against the
 // sizes it is given; the entry points check shapes, dtypes and alignment.
+#include <atomic>
 #include <cstdlib>
 #include <mutex>
 
@@ -209,27 +210,42 @@ __global__ __launch_bounds__(kBlock) void k_cast_tensor(
 //
 // Exchange (no atomics: same-address device atomics serialize at ~25 ns each
 // on MI355X, 6 us for one per workgroup). Control block layout, bytes:
-//   0      gen     64-bit call count of this workspace
-//   512    status  sticky; 1 when a workgroup's wait timed out
-//   1024   slot[b] 64-bit per workgroup: (low 32 bits of gen + 1) << 32 |
-//                  the workgroup's |x| maximum (float bits)
-// Every workgroup reads gen when it starts, publishes its slot with the tag
-// gen + 1, and polls all slots until every tag is gen + 1; workgroup 0 then
-// stores gen + 1 (every workgroup has read gen by then: its slot carries it).
-// Each call rewrites every slot, so no word needs resetting, and a stale tag
-// is always the previous call's. A wait gives up after spin_limit polls
-// (only possible when the grid is not resident at once, e.g. other work
-// holding CUs for about a second): the workgroup sets status and writes NaN
-// codes (INT8: 0) and a NaN scale instead of quietly wrong ones. A timed-out
-// call can leave slots tagged for the next call, so a set status poisons the
-// workspace: every later call writes NaN codes and scale without exchanging,
-// until the caller zero-fills the control block again.
+//   0      gen      tag of the last call whose exchange completed (low 32
+//                   bits of a 64-bit word; 0 in a zero-filled block)
+//   512    status   sticky int32 for the caller: 1 once a workgroup of any
+//                   call gave up waiting (cleared only by the caller)
+//   520    suspect  tag of the last call in which a workgroup gave up
+//   1024   slot[b]  64-bit per workgroup: tag << 32 | its |x| maximum (bits)
+// A call's tag is gen + 1 (skipping 0, the tag of a zero-filled slot). Each
+// workgroup reads gen when it starts, publishes its slot (and refreshes the
+// slots b + G, b + 2G, ... beyond the grid, so that no slot ever holds a tag
+// older than the previous call's), and polls slots [0, G) until every tag is
+// the call's. Only a workgroup whose wait completed advances gen (workgroup
+// 0 normally): a completed wait proves that every workgroup has read gen, so
+// every workgroup of a call uses the same tag, and the next call (stream
+// order: it starts after this one has ended) uses a tag no slot carries.
+//
+// A wait gives up after spin_limit polls (only possible when the grid is not
+// resident at once, e.g. other work holding CUs for about a second). Then the
+// workgroup stores suspect = tag and status = 1, waits for both stores, and
+// polls once more:
+//  * if every slot now carries the tag, it goes on as a completed wait;
+//  * otherwise it gives up: its codes are NaN (INT8: 0) and it writes a NaN
+//    scale. Some slot j was missing at that final poll, so workgroup j
+//    published after the suspect store, and every completed wait of the call
+//    (each must see slot j) reads suspect == tag afterwards. Those
+//    workgroups advance gen (the last workgroup to publish always completes,
+//    so gen always advances), and workgroup 0 returns NaN, so the scale is
+//    NaN whenever any workgroup gave up.
+// A scale that is not NaN therefore comes with every code exact. Later calls
+// are exact again without any reset; status tells the caller that a call
+// since it last cleared the word was touched by a timeout.
 // ---------------------------------------------------------------------------
 constexpr int kFusedBlock = 1024;                // 16 waves: four per SIMD
 constexpr int kFusedU = 4;                       // chunks per thread and step
 constexpr int64_t kFusedMinElems = int64_t(1) << 20;
 constexpr uint32_t kFusedSpinLimit = 1u << 20;   // polls (each >= one memory round trip)
-constexpr int kCtlGen = 0, kCtlStatus = 512, kCtlSlots = 1024;
+constexpr int kCtlGen = 0, kCtlStatus = 512, kCtlSuspect = 520, kCtlSlots = 1024;
 constexpr int kMaxFusedGrid = (CBQ_WS_CTRL_BYTES - kCtlSlots) / 8;
 
 // Steps held in registers: 24 chunks (96 VGPRs) of 2-byte input, 12 of fp32.
@@ -296,52 +312,88 @@ __device__ __forceinline__ void cast_store8_buf(const Raw8<DT>& r, float inv,
                                         CBQ_NT_STORES_NARROW ? kAuxNT : 0);
 }
 
-// Grid-wide maximum of the workgroups' m (see the exchange above); returns
-// NaN if the wait timed out. Every thread of the workgroup gets the result.
+// Grid-wide maximum of the workgroups' m (see the exchange above); NaN in a
+// workgroup that gave up waiting, and in workgroup 0 of a call in which any
+// workgroup did. Every thread of the workgroup gets the result.
 __device__ float grid_max_exchange(float m, char* ctl, uint32_t spin_limit, float* red) {
-  __shared__ unsigned long long s_gen;
-  __shared__ int s_poisoned;
+  __shared__ uint32_t s_tag;
+  __shared__ int s_nan;
   auto* gen_w = reinterpret_cast<unsigned long long*>(ctl + kCtlGen);
   auto* status = reinterpret_cast<unsigned int*>(ctl + kCtlStatus);
+  auto* suspect = reinterpret_cast<unsigned int*>(ctl + kCtlSuspect);
   auto* slots = reinterpret_cast<unsigned long long*>(ctl + kCtlSlots);
+  const int G = static_cast<int>(gridDim.x);
+  const int b = static_cast<int>(blockIdx.x);
   if (threadIdx.x == 0) {
-    const unsigned long long gen = __hip_atomic_load(gen_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const unsigned st = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_gen = gen;
-    s_poisoned = st != 0;
-    if (st == 0)
-      __hip_atomic_store(slots + blockIdx.x,
-                         (static_cast<unsigned long long>(static_cast<uint32_t>(gen + 1)) << 32) |
-                             __float_as_uint(m),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t g = static_cast<uint32_t>(
+        __hip_atomic_load(gen_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const uint32_t tag = g + 1 == 0 ? 1u : g + 1;
+    s_tag = tag;
+    __hip_atomic_store(slots + b,
+                       (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(m),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);   // the slot store has been performed before any poll
   }
   __syncthreads();
-  if (s_poisoned) return __builtin_nanf("");
-  const uint32_t tag = static_cast<uint32_t>(s_gen + 1);
-  const int G = static_cast<int>(gridDim.x);
-  uint32_t spins = 0;
-  float mx;
-  int ok;
-  for (;;) {
-    ok = 1;
+  const uint32_t tag = s_tag;
+  const unsigned long long mine = (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(m);
+  for (int k = static_cast<int>(threadIdx.x) + 1; b + static_cast<int64_t>(k) * G < kMaxFusedGrid;
+       k += static_cast<int>(blockDim.x))   // slots beyond the grid: refreshed, never read
+    __hip_atomic_store(slots + b + k * G, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  auto poll = [&](float& mx) {
+    int ok = 1;
     mx = 0.0f;
     for (int i = threadIdx.x; i < G; i += blockDim.x) {
       const unsigned long long v = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       ok &= static_cast<uint32_t>(v >> 32) == tag;
       mx = fmaxf(mx, __uint_as_float(static_cast<uint32_t>(v)));
     }
-    ok = __syncthreads_and(ok);
+    return __syncthreads_and(ok);
+  };
+  uint32_t spins = 0;
+  float mx;
+  int ok;
+  for (;;) {
+    ok = poll(mx);
     if (ok || spins >= spin_limit) break;
     ++spins;
     __builtin_amdgcn_s_sleep(2);
   }
-  mx = block_max(mx, red);
-  if (threadIdx.x == 0) {
-    if (!ok) __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (blockIdx.x == 0)
-      __hip_atomic_store(gen_w, s_gen + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (!ok) {
+    if (threadIdx.x == 0) {
+      __hip_atomic_store(suspect, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);   // both performed before the final poll
+    }
+    __syncthreads();
+    ok = poll(mx);
   }
-  return ok ? mx : __builtin_nanf("");
+  if (threadIdx.x == 0) {
+    int nan = !ok;
+    if (ok) {
+      const uint32_t sp = __hip_atomic_load(suspect, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (sp == tag) {
+        // a workgroup of this call gave up: make sure gen advances, and let
+        // workgroup 0 write a NaN scale
+        __hip_atomic_store(gen_w, static_cast<unsigned long long>(tag), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        nan = b == 0;
+      } else if (b == 0) {
+        __hip_atomic_store(gen_w, static_cast<unsigned long long>(tag), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        if (sp != 0) {   // an earlier call's record: clear it unless a workgroup of this call
+                         // has just replaced it
+          uint32_t expect = sp;
+          __hip_atomic_compare_exchange_strong(suspect, &expect, 0u, __ATOMIC_RELAXED,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+    s_nan = nan;
+  }
+  mx = block_max(mx, red);   // contains a barrier: s_nan is visible after it
+  return s_nan ? __builtin_nanf("") : mx;
 }
 
 template <int DT, bool FP8>
@@ -1428,17 +1480,19 @@ int64_t tensor_grid(int64_t n, bool vec) {
 }
 
 // Polls a one-launch wait makes before giving up: kFusedSpinLimit, or the
-// CBQ_TENSOR_SPIN_LIMIT environment variable read at the first call (a host
-// switch that lets tests exercise the timeout path with every kernel still
-// ending normally).
-uint32_t fused_spin_limit() {
-  static const uint32_t v = [] {
+// CBQ_TENSOR_SPIN_LIMIT environment variable read at the first call, or the
+// value set by cbq_set_tensor_spin_limit (a host switch that lets tests
+// exercise the timeout path with every kernel still ending normally, and
+// callers that share the GPU with long-running kernels pick their bound).
+std::atomic<uint32_t>& spin_limit_var() {
+  static std::atomic<uint32_t> v{[] {
     const char* e = getenv("CBQ_TENSOR_SPIN_LIMIT");
     if (!e || !*e) return kFusedSpinLimit;
     return static_cast<uint32_t>(strtoul(e, nullptr, 10));
-  }();
+  }()};
   return v;
 }
+uint32_t fused_spin_limit() { return spin_limit_var().load(std::memory_order_relaxed); }
 
 // True if one workgroup of the one-launch kernel fits on a CU, i.e. a grid
 // of one workgroup per CU is resident at once (cached per device and kernel).
@@ -1454,6 +1508,13 @@ bool fused_fits() {
     cached[dev] = (e == hipSuccess && nb >= 1) ? 1 : 2;
   }
   return cached[dev] == 1;
+}
+
+// Clears the sticky status word of a per-tensor control block (a kernel,
+// not hipMemsetAsync, so that it is stream-ordered and safe under capture).
+__global__ void k_clear_tensor_status(char* ctl) {
+  __hip_atomic_store(reinterpret_cast<unsigned int*>(ctl + kCtlStatus), 0u, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int DT>
@@ -2030,6 +2091,44 @@ extern "C" int cbq_quant_fp8_tensor_noalloc(const void* x, int dtype, int64_t n,
   if (rc != CBQ_OK) return rc;
   return tensor_quant(x, dtype, n, eps, ws, kNoAllocScratchBytes, q, scale, true,
                       as_stream(stream));
+}
+
+extern "C" uint32_t cbq_set_tensor_spin_limit(uint32_t polls) {
+  return spin_limit_var().exchange(polls, std::memory_order_relaxed);
+}
+
+extern "C" int cbq_tensor_quant_status(const void* ws, cbq_stream_t stream, int* status) {
+  clear_error();
+  const char* what = "cbq_tensor_quant_status";
+  CBQ_REQUIRE(status, "%s: null status pointer", what);
+  void* ctl = const_cast<void*>(ws);
+  if (!ctl) {
+    const int rc = scratch_for_current_device(&ctl, what);
+    if (rc != CBQ_OK) return rc;
+  }
+  int32_t v = 0;
+  const hipStream_t s = as_stream(stream);
+  hipError_t e = hipMemcpyAsync(&v, static_cast<char*>(ctl) + kCtlStatus, sizeof(v),
+                                hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) {
+    set_error("%s: reading the status word failed: %s", what, hipGetErrorString(e));
+    return CBQ_ELAUNCH;
+  }
+  *status = v;
+  return CBQ_OK;
+}
+
+extern "C" int cbq_tensor_quant_status_clear(void* ws, cbq_stream_t stream) {
+  clear_error();
+  const char* what = "cbq_tensor_quant_status_clear";
+  void* ctl = ws;
+  if (!ctl) {
+    const int rc = scratch_for_current_device(&ctl, what);
+    if (rc != CBQ_OK) return rc;
+  }
+  k_clear_tensor_status<<<dim3(1), dim3(1), 0, as_stream(stream)>>>(static_cast<char*>(ctl));
+  return launch_status(what);
 }
 
 extern "C" int cbq_quant_fp8_tensor(const void* x, int dtype, int64_t n, float eps, void* ws,

@@ -47,22 +47,27 @@ enum { CBQ_OK = 0, CBQ_EINVAL = 1, CBQ_ELAUNCH = 2 };
  * 16-byte aligned device buffer of at least the size their *_ws_bytes query
  * returns. The first CBQ_WS_CTRL_BYTES bytes are a control block: zero-fill
  * it once before the first call on that workspace and do not write to it
- * afterwards (zero-filling all of it again is allowed between calls: it
+ * afterwards (zero-filling all of it again between calls is allowed: it
  * resets it). The per-tensor quant entry points keep their cross-workgroup
- * state there (a generation counter at byte 0, tagged per-workgroup slots
- * from byte 1024) and a sticky int32 status word at byte 512: nonzero after
- * a call whose workgroups gave up waiting for each other, after which every
- * per-tensor call on that workspace writes a NaN scale (FP8 codes NaN, INT8
- * codes 0) until the block is zero-filled again. The other entry points
- * leave the control block alone. The rest is per-call scratch. One workspace
- * serves one stream at a time: calls that overlap in time must not share
- * it. */
+ * state there (a generation tag at byte 0, the tag of the last call that
+ * timed out at byte 520, tagged per-workgroup slots from byte 1024) and a
+ * sticky int32 status word at byte 512 (cbq_tensor_quant_status): 1 once the
+ * workgroups of a call gave up waiting for each other (only possible when
+ * other work keeps part of the grid off the GPU for about a second). Such a
+ * call writes a NaN scale whenever any of its codes is not exact (FP8 codes
+ * NaN, INT8 codes 0 there); a scale that is not NaN comes with every code
+ * exact. The next call on the workspace is exact again, with no reset; the
+ * status word stays 1 until cbq_tensor_quant_status_clear. The other entry
+ * points leave the control block alone. The rest is per-call scratch. One
+ * workspace serves one stream at a time: calls that overlap in time must not
+ * share it. */
 #define CBQ_WS_CTRL_BYTES 16384
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* cbq_last_error(void);
 
-/* ABI version (major * 100 + minor). */
+/* ABI version (major * 100 + minor). A caller built against another major
+ * version must not call the library: signatures differ between majors. */
 int cbq_abi_version(void);
 
 /* Workspace bytes needed by cbq_quant_fp8_tensor / cbq_quant_int8_tensor
@@ -95,9 +100,33 @@ int cbq_quant_fp8_tensor(const void* x, int dtype, int64_t n, float eps,
  * call on that GPU: calls that overlap in time on one GPU (other streams,
  * other threads) race and must be serialised by the caller. Allocates nothing;
  * the first call on a device looks the array's address up
- * (hipGetSymbolAddress), so make that call outside graph capture. */
+ * (hipGetSymbolAddress), so make that call outside graph capture. A timed-out
+ * exchange behaves as described under the workspace contract: read and clear
+ * its status with cbq_tensor_quant_status / _clear and ws = NULL. */
 int cbq_quant_fp8_tensor_noalloc(const void* x, int dtype, int64_t n, float eps,
                                  uint8_t* q, float* scale, cbq_stream_t stream);
+
+/* No counterpart in the reference (its per-tensor kernels never wait on each
+ * other). Status of the one-launch per-tensor quant's control block:
+ * *status = the sticky word described under the workspace contract (0: no
+ * call on this workspace timed out since the word was last cleared). ws: a
+ * workspace given to cbq_quant_{fp8,int8}_tensor, or NULL for the static
+ * array of cbq_quant_fp8_tensor_noalloc on the current device. Reads the word
+ * in stream order and synchronises the stream (not under graph capture). */
+int cbq_tensor_quant_status(const void* ws, cbq_stream_t stream, int* status);
+
+/* Clears that status word, in stream order (a one-thread kernel: allowed
+ * under graph capture). ws as for cbq_tensor_quant_status. */
+int cbq_tensor_quant_status_clear(void* ws, cbq_stream_t stream);
+
+/* Sets how many polls a per-tensor quant's workgroups make while waiting for
+ * each other before they give up (default 1048576, about a second; the
+ * environment variable CBQ_TENSOR_SPIN_LIMIT read at the first call
+ * overrides the default). Takes effect for later launches; returns the
+ * previous value. 0 makes every workgroup that does not find all the others
+ * at its first poll give up: tests use it to force the timeout path while
+ * every kernel still ends normally. */
+uint32_t cbq_set_tensor_spin_limit(uint32_t polls);
 
 /* Replaces dequantize_per_tensor_fp8_cuda (dequantize_per_tensor_fp8.cu:84-109;
  * kernel :23-66), bound as dequantize_fp8.dequantize_per_tensor_fp8

@@ -34,7 +34,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     L = _lib()
     names = declared_symbols()
-    assert len(names) == 24
+    assert len(names) == 27
     for n in names:
         assert hasattr(L, n), n
     from cublade_amd import _abi
@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_slot():
     L = _lib()
-    assert L.cbq_abi_version() == 106
+    assert L.cbq_abi_version() == 200
     assert L.cbq_last_error() in (b"",) or isinstance(L.cbq_last_error(), bytes)
 
 
