@@ -204,29 +204,52 @@ def extras(torch, dev, no_w8a16):
         3 * n + 4 * (n // 128), 3 * n + 4 * (n // 128))
     del x
     if not no_w8a16:
-        for M in (16, 256, 4096):
+        def w8a16_rec(M, N, K, us, us_fp16=None):
+            flops = 2.0 * M * N * K
+            bytes_ = N * K + 2 * N + 2 * M * K + 2 * M * N
+            r = {"us": round(us, 2), "tflops": round(flops / us / 1e6, 2),
+                 "mfma_frac": round(flops / (us * 1e-6) / FP16_PEAK, 4),
+                 "gbs": round(bytes_ / us / 1e3, 1),
+                 "hbm_frac": round(bytes_ / (us * 1e-6) / HBM_PEAK, 4)}
+            if us_fp16 is not None:
+                r["fp16_linear_us"] = round(us_fp16, 2)
+                r["speedup_vs_fp16_linear"] = round(us_fp16 / us, 3)
+            return r
+
+        # config 5 at its three M, then the bottom of the north star's M >= 1024
+        # range (1024, 1536), each next to an fp16 F.linear of the dequantized
+        # weight (the runtime's GEMM library) timed the same way
+        for M in (16, 256, 1024, 1536, 4096):
             xa, w = configs.c5_w8a16(M)
             N, K = w.shape
             layer = cuBladeW8A16LinearLayer(K, N, bias=False, dtype=torch.float16)
             layer.quantize(w.to(dev))
             xd = xa.to(dev)
             us = statistics.median(time_op(lambda: layer(xd), EXTRA_REPS, 2, flush))
-            # the same product with the dequantized weight as an fp16 F.linear
-            # (the runtime's GEMM library), timed the same way
             wd = (layer.int8_weights.half() * layer.scales[:, None]).contiguous()
             us_fp16 = statistics.median(time_op(lambda: torch.nn.functional.linear(xd, wd),
                                                 EXTRA_REPS, 2, flush))
-            flops = 2.0 * M * N * K
-            bytes_ = N * K + 2 * N + 2 * M * K + 2 * M * N
-            out[f"c5_w8a16_m{M}"] = {"us": round(us, 2), "tflops": round(flops / us / 1e6, 2),
-                                     "mfma_frac": round(flops / (us * 1e-6) / FP16_PEAK, 4),
-                                     "gbs": round(bytes_ / us / 1e3, 1),
-                                     "hbm_frac": round(bytes_ / (us * 1e-6) / HBM_PEAK, 4),
-                                     "fp16_linear_us": round(us_fp16, 2),
-                                     "speedup_vs_fp16_linear": round(us_fp16 / us, 3)}
+            out[f"c5_w8a16_m{M}"] = w8a16_rec(M, N, K, us, us_fp16)
             print(f"[bench] w8a16 M={M}: {us:.1f} us (fp16 F.linear {us_fp16:.1f} us)",
                   file=sys.stderr, flush=True)
-            del layer, xd, wd
+            del layer, wd
+            # config 5's outlier threshold (6.0) applied the LLM.int8 way: the
+            # layer's opt-in activation mode routes the 6 outlier features of x
+            # through the fp16 side-GEMM
+            if M in (16, 256, 4096):
+                lo = cuBladeW8A16LinearLayer(K, N, bias=False, dtype=torch.float16,
+                                             handle_outliers=True, outlier_threshold=6.0,
+                                             outlier_mode="activation")
+                lo.quantize(w.to(dev), activations=xa)
+                us_o = statistics.median(time_op(lambda: lo(xd), EXTRA_REPS, 2, flush))
+                r = w8a16_rec(M, N, K, us_o)
+                r["n_outlier_cols"] = int(lo.outlier_cols.numel())
+                r["plain_us"] = round(us, 2)
+                out[f"c5_w8a16_outliers_m{M}"] = r
+                print(f"[bench] w8a16 outliers M={M}: {us_o:.1f} us ({r['n_outlier_cols']} "
+                      f"columns through the side-GEMM)", file=sys.stderr, flush=True)
+                del lo
+            del xd
     return out
 
 

@@ -447,3 +447,37 @@ def test_activation_outlier_columns_and_mode_checks():
         layer.quantize(torch.zeros(4, 8))
     with pytest.raises(ValueError, match="calibration batch"):
         layer.quantize(torch.zeros(4, 8), activations=torch.zeros(3, 7))
+
+
+def test_benchmark_returns_the_reference_contract(capsys):
+    """cublade.benchmark.benchmark keeps the reference's signature (n_flop a
+    required keyword) and result dict (benchmark/core.py:5-71): keys
+    kernel.{time_ms, gflops, max_err, passed, output} and
+    reference.{time_ms, gflops, output}, plus the printed table."""
+    import inspect
+
+    from cublade_amd.benchmark import benchmark
+
+    sig = inspect.signature(benchmark)
+    assert sig.parameters["n_flop"].kind is inspect.Parameter.KEYWORD_ONLY
+    assert sig.parameters["n_flop"].default is inspect.Parameter.empty
+    for name, default in (("warmup", 1), ("atol", 1e-5), ("rtol", 1e-3)):
+        assert sig.parameters[name].default == default
+    a = torch.randn(64, 64)
+
+    def ref(x):
+        return x @ x
+
+    def kern(x):
+        return torch.mm(x, x)
+
+    with pytest.raises(TypeError):
+        benchmark(kern, ref, a)
+    res = benchmark(kern, ref, a, n_flop=2 * 64 ** 3, reps=3)
+    assert set(res) == {"kernel", "reference"}
+    assert set(res["kernel"]) == {"time_ms", "gflops", "max_err", "passed", "output"}
+    assert set(res["reference"]) == {"time_ms", "gflops", "output"}
+    assert res["kernel"]["passed"] is True and res["kernel"]["max_err"] < 1e-3
+    assert res["kernel"]["time_ms"] > 0 and res["reference"]["gflops"] > 0
+    out = capsys.readouterr().out
+    assert "GFLOPS" in out and "PASS" in out and "REF" in out
