@@ -38,10 +38,18 @@
 //                   few long rows (fewer than about two per CU): each row cut
 //                   into slices over the CUs, one partial maximum per slice
 //                   in the workspace, then the cast of each slice
+//   k_quant_cols_1pass
+//                   per-column (axis 1) quant in one launch for rows of 8192,
+//                   16384 or 32768 elements and x of 2^22 elements up to
+//                   352 MiB: k_quant_tensor_1pass's step layout with running
+//                   column maxima per thread, then two grid-wide exchanges
+//                   (partial column maxima; each workgroup's slice of
+//                   multipliers) and the cast from registers / LDS
 //   k_colmax / k_col_finalize / k_cast_cols
-//                   per-column (axis 1) quant: partial column maxima per row
-//                   block, one finalize pass, then the cast with each
-//                   thread's eight column multipliers held in registers
+//                   per-column (axis 1) quant otherwise: partial column
+//                   maxima per row block, one finalize pass, then the cast
+//                   with each thread's eight column multipliers held in
+//                   registers
 //   k_colmax_narrow / k_cast_cols_narrow
 //                   the same for rows of at most 1024 columns: several rows
 //                   per workgroup pass, so every thread has a chunk
@@ -520,6 +528,357 @@ __global__ __launch_bounds__(kFusedBlock) void k_quant_tensor_1pass(
   if (blockIdx.x == 0 && threadIdx.x < 8 && n8 * 8 + threadIdx.x < n) {
     const float v = tail * inv;
     q[n8 * 8 + threadIdx.x] = FP8 ? q_fp8_1(v) : static_cast<uint8_t>(q_int8(v));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Per column (axis 1) in one launch, for rows of 8192, 16384 or 32768
+// elements (c8 = cols / 8 = 1024 CPT chunks, CPT = 1, 2 or 4) and x of up to
+// CBQ_COLS_1PASS_MAX_BYTES (the host checks both). The step
+// layout of k_quant_tensor_1pass: a resident grid of G workgroups (a power
+// of two) reads x once in grid-wide steps of G x 4096 chunks, holding the
+// last HS steps of each thread in registers and parking the first LS streamed
+// steps in LDS (128 MiB of 2-byte x in all on 256 CUs); since a step starts
+// at a multiple of c8 chunks, chunk u of thread t is always of chunk-column
+// t + 1024 (u % CPT), so each thread keeps the running |x| maxima of its CPT
+// chunk-columns (8 columns each). Then two grid-wide exchanges through the
+// workspace:
+//  1. every workgroup stores its [cols] partial maxima (part[b], as 4
+//     planes of float pairs: a wave's stores cover 512 contiguous bytes; with
+//     8-byte stores 32 bytes apart the exchange ran at under 1 TB/s) and
+//     publishes its slot with tag T1; once every slot carries T1 (or T2),
+//     workgroup b reduces the partials of its slice of c8 / G chunk-columns
+//     (<= 16) over all G workgroups, stores the slice's multipliers inv[c] =
+//     fp32(127 / max(amax_c, eps)) and publishes T2;
+//  2. once every slot carries T2, every thread loads the multipliers of its
+//     chunk-columns and casts its held steps from registers, the parked ones
+//     from LDS, and re-reads the rest; workgroup b writes its slice's scales.
+// HBM traffic 2N (+ the re-read beyond 128 MiB) + N + the 4 G cols-byte
+// partials, against 2N + 2N + N for k_colmax + k_cast_cols.
+//
+// Tags and timeouts follow the per-tensor exchange (the same control block:
+// gen, status, suspect, slots). T1 = gen + 1 and T2 = T1 + 1 (skipping 0);
+// only a workgroup whose second wait completed advances gen (workgroup 0, or
+// any of them once suspect holds T1 or T2). A workgroup that gives up on the
+// first wait publishes NaN multipliers for its slice (so those columns get a
+// NaN scale and 0 codes everywhere); one that gives up on the second writes 0
+// codes, and then every workgroup that completes the second wait finds
+// suspect == T2 and writes NaN scales. A scale that is not NaN therefore
+// comes with every code of its column exact.
+// ---------------------------------------------------------------------------
+constexpr int kColsMaxSlice = 16;   // chunk-columns per workgroup in the slice reduction
+constexpr int64_t kColsMinElems = int64_t(1) << 22;
+// Largest x (bytes) the one-launch column path takes; larger ones take
+// k_colmax + k_cast_cols. Measured on MI355X (bf16, cols 8192, op time after
+// a cache sweep, one-launch against two-pass): 64 MiB 36.5 / 37.8 us,
+// 128 MiB 51.4 / 62.4, 192 MiB 78.1 / 86.8, 256 MiB 105.0 / 112.2, 320 MiB
+// 132.0 / 135.2, 448 MiB 187.5 / 184.0 us: past what registers and LDS hold
+// (128 MiB) the re-read of the rest and the exchange cost what the single
+// read saves. A compile-time tuning knob.
+#ifndef CBQ_COLS_1PASS_MAX_BYTES
+#define CBQ_COLS_1PASS_MAX_BYTES (int64_t(352) << 20)
+#endif
+
+// Steps held in registers: those of k_quant_tensor_1pass, less what the CPT
+// chunk-columns' 8 maxima (then multipliers) per thread take.
+template <int DT, int CPT>
+constexpr int cols_hold_steps() {
+  return DT == kF32 ? (CPT == 1 ? 3 : CPT == 2 ? 2 : 1) : (CPT == 1 ? 6 : CPT == 2 ? 5 : 3);
+}
+
+__device__ __forceinline__ uint32_t next_tag(uint32_t g) { return g + 1 == 0 ? 1u : g + 1; }
+
+// Agent-scope 64-bit accesses (coherent across the XCDs' L2s, like the
+// slots) to the exchange arrays, which hold 8 floats per chunk-column as 4
+// planes of pairs: element (i, c) = floats 2i, 2i + 1 of chunk-column c, so
+// that the 64 lanes of a wave (consecutive c) access 512 contiguous bytes.
+__device__ __forceinline__ void ld8_pairs(const unsigned long long* p, int64_t plane,
+                                          int64_t c, float (&v)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const unsigned long long d =
+        __hip_atomic_load(p + i * plane + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    v[2 * i] = __uint_as_float(static_cast<uint32_t>(d));
+    v[2 * i + 1] = __uint_as_float(static_cast<uint32_t>(d >> 32));
+  }
+}
+
+__device__ __forceinline__ void st8_pairs(unsigned long long* p, int64_t plane, int64_t c,
+                                          const float (&v)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    __hip_atomic_store(p + i * plane + c,
+                       static_cast<unsigned long long>(__float_as_uint(v[2 * i])) |
+                           (static_cast<unsigned long long>(__float_as_uint(v[2 * i + 1])) << 32),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits until every slot [0, G) carries tag or alt; after spin_limit polls
+// records suspect = tag and status = 1 (both performed before it) and polls
+// once more. Returns whether the wait completed (every thread gets it).
+__device__ int slot_wait(char* ctl, uint32_t tag, uint32_t alt, uint32_t spin_limit) {
+  auto* slots = reinterpret_cast<unsigned long long*>(ctl + kCtlSlots);
+  const int G = static_cast<int>(gridDim.x);
+  auto poll = [&]() {
+    int ok = 1;
+    for (int i = threadIdx.x; i < G; i += blockDim.x) {
+      const uint32_t t = static_cast<uint32_t>(
+          __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> 32);
+      ok &= (t == tag) | (t == alt);
+    }
+    return __syncthreads_and(ok);
+  };
+  uint32_t spins = 0;
+  int ok;
+  for (;;) {
+    ok = poll();
+    if (ok || spins >= spin_limit) break;
+    ++spins;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  if (!ok) {
+    if (threadIdx.x == 0) {
+      __hip_atomic_store(reinterpret_cast<unsigned int*>(ctl + kCtlSuspect), tag, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(reinterpret_cast<unsigned int*>(ctl + kCtlStatus), 1u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+    __syncthreads();
+    ok = poll();
+  }
+  return ok;
+}
+
+// Thread 0 publishes the workgroup's slot with tag (after the workgroup's
+// data stores, which every thread has waited for before the barrier that
+// precedes this call); with refresh, the slots b + G, b + 2G, ... beyond the
+// grid too (by the whole workgroup).
+__device__ __forceinline__ void slot_publish(char* ctl, uint32_t tag, bool refresh) {
+  auto* slots = reinterpret_cast<unsigned long long*>(ctl + kCtlSlots);
+  const int G = static_cast<int>(gridDim.x), b = static_cast<int>(blockIdx.x);
+  const unsigned long long v = static_cast<unsigned long long>(tag) << 32;
+  if (threadIdx.x == 0) {
+    __hip_atomic_store(slots + b, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+  }
+  if (refresh)
+    for (int k = static_cast<int>(threadIdx.x) + 1; b + static_cast<int64_t>(k) * G < kMaxFusedGrid;
+         k += static_cast<int>(blockDim.x))
+      __hip_atomic_store(slots + b + k * G, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+}
+
+template <int DT, int CPT>
+__device__ __forceinline__ void colmax8(const Raw8<DT>& r, float (&m)[8]) {
+  float f[8];
+  cvt8<DT>(r, f);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) m[e] = fmaxf(m[e], __builtin_fabsf(f[e]));
+}
+
+template <int DT>
+__device__ __forceinline__ uint2 cast8_cols(const Raw8<DT>& r, const float (&inv)[8]) {
+  float f[8];
+  cvt8<DT>(r, f);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] *= inv[e];
+  return pack8_int8(f, 1.0f);   // x 1: exact
+}
+
+template <int DT, int CPT>
+__global__ __launch_bounds__(kFusedBlock) void k_quant_cols_1pass(
+    const void* __restrict__ x, int64_t n8, float eps, int8_t* __restrict__ q,
+    float* __restrict__ scale_out, char* __restrict__ ctl, float* __restrict__ part,
+    float* __restrict__ invs, uint32_t spin_limit) {
+  constexpr int U = kFusedU;
+  constexpr int HS = cols_hold_steps<DT, CPT>();
+  constexpr int LS = fused_lds_steps<DT>();
+  constexpr int EB = 8 * elem_bytes<DT>();            // bytes of x per chunk
+  constexpr int QW = EB / 16;                         // 16-byte words per chunk
+  constexpr int C8 = 1024 * CPT;                      // chunk-columns
+  static_assert(U % CPT == 0, "chunk u of a thread is of chunk-column t + 1024 (u % CPT)");
+  __shared__ u32x4 park[LS * U * QW * kFusedBlock];
+  __shared__ float red[(kFusedBlock / kWave) * kColsMaxSlice * 8];
+  __shared__ uint32_t s_t1;
+  __shared__ int s_nan;
+
+  const int G = static_cast<int>(gridDim.x), b = static_cast<int>(blockIdx.x);
+  const int t = static_cast<int>(threadIdx.x), lane = t % kWave, wave = t / kWave;
+  auto* gen_w = reinterpret_cast<unsigned long long*>(ctl + kCtlGen);
+  auto* suspect = reinterpret_cast<unsigned int*>(ctl + kCtlSuspect);
+  if (t == 0)
+    s_t1 = next_tag(static_cast<uint32_t>(
+        __hip_atomic_load(gen_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
+
+  const int64_t SB = static_cast<int64_t>(kFusedBlock) * U;   // chunks per workgroup and step
+  const int64_t GS = static_cast<int64_t>(G) * SB;            // chunks per grid step
+  const int64_t I = (n8 + GS - 1) / GS;
+  const int64_t held0 = I > HS ? I - HS : 0;
+  const char* xw = static_cast<const char*>(x) + static_cast<int64_t>(b) * SB * EB;
+  int8_t* qw = q + static_cast<int64_t>(b) * SB * 8;
+  const uint32_t xo = t * EB, qo = t * 8;
+
+  // Pass 1: column maxima; streamed steps (the first LS parked), then the
+  // held steps into r[].
+  float m[CPT][8];
+#pragma unroll
+  for (int s = 0; s < CPT; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) m[s][e] = 0.0f;
+  for (int64_t i = 0; i < held0; ++i) {
+    Raw8<DT> v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = ld8_at<DT>(xw + (i * GS + u * kFusedBlock) * EB, xo);
+#pragma unroll
+    for (int u = 0; u < U; ++u) colmax8<DT, CPT>(v[u], m[u % CPT]);
+    if (i < LS) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        u32x4* pk = park + (static_cast<int>(i) * U + u) * QW * kFusedBlock + t;
+        pk[0] = u32x4{v[u].a.x, v[u].a.y, v[u].a.z, v[u].a.w};
+        if constexpr (DT == kF32) pk[kFusedBlock] = u32x4{v[u].b.x, v[u].b.y, v[u].b.z, v[u].b.w};
+      }
+    }
+  }
+  const int64_t cb = static_cast<int64_t>(b) * SB;
+  Raw8<DT> r[HS * U];
+#pragma unroll
+  for (int k = 0; k < HS; ++k) {
+    const int64_t c0 = (held0 + k) * GS + cb;
+    const int64_t left = n8 - c0;
+    __builtin_amdgcn_sched_barrier(0);
+    if (left > 0) {
+      const auto rs = rsrc(static_cast<const char*>(x) + c0 * EB, (left < SB ? left : SB) * EB);
+#pragma unroll
+      for (int u = 0; u < U; ++u) r[k * U + u] = ld8_buf<DT>(rs, u * kFusedBlock * EB + xo);
+#pragma unroll
+      for (int u = 0; u < U; ++u) colmax8<DT, CPT>(r[k * U + u], m[u % CPT]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < HS * U; ++j) reload_barrier<DT>(r[j]);
+
+  // Exchange 1: this workgroup's partial maxima (part: [G][4 planes][C8]
+  // pairs), then tag T1.
+  auto* part64 = reinterpret_cast<unsigned long long*>(part);
+  auto* inv64 = reinterpret_cast<unsigned long long*>(invs);   // [4 planes][C8] pairs
+#pragma unroll
+  for (int s = 0; s < CPT; ++s) st8_pairs(part64 + static_cast<int64_t>(b) * 4 * C8, C8, t + 1024 * s, m[s]);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  const uint32_t T1 = s_t1, T2 = next_tag(T1);
+  slot_publish(ctl, T1, false);
+  const int ok1 = slot_wait(ctl, T1, T2, spin_limit);
+
+  // Slice reduction: chunk-columns [b SCC, b SCC + SCC) over the G partials.
+  // Thread t takes chunk-column cc = t % SCC of partials (t + 1024 j) / SCC,
+  // then the lanes of a wave with the same cc combine (xor shuffles), then
+  // the waves through LDS.
+  const int SCC = C8 / G;                             // power of two, <= kColsMaxSlice
+  const int cc = t & (SCC - 1);
+  float sm[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sm[e] = 0.0f;
+  if (ok1) {
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int p = (t + 1024 * j) / SCC;             // < G: G * SCC = C8 = 1024 CPT
+      float v[8];
+      ld8_pairs(part64 + static_cast<int64_t>(p) * 4 * C8, C8, b * SCC + cc, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm[e] = fmaxf(sm[e], v[e]);
+    }
+  }
+  for (int o = SCC; o < kWave; o <<= 1)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sm[e] = fmaxf(sm[e], __shfl_xor(sm[e], o));
+  if (lane < SCC) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[(wave * SCC + lane) * 8 + e] = sm[e];
+  }
+  __syncthreads();
+  float inv_mine = 0.0f;                              // thread t < 8 SCC: column 8 (b SCC) + t
+  if (t < 8 * SCC) {
+    float mx = 0.0f;
+    for (int w = 0; w < kFusedBlock / kWave; ++w) mx = fmaxf(mx, red[(w * SCC + (t >> 3)) * 8 + (t & 7)]);
+    inv_mine = ok1 ? inv_scale(mx, eps, kQmaxInt8) : __builtin_nanf("");
+    // column 8 (b SCC + t / 8) + t % 8: plane (t % 8) / 2, half t % 2 of the pair
+    __hip_atomic_store(reinterpret_cast<unsigned int*>(inv64 + ((t & 7) >> 1) * C8 + b * SCC + (t >> 3)) +
+                           (t & 1),
+                       __float_as_uint(inv_mine), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  slot_publish(ctl, T2, true);
+  const int ok2 = slot_wait(ctl, T2, T2, spin_limit);
+  if (t == 0) {
+    int nan = !ok2;
+    if (ok2) {
+      const uint32_t sp = __hip_atomic_load(suspect, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (b == 0 || sp == T1 || sp == T2)
+        __hip_atomic_store(gen_w, static_cast<unsigned long long>(T2), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      nan = sp == T2;
+      if (b == 0 && sp != 0 && sp != T1 && sp != T2) {   // an earlier call's record
+        uint32_t expect = sp;
+        __hip_atomic_compare_exchange_strong(suspect, &expect, 0u, __ATOMIC_RELAXED,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    s_nan = nan;
+  }
+  __syncthreads();
+  if (t < 8 * SCC) scale_out[b * SCC * 8 + t] = s_nan ? __builtin_nanf("") : 1.0f / inv_mine;
+
+  // Pass 2: multipliers of the thread's chunk-columns, then the cast.
+  float iv[CPT][8];
+#pragma unroll
+  for (int s = 0; s < CPT; ++s) {
+    if (ok2) {
+      ld8_pairs(inv64, C8, t + 1024 * s, iv[s]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) iv[s][e] = __builtin_nanf("");
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < HS; ++k) {
+    const int64_t c0 = (held0 + k) * GS + cb;
+    const int64_t left = n8 - c0;
+    if (left > 0) {
+      const auto rs = rsrc(q + c0 * 8, (left < SB ? left : SB) * 8);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint2 c = cast8_cols<DT>(r[k * U + u], iv[u % CPT]);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, u32x2{c.x, c.y}), rs,
+                                              u * kFusedBlock * 8 + qo, 0,
+                                              CBQ_NT_STORES_NARROW ? kAuxNT : 0);
+      }
+    }
+  }
+  const int64_t parked = held0 < LS ? held0 : LS;
+  for (int64_t i = 0; i < parked; ++i) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const u32x4* pk = park + (static_cast<int>(i) * U + u) * QW * kFusedBlock + t;
+      Raw8<DT> v;
+      const u32x4 a = pk[0];
+      v.a = make_uint4(a.x, a.y, a.z, a.w);
+      if constexpr (DT == kF32) {
+        const u32x4 bb = pk[kFusedBlock];
+        v.b = make_uint4(bb.x, bb.y, bb.z, bb.w);
+      }
+      stg8(qw + (i * GS + u * kFusedBlock) * 8 + qo, cast8_cols<DT>(v, iv[u % CPT]));
+    }
+  }
+  for (int64_t i = parked; i < held0; ++i) {
+    Raw8<DT> v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = ld8_at<DT>(xw + (i * GS + u * kFusedBlock) * EB, xo);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      stg8(qw + (i * GS + u * kFusedBlock) * 8 + qo, cast8_cols<DT>(v[u], iv[u % CPT]));
   }
 }
 
@@ -1821,13 +2180,47 @@ ColGeom col_geom(int64_t rows, int64_t cols, bool vec) {
   return g;
 }
 
+// Grid of the one-launch column quant (k_quant_cols_1pass) for x of rows x
+// cols, or 0 when it does not apply: rows of 8192, 16384 or 32768 elements,
+// at least kColsMinElems elements, a power-of-two grid of at most one
+// workgroup per CU that splits the chunk-columns into slices of at most
+// kColsMaxSlice.
+int cols_1pass_grid(int64_t rows, int64_t cols) {
+  if (cols != 8192 && cols != 16384 && cols != 32768) return 0;
+  if (rows * cols < kColsMinElems) return 0;
+  int g = 1;
+  while (2 * g <= device_cus() && 2 * g <= kMaxFusedGrid) g *= 2;
+  const int64_t c8 = cols / 8;
+  if (c8 % g != 0 || c8 / g > kColsMaxSlice) return 0;
+  return g;
+}
+
+// True if one workgroup of k_quant_cols_1pass<DT, CPT> fits on a CU, so that
+// the whole grid is resident at once (cached per device and instantiation).
+template <int DT, int CPT>
+bool cols_1pass_fits() {
+  static int cached[64];   // 0 unknown, 1 fits, 2 does not
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  if (cached[dev] == 0) {
+    int nb = 0;
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &nb, reinterpret_cast<const void*>(&k_quant_cols_1pass<DT, CPT>), kFusedBlock, 0);
+    cached[dev] = (e == hipSuccess && nb >= 1) ? 1 : 2;
+  }
+  return cached[dev] == 1;
+}
+
 size_t col_ws_bytes(int64_t rows, int64_t cols) {
   // The byte count does not depend on the vector path: nrb is computed for
   // the smaller (vector) column-block count, which never yields fewer row
-  // blocks than the scalar path does.
+  // blocks than the scalar path does. The one-launch path needs one [cols]
+  // row of partial maxima per workgroup plus the [cols] multipliers.
   const ColGeom gv = col_geom(rows, cols, true);
   const ColGeom gs = col_geom(rows, cols, false);
-  const int64_t nrb = gv.nrb > gs.nrb ? gv.nrb : gs.nrb;
+  int64_t nrb = gv.nrb > gs.nrb ? gv.nrb : gs.nrb;
+  const int64_t g1 = cols_1pass_grid(rows, cols);
+  if (g1 > nrb) nrb = g1;
   return CBQ_WS_CTRL_BYTES + static_cast<size_t>(nrb) * cols * 4 + static_cast<size_t>(cols) * 4;
 }
 
@@ -1850,6 +2243,29 @@ template <int DT>
 int cols_quant_t(const void* x, int64_t rows, int64_t cols, int64_t inner, float eps, void* ws,
                  int8_t* q, float* scale, hipStream_t s, const char* what) {
   const bool vec = (cols % 8 == 0) && aligned(x, 16) && aligned(q, 8);
+  if (vec && inner == 1 && rows * cols * elem_bytes<DT>() <= CBQ_COLS_1PASS_MAX_BYTES) {
+    const int g1 = cols_1pass_grid(rows, cols);
+    const int cpt = static_cast<int>(cols / 8192);
+    if (g1 > 0 && (cpt == 1   ? cols_1pass_fits<DT, 1>()
+                   : cpt == 2 ? cols_1pass_fits<DT, 2>()
+                              : cols_1pass_fits<DT, 4>())) {
+      char* ctl = static_cast<char*>(ws);
+      float* part = reinterpret_cast<float*>(ctl + CBQ_WS_CTRL_BYTES);
+      float* invs = part + static_cast<int64_t>(g1) * cols;
+      const int64_t n8 = rows * cols / 8;
+      const dim3 grid(static_cast<unsigned>(g1)), blk(kFusedBlock);
+      if (cpt == 1)
+        k_quant_cols_1pass<DT, 1><<<grid, blk, 0, s>>>(x, n8, eps, q, scale, ctl, part, invs,
+                                                       fused_spin_limit());
+      else if (cpt == 2)
+        k_quant_cols_1pass<DT, 2><<<grid, blk, 0, s>>>(x, n8, eps, q, scale, ctl, part, invs,
+                                                       fused_spin_limit());
+      else
+        k_quant_cols_1pass<DT, 4><<<grid, blk, 0, s>>>(x, n8, eps, q, scale, ctl, part, invs,
+                                                       fused_spin_limit());
+      return launch_status(what);
+    }
+  }
   const ColGeom g = col_geom(rows, cols, vec);
   float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + CBQ_WS_CTRL_BYTES);
   float* inv = partial + g.nrb * cols;

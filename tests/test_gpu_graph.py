@@ -86,6 +86,25 @@ def test_graph_quant_dequant_per_tensor():
                    fn, g, out)
 
 
+def test_graph_per_column_one_launch_and_per_tensor():
+    """The one-launch per-column quant (two grid-wide exchanges through the
+    workspace's control block) and the one-launch per-tensor quant, sharing
+    that control block, captured in one graph: every replay's tags follow
+    the generation left in memory by the one before."""
+    from cublade_amd.quantization import dequantize_tensor, quantize_tensor
+    x = (0.02 * torch.randn(2048, 8192, generator=torch.Generator().manual_seed(4))).bfloat16().to(DEV)
+
+    def fn():
+        qc = quantize_tensor(x, dtype=torch.int8, mode="channel", ch_axis=1)
+        qt = quantize_tensor(x, dtype=torch.int8, mode="tensor")
+        return qc.data, qc.scale, qt.data, qt.scale, dequantize_tensor(qc)
+
+    g, out = _capture(fn, torch.cuda.Stream())
+    _check_replays(x, lambda i: ((0.5 + i) * torch.randn(2048, 8192, generator=torch.Generator()
+                                                         .manual_seed(40 + i))).bfloat16().to(DEV),
+                   fn, g, out)
+
+
 def test_graph_group_and_fp8():
     """Per-group INT8 (G = 128) and per-tensor FP8 in one graph."""
     from cublade_amd.quantization import dequantize_tensor, quantize_tensor

@@ -148,3 +148,73 @@ def test_forced_exchange_timeout_recovers_exactly():
     print(proc.stdout[-3000:], proc.stderr[-3000:], flush=True)
     assert proc.returncode == 0, proc.stderr[-3000:]
     assert "RECOVERY_OK" in proc.stdout
+
+
+CHILD_COLS = textwrap.dedent("""
+    import ctypes, sys
+    sys.path.insert(0, {root!r})
+    sys.path.insert(0, {root!r} + "/tests")
+    import numpy as np
+    import torch
+    import oracle
+    from cublade_amd import _abi
+    from _util import bits
+    L = _abi.lib()
+    dev = torch.device("cuda:0")
+    stream = _abi.stream_handle(dev)
+    g = torch.Generator().manual_seed(11)
+    R, C = 13000, 8192
+    x = (torch.randn(R, C, generator=g) * 0.05)
+    x[7, 5], x[12000, 6000] = 30.0, -25.0
+    x = x.to(torch.bfloat16)
+    qo, so = oracle.quant_int8_channel(bits(x), oracle.BF16, axis=1)
+    qo = np.asarray(qo).reshape(R, C)
+    so_bits = np.asarray(so, np.float32).view(np.uint32)
+    xd = x.to(dev)
+    ws = torch.zeros(L.cbq_quant_int8_channel_ws_bytes(R, C, 1), dtype=torch.uint8, device=dev)
+    def call():
+        q = torch.empty(R, C, dtype=torch.int8, device=dev)
+        s = torch.empty(C, dtype=torch.float32, device=dev)
+        _abi.check(L.cbq_quant_int8_channel(xd.data_ptr(), _abi.BF16, R, C, 1, ctypes.c_float(1e-12),
+                                            ws.data_ptr(), ws.numel(), q.data_ptr(), s.data_ptr(),
+                                            stream), "channel axis 1")
+        torch.cuda.synchronize()
+        return q.cpu().numpy(), s.cpu().numpy()
+    def status():
+        st = ctypes.c_int(-1)
+        _abi.check(L.cbq_tensor_quant_status(ws.data_ptr(), stream, ctypes.byref(st)), "status")
+        return st.value
+    q, s = call()
+    assert np.array_equal(q, qo) and np.array_equal(s.view(np.uint32), so_bits), "exact first"
+    default = _abi.set_tensor_spin_limit(0)
+    forced = 0
+    for _ in range(3):
+        q, s = call()
+        forced += status() == 1
+        finite = ~np.isnan(s)
+        # a column whose scale is not NaN has its exact scale and codes
+        assert np.array_equal(s.view(np.uint32)[finite], so_bits[finite]), "finite scale differs"
+        assert np.array_equal(q[:, finite], qo[:, finite]), "codes of a finite-scale column differ"
+    _abi.set_tensor_spin_limit(default)
+    print("  forced column calls that set status:", forced, flush=True)
+    assert status() == 1
+    for _ in range(2):
+        q, s = call()
+        assert np.array_equal(q, qo) and np.array_equal(s.view(np.uint32), so_bits), "after timeout"
+    _abi.check(L.cbq_tensor_quant_status_clear(ws.data_ptr(), stream), "clear")
+    assert status() == 0
+    print("COLS_RECOVERY_OK", flush=True)
+""")
+
+
+def test_forced_column_exchange_timeout_recovers_exactly():
+    """The one-launch per-column quant (two grid-wide exchanges) under a spin
+    limit of 0: the status word is set, every column whose scale is not NaN
+    has exact codes and scale, and the calls after it are exact."""
+    print("[timeout] column child process with the spin limit forced to 0", flush=True)
+    proc = subprocess.run([sys.executable, "-c", CHILD_COLS.format(root=str(ROOT))],
+                          env={**os.environ, "CUBLADE_SKIP_WARMUP": "1"},
+                          capture_output=True, text=True, timeout=180)
+    print(proc.stdout[-3000:], proc.stderr[-3000:], flush=True)
+    assert proc.returncode == 0, proc.stderr[-3000:]
+    assert "COLS_RECOVERY_OK" in proc.stdout
