@@ -1873,6 +1873,41 @@ int64_t planes_bytes(int64_t M, int64_t N, int64_t K) {
   return 2 * planes_x_bytes(M, K) + tiles * 2 * p.ks * (64 * p.tm) * 256 * 4;
 }
 
+// Workspace cap of the two-plane path: M is processed in chunks of rows
+// (multiples of 256, one after the other on the stream, reusing the
+// workspace) whose planes and partial tiles fit kPlanesMaxBytes (at M = 4096,
+// N = 11008, K = 4096 one launch would need 428 MB: two chunks of 2560 and
+// 1536 rows). A remainder of at most 64 rows joins the chunk before it, so
+// that every chunk keeps the plan of M > 64; chunks of 256 rows that alone
+// exceed the cap (very wide weights) are taken as they are.
+constexpr int64_t kPlanesMaxBytes = int64_t(256) << 20;
+
+int64_t planes_chunk_rows(int64_t M, int64_t N, int64_t K) {
+  if (planes_bytes(M, N, K) <= kPlanesMaxBytes) return M;
+  int64_t mc = 256;
+  while (mc + 256 < M && planes_bytes(mc + 256, N, K) <= kPlanesMaxBytes) mc += 256;
+  return mc;
+}
+
+// Rows of the chunk starting at m0.
+int64_t planes_chunk_at(int64_t m0, int64_t M, int64_t mc) {
+  const int64_t left = M - m0;
+  return left <= mc + 64 ? left : mc;
+}
+
+// Workspace of the two-plane path: the most any of its chunks needs (the
+// chunks of w8a16_f32_planes, walked the same way).
+int64_t planes_ws_bytes(int64_t M, int64_t N, int64_t K) {
+  const int64_t mc = planes_chunk_rows(M, N, K);
+  int64_t most = 0;
+  for (int64_t m0 = 0; m0 < M;) {
+    const int64_t mr = planes_chunk_at(m0, M, mc);
+    most = std::max(most, planes_bytes(mr, N, K));
+    m0 += mr;
+  }
+  return most;
+}
+
 template <int TM>
 void launch_planes(GemmArgs a, const PlanesPlan& p, const float* sc, const float* bias, float* y,
                    hipStream_t s) {
@@ -1894,30 +1929,35 @@ int w8a16_f32_planes(const void* x, const int8_t* wq, const void* scales, const 
                      int64_t n_out, int64_t M, int64_t N, int64_t K, void* ws, size_t ws_bytes,
                      void* y, hipStream_t s) {
   if (!planes_ok(M, N, K, n_out) || !ws || !aligned(x, 16) || !aligned(wq, 16) ||
-      ws_bytes < static_cast<size_t>(CBQ_WS_CTRL_BYTES + planes_bytes(M, N, K)))
+      ws_bytes < static_cast<size_t>(CBQ_WS_CTRL_BYTES + planes_ws_bytes(M, N, K)))
     return -1;
-  uint8_t* base = static_cast<uint8_t*>(ws) + CBQ_WS_CTRL_BYTES;
-  uint16_t* xh = reinterpret_cast<uint16_t*>(base);
-  uint16_t* xl = reinterpret_cast<uint16_t*>(base + planes_x_bytes(M, K));
-  const int64_t n4 = M * K / 4;   // K % 64 == 0
-  k_f32_planes<<<dim3(static_cast<unsigned>(cdiv(n4, static_cast<int64_t>(kBlock)))), dim3(kBlock),
-                 0, s>>>(static_cast<const float*>(x), n4, xh, xl);
-  GemmArgs a{};
-  a.x = xh;
-  a.x2 = xl;
-  a.wq = wq;
-  a.part = reinterpret_cast<float*>(base + 2 * planes_x_bytes(M, K));
-  a.M = static_cast<int>(M);
-  a.N = static_cast<int>(N);
-  a.K = static_cast<int>(K);
-  const float* sc = static_cast<const float*>(scales);
-  const float* bs = static_cast<const float*>(bias);
-  float* yo = static_cast<float*>(y);
-  const PlanesPlan p = planes_plan(M, N, K);
-  switch (p.tm) {
-    case 2: launch_planes<2>(a, p, sc, bs, yo, s); break;
-    case 3: launch_planes<3>(a, p, sc, bs, yo, s); break;
-    default: launch_planes<4>(a, p, sc, bs, yo, s); break;
+  const int64_t mc = planes_chunk_rows(M, N, K);
+  for (int64_t m0 = 0; m0 < M;) {
+    const int64_t mr = planes_chunk_at(m0, M, mc);
+    uint8_t* base = static_cast<uint8_t*>(ws) + CBQ_WS_CTRL_BYTES;
+    uint16_t* xh = reinterpret_cast<uint16_t*>(base);
+    uint16_t* xl = reinterpret_cast<uint16_t*>(base + planes_x_bytes(mr, K));
+    const int64_t n4 = mr * K / 4;   // K % 64 == 0
+    k_f32_planes<<<dim3(static_cast<unsigned>(cdiv(n4, static_cast<int64_t>(kBlock)))),
+                   dim3(kBlock), 0, s>>>(static_cast<const float*>(x) + m0 * K, n4, xh, xl);
+    GemmArgs a{};
+    a.x = xh;
+    a.x2 = xl;
+    a.wq = wq;
+    a.part = reinterpret_cast<float*>(base + 2 * planes_x_bytes(mr, K));
+    a.M = static_cast<int>(mr);
+    a.N = static_cast<int>(N);
+    a.K = static_cast<int>(K);
+    const float* sc = static_cast<const float*>(scales);
+    const float* bs = static_cast<const float*>(bias);
+    float* yo = static_cast<float*>(y) + m0 * N;
+    const PlanesPlan p = planes_plan(mr, N, K);
+    switch (p.tm) {
+      case 2: launch_planes<2>(a, p, sc, bs, yo, s); break;
+      case 3: launch_planes<3>(a, p, sc, bs, yo, s); break;
+      default: launch_planes<4>(a, p, sc, bs, yo, s); break;
+    }
+    m0 += mr;
   }
   return launch_status("cbq_w8a16_linear");
 }
@@ -2011,7 +2051,7 @@ extern "C" size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_
   const int64_t bytes =
       mfma ? splitk_bytes(M, N, split_plan(M, N, K), n_out)
       : (act_dtype == kF32 && planes_ok(M, N, K, n_out))
-          ? std::max(planes_bytes(M, N, K), general_split_bytes(M, N, K))
+          ? std::max(planes_ws_bytes(M, N, K), general_split_bytes(M, N, K))
           : general_split_bytes(M, N, K);
   return CBQ_WS_CTRL_BYTES + static_cast<size_t>(bytes);
 }

@@ -250,9 +250,13 @@ int cbq_dequant_int8_group_nd(const int8_t* q, const float* scale,
  * on MI355X), with n_out > 0 one more tile per tail tile for the outlier
  * side-GEMM block, else nothing. CBQ_F32 on the matrix-core path (see
  * cbq_w8a16_linear): two bf16 planes of x (4 M K bytes) and the fp32
- * partial tiles of both planes (8 bytes per output of the padded tiles; 360
- * MB at M = 4096, N = 11008; for M <= 64 times the k-ranges per plane, at
- * most 8: 32 MB at M = 16, N = 4096, K = 11008). Other CBQ_F32
+ * partial tiles of both planes (8 bytes per output of the padded tiles; for
+ * M <= 64 times the k-ranges per plane, at most 8: 32 MB at M = 16, N = 4096,
+ * K = 11008), capped at 256 MiB: a larger M runs in chunks of rows
+ * (multiples of 256, one after another, reusing the workspace), so the size
+ * is that of the largest chunk (M = 4096, N = 11008, K = 4096: chunks of 2560
+ * and 1536 rows, 241 MB instead of 428 MB; chunks of 256 rows that alone
+ * exceed the cap are used as they are). Other CBQ_F32
  * shapes and K % 16 != 0 (general kernel): fp32 partial sums, up to 16 x M x
  * N x 4 bytes when its tiles give fewer than two workgroups per CU. The
  * reference allocates its temporaries inside the forward (linear.py:105-131). */

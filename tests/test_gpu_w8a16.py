@@ -160,12 +160,14 @@ def test_general_path_fp32_tiles(M, K, N):
 
 @pytest.mark.parametrize("M,K,N", [(65, 64, 40), (300, 1024, 700), (1100, 256, 520),
                                    (2137, 2048, 8192), (16, 4096, 2048), (1, 8192, 1024),
-                                   (40, 2048, 4160), (64, 11008, 1024)])
+                                   (40, 2048, 4160), (64, 11008, 1024), (5160, 4096, 11008)])
 def test_fp32_two_plane_path(M, K, N):
     """fp32 activations with K % 64 == 0, no outlier columns and M > 64 (or
     M <= 64 with a weight of at least 8 MB, then K also split into up to 8
     ranges per plane) run on the matrix cores as two bf16 planes of x (hi
-    truncated, lo = bf16(x - hi)) against the int8 weights. Sampled rows
+    truncated, lo = bf16(x - hi)) against the int8 weights; M = 5160 at
+    N = 11008 exceeds the path's 256 MiB workspace cap and runs as chunks of
+    2560 and 2600 rows (the 40-row remainder joins the last chunk). Sampled rows
     against the oracle; the whole output against a float64 product within
     2^-14 of sum_k |x w s| (x keeps 16 significant bits; dropping the lo plane
     would leave only 8); with outlier columns the VALU kernel runs, also
