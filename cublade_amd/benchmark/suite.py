@@ -10,7 +10,7 @@ every quant (x read once, codes and scales written), N + 4 * scales read +
 FLOPs (int8 GEMMs against the 5.0 POP/s dense int8 peak, the fp32-activation
 W8A16 against the 157.3 TFLOP/s fp32 peak).
 
-    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5,c5m,c5o,c5f32,f1,f3,fx,f4,f4s [--json out.json]
+    python -m cublade_amd.benchmark.suite --configs c1,c2,c3,c3s,c4,c5,c5m,c5o,c5f32,f1,f3,fx,f4,f4s [--json out.json]
 
 fx is a set of shapes off the configs (odd group sizes, few long rows,
 narrow rows).
@@ -78,6 +78,17 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
         q_and_dq("c3", x, dict(dtype=torch.int8, mode="channel", ch_axis=1),
                  2 * n + n + 4 * F, n + 2 * n + 4 * F, "_axis1")
         del x
+    if "c3s" in selected:
+        # config 3's weight cut to 8192 and 16384 rows (128 / 256 MiB): the
+        # per-column (axis 1) quant then takes the one-launch path, x read once
+        full = configs.c3_int8_channel()
+        for rows in (8192, 16384):
+            x = full[:rows].contiguous().to(dev)
+            n, F = x.numel(), x.shape[1]
+            q_and_dq("c3s", x, dict(dtype=torch.int8, mode="channel", ch_axis=1),
+                     2 * n + n + 4 * F, n + 2 * n + 4 * F, f"_axis1_rows{rows}")
+            del x
+        del full
     if "c4" in selected:
         x = configs.c4_int8_group().to(dev)
         n = x.numel()
@@ -344,7 +355,7 @@ def run(selected, reps=20, warmup=3, flush_mode="clean"):
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,c5m,c5o,c5f32,f1,f3,fx,f4,f4s")
+    ap.add_argument("--configs", default="c1,c2,c3,c3s,c4,c5,c5m,c5o,c5f32,f1,f3,fx,f4,f4s")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--json", default=None)
