@@ -142,3 +142,31 @@ def test_cols_1pass_api(rows, cols, code):
 @pytest.mark.parametrize("rows,cols,code", [(13000, 8192, oracle.BF16), (2049, 32768, oracle.F16)])
 def test_cols_1pass_abi_repeated(rows, cols, code):
     check(rows, cols, code, seed=7 * rows + cols, via_api=False)
+
+
+@pytest.mark.parametrize("code", [oracle.BF16, oracle.F16, oracle.F32])
+def test_cols_1pass_special_values(code):
+    """NaN (ignored by the column maxima, encoded as 0), +-inf (a column
+    with inf gets scale inf and codes 0 / +-127 as the oracle defines), an
+    all-zero column (amax = 0: the eps floor), all-NaN and subnormal columns,
+    and -0, through the one-launch path ([2048, 8192]: 16M elements, held
+    steps only for 2-byte input, held + parked for fp32)."""
+    rows, cols = 2048, 8192
+    g = torch.Generator().manual_seed(77)
+    v = torch.randn(rows, cols, generator=g) * 0.1
+    v[5, 3] = float("nan")
+    v[1000, 3] = 2.0                       # the column's maximum despite the NaN
+    v[7, 11] = float("inf")
+    v[1500, 12] = -float("inf")
+    v[:, 20] = 0.0                         # all zero
+    v[:, 21] = float("nan")                # all NaN
+    v[:, 22] = 1e-7 if code == oracle.F16 else 1e-39   # subnormal in the input dtype
+    v[:, 23] = -0.0
+    v[2047, 8191] = -40.0                  # last element of x
+    xb = bits(v.to(TORCH[code]))
+    qo, so = oracle.quant_int8_channel(xb.reshape(rows, cols), code, axis=1)
+    from cublade_amd.quantization import quantize_tensor
+    qt = quantize_tensor(from_bits(xb.reshape(-1), code, "cuda").view(rows, cols),
+                         dtype=torch.int8, mode="channel", ch_axis=1)
+    assert_array_equal(bits(qt.data), qo, "codes")
+    assert_scales_equal(bits(qt.scale), so, "scales")
