@@ -264,8 +264,9 @@ def load_traffic():
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                                   "(the multi-GPU layout is described in DESIGN.md)"}))
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (the kernels "
+                                   "would shard by rows, groups or output columns, one process "
+                                   "per GPU)"}))
         sys.exit(2)
     import torch
 
