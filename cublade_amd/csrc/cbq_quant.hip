@@ -41,7 +41,7 @@
 //   k_quant_cols_1pass
 //                   per-column (axis 1) quant in one launch for rows of 8192,
 //                   16384 or 32768 elements and x of 2^22 elements up to
-//                   352 MiB: k_quant_tensor_1pass's step layout with running
+//                   480 MiB: k_quant_tensor_1pass's step layout with running
 //                   column maxima per thread, then two grid-wide exchanges
 //                   (partial column maxima; each workgroup's slice of
 //                   multipliers) and the cast from registers / LDS
@@ -543,9 +543,10 @@ __global__ __launch_bounds__(kFusedBlock) void k_quant_tensor_1pass(
 // t + 1024 (u % CPT), so each thread keeps the running |x| maxima of its CPT
 // chunk-columns (8 columns each). Then two grid-wide exchanges through the
 // workspace:
-//  1. every workgroup stores its [cols] partial maxima (part[b], as 4
-//     planes of float pairs: a wave's stores cover 512 contiguous bytes; with
-//     8-byte stores 32 bytes apart the exchange ran at under 1 TB/s) and
+//  1. every workgroup stores its [cols] partial maxima (part[b], in planes
+//     of 64-bit words: a wave's stores cover 512 contiguous bytes; with
+//     8-byte stores 32 bytes apart the exchange ran at under 1 TB/s; 16-bit
+//     values of the input dtype for 2-byte input, see st8_max) and
 //     publishes its slot with tag T1; once every slot carries T1 (or T2),
 //     workgroup b reduces the partials of its slice of c8 / G chunk-columns
 //     (<= 16) over all G workgroups, stores the slice's multipliers inv[c] =
@@ -570,13 +571,13 @@ constexpr int kColsMaxSlice = 16;   // chunk-columns per workgroup in the slice 
 constexpr int64_t kColsMinElems = int64_t(1) << 22;
 // Largest x (bytes) the one-launch column path takes; larger ones take
 // k_colmax + k_cast_cols. Measured on MI355X (bf16, cols 8192, op time after
-// a cache sweep, one-launch against two-pass): 64 MiB 36.5 / 37.8 us,
-// 128 MiB 51.4 / 62.4, 192 MiB 78.1 / 86.8, 256 MiB 105.0 / 112.2, 320 MiB
-// 132.0 / 135.2, 448 MiB 187.5 / 184.0 us: past what registers and LDS hold
-// (128 MiB) the re-read of the rest and the exchange cost what the single
-// read saves. A compile-time tuning knob.
+// a cache sweep, one-launch against two-pass, same process): 64 MiB 32.6 /
+// 37.8 us, 128 MiB 48.4 / 62.4, 256 MiB 101.6 / 112.2, 384 MiB 154.2 /
+// 159.3, 448 MiB 182.2 / 184.0, 576 MiB 235.7 / 232.9 us: past what
+// registers and LDS hold (128 MiB) the re-read of the rest and the exchange
+// cost about what the single read saves. A compile-time tuning knob.
 #ifndef CBQ_COLS_1PASS_MAX_BYTES
-#define CBQ_COLS_1PASS_MAX_BYTES (int64_t(352) << 20)
+#define CBQ_COLS_1PASS_MAX_BYTES (int64_t(480) << 20)
 #endif
 
 // Steps held in registers: those of k_quant_tensor_1pass, less what the CPT
@@ -611,6 +612,59 @@ __device__ __forceinline__ void st8_pairs(unsigned long long* p, int64_t plane, 
                        static_cast<unsigned long long>(__float_as_uint(v[2 * i])) |
                            (static_cast<unsigned long long>(__float_as_uint(v[2 * i + 1])) << 32),
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The column maxima of one chunk-column (8 columns) as they cross the
+// exchange: for 2-byte input as the input dtype's 16-bit values, 4 per
+// 64-bit word in 2 planes (each maximum is the absolute value of an input
+// element, so it is exact in that dtype; half the bytes of fp32), for fp32
+// input as fp32 pairs in 4 planes.
+template <int DT> constexpr int max_planes() { return DT == kF32 ? 4 : 2; }
+
+template <int DT>
+__device__ __forceinline__ uint32_t max_to16(float f) {
+  if constexpr (DT == kBF16) return __float_as_uint(f) >> 16;
+  else return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+template <int DT>
+__device__ __forceinline__ float max_from16(uint32_t h) {
+  if constexpr (DT == kBF16) return __uint_as_float(h << 16);
+  else return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+template <int DT>
+__device__ __forceinline__ void st8_max(unsigned long long* p, int64_t plane, int64_t c,
+                                        const float (&v)[8]) {
+  if constexpr (DT == kF32) {
+    st8_pairs(p, plane, c, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      unsigned long long w = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        w |= static_cast<unsigned long long>(max_to16<DT>(v[4 * i + j])) << (16 * j);
+      __hip_atomic_store(p + i * plane + c, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void ld8_max(const unsigned long long* p, int64_t plane, int64_t c,
+                                        float (&v)[8]) {
+  if constexpr (DT == kF32) {
+    ld8_pairs(p, plane, c, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const unsigned long long w =
+          __hip_atomic_load(p + i * plane + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        v[4 * i + j] = max_from16<DT>(static_cast<uint32_t>(w >> (16 * j)) & 0xffffu);
+    }
+  }
 }
 
 // Waits until every slot [0, G) carries tag or alt; after spin_limit polls
@@ -759,12 +813,14 @@ __global__ __launch_bounds__(kFusedBlock) void k_quant_cols_1pass(
 #pragma unroll
   for (int j = 0; j < HS * U; ++j) reload_barrier<DT>(r[j]);
 
-  // Exchange 1: this workgroup's partial maxima (part: [G][4 planes][C8]
-  // pairs), then tag T1.
+  // Exchange 1: this workgroup's partial maxima (part: [G][NP planes][C8]
+  // words), then tag T1.
+  constexpr int NP = max_planes<DT>();
   auto* part64 = reinterpret_cast<unsigned long long*>(part);
   auto* inv64 = reinterpret_cast<unsigned long long*>(invs);   // [4 planes][C8] pairs
 #pragma unroll
-  for (int s = 0; s < CPT; ++s) st8_pairs(part64 + static_cast<int64_t>(b) * 4 * C8, C8, t + 1024 * s, m[s]);
+  for (int s = 0; s < CPT; ++s)
+    st8_max<DT>(part64 + static_cast<int64_t>(b) * NP * C8, C8, t + 1024 * s, m[s]);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   const uint32_t T1 = s_t1, T2 = next_tag(T1);
@@ -785,7 +841,7 @@ __global__ __launch_bounds__(kFusedBlock) void k_quant_cols_1pass(
     for (int j = 0; j < CPT; ++j) {
       const int p = (t + 1024 * j) / SCC;             // < G: G * SCC = C8 = 1024 CPT
       float v[8];
-      ld8_pairs(part64 + static_cast<int64_t>(p) * 4 * C8, C8, b * SCC + cc, v);
+      ld8_max<DT>(part64 + static_cast<int64_t>(p) * NP * C8, C8, b * SCC + cc, v);
 #pragma unroll
       for (int e = 0; e < 8; ++e) sm[e] = fmaxf(sm[e], v[e]);
     }

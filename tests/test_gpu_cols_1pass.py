@@ -1,7 +1,7 @@
 """The one-launch per-column (axis 1) quant, against the oracle, bit for bit.
 
 k_quant_cols_1pass takes rows of 8192, 16384 or 32768 elements (x of 2^22
-elements up to 352 MiB, 16-byte aligned; larger x takes the two-pass path,
+elements up to 480 MiB, 16-byte aligned; larger x takes the two-pass path,
 which the full config-3 test covers): the per-tensor one-launch step layout
 (grid-wide steps of 2^23 elements on 256 CUs; the last HS steps of each
 thread held in registers, the first LS streamed ones parked in LDS, the
