@@ -554,8 +554,9 @@ __global__ __launch_bounds__(kFusedBlock) void k_quant_tensor_1pass(
 //  2. once every slot carries T2, every thread loads the multipliers of its
 //     chunk-columns and casts its held steps from registers, the parked ones
 //     from LDS, and re-reads the rest; workgroup b writes its slice's scales.
-// HBM traffic 2N (+ the re-read beyond 128 MiB) + N + the 4 G cols-byte
-// partials, against 2N + 2N + N for k_colmax + k_cast_cols.
+// HBM traffic 2N (+ the re-read beyond 128 MiB) + N + the partial maxima
+// (2 G cols bytes for 2-byte input, 4 G cols for fp32, each written and read
+// once), against 2N + 2N + N for k_colmax + k_cast_cols.
 //
 // Tags and timeouts follow the per-tensor exchange (the same control block:
 // gen, status, suspect, slots). T1 = gen + 1 and T2 = T1 + 1 (skipping 0);
