@@ -170,3 +170,36 @@ def test_cols_1pass_special_values(code):
                          dtype=torch.int8, mode="channel", ch_axis=1)
     assert_array_equal(bits(qt.data), qo, "codes")
     assert_scales_equal(bits(qt.scale), so, "scales")
+
+
+def _random_cases(n=6, seed=2024):
+    """Seeded random shapes that take the one-launch path: width 8192 /
+    16384 / 32768, a row count giving 2^22 elements up to ~320 MiB, any
+    dtype."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        cols = int(rng.choice([8192, 16384, 32768]))
+        code = int(rng.choice([oracle.BF16, oracle.F16, oracle.F32]))
+        eb = 4 if code == oracle.F32 else 2
+        lo, hi = (1 << 22) // cols, (320 << 20) // (cols * eb)
+        cases.append((int(rng.integers(lo, hi)), cols, code, int(rng.integers(1 << 30))))
+    return cases
+
+
+@pytest.mark.parametrize("rows,cols,code,seed", _random_cases())
+def test_cols_1pass_random(rows, cols, code, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(rows, cols, generator=g) * torch.exp(torch.randn(1, cols, generator=g))
+    k = max(1, cols // 1000)                # a few outlier columns at random rows
+    oc = torch.randperm(cols, generator=g)[:k]
+    orow = torch.randint(0, rows, (k,), generator=g)
+    x[orow, oc] *= 50.0
+    xb = bits(x.to(TORCH[code]))
+    print(f"[cols1 random] rows={rows} cols={cols} code={code} seed={seed}", flush=True)
+    qo, so = oracle.quant_int8_channel(xb.reshape(rows, cols), code, axis=1)
+    from cublade_amd.quantization import quantize_tensor
+    qt = quantize_tensor(from_bits(xb.reshape(-1), code, "cuda").view(rows, cols),
+                         dtype=torch.int8, mode="channel", ch_axis=1)
+    assert_array_equal(bits(qt.data), qo, "codes")
+    assert_scales_equal(bits(qt.scale), so, "scales")
