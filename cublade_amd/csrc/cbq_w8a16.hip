@@ -38,8 +38,9 @@
 // dma_plan picks the tile height and the split with a fitted time model.
 // Outlier columns run on the matrix cores too: per 16 columns the tile's
 // gathered x columns and w_out rows are staged in LDS in one round of loads,
-// then one rank-16 MFMA update per 32 x 32 block (onto the scaled
-// accumulators, or, in a split, into one more partial plane).
+// then one rank-16 MFMA update per 32 x 32 block onto the scaled
+// accumulators. Split tiles leave them to k_splitk_reduce, which stages the
+// same operands per workgroup and adds them per output.
 //
 // k_stream1<ACT> (M <= 16) and k_stream<ACT, TM> (M <= 64): persistent
 // weight streaming for large weights (see the kernels' comments).
@@ -704,10 +705,8 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
   const int mw = m0 + wm * TM * 32, nw = n0 + wn * 64;
   if (SPLIT && partial) {
     // Partial tile in lane order: f4 (split, tail tile, wave, i, j, q, lane),
-    // one contiguous 1 KiB store per (i, j, q); k_splitk_reduce finishes it.
-    // With outlier columns, the first k-range also stores the tile's
-    // side-GEMM block (matrix cores, see outlier_w_frag) as one more plane,
-    // after the `splits` planes, which the reduce adds after the scale.
+    // one contiguous 1 KiB store per (i, j, q); k_splitk_reduce finishes it
+    // (scale, outlier columns, bias).
     const int rest = a.tiles_m * a.tiles_n - a.full_tiles;
     f4* dst = reinterpret_cast<f4*>(a.part) +
               ((static_cast<int64_t>(split) * rest + ptile) * 8 + wave) * (TN * TM * 4 * 64) + lane;
@@ -719,43 +718,6 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
         for (int q = 0; q < 4; ++q)
           dst[((i * TM + j) * 4 + q) * 64] =
               f4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-    if (a.n_out > 0 && split == 0) {
-      // one block live at a time; later chunks add onto the stored plane
-      // (each lane re-reads only its own stores)
-      f4* od = reinterpret_cast<f4*>(a.part) +
-               ((static_cast<int64_t>(a.splits) * rest + ptile) * 8 + wave) * (TN * TM * 4 * 64) +
-               lane;
-      for (int c0 = 0; c0 < a.n_out; c0 += 16) {
-        __syncthreads();   // every wave is done with the operand stages / previous chunk
-        stage_outliers<ACT, BM>(a, m0, n0, c0, so);
-        __syncthreads();
-        u32x4 wf[TN];
-#pragma unroll
-        for (int i = 0; i < TN; ++i)
-          wf[i] = *reinterpret_cast<const u32x4*>(so + BM * 32 + (wn * 64 + i * 32 + r32) * 32 + h * 16);
-#pragma unroll
-        for (int j = 0; j < TM; ++j) {
-          const u32x4 xf =
-              *reinterpret_cast<const u32x4*>(so + (wm * TM * 32 + j * 32 + r32) * 32 + h * 16);
-#pragma unroll
-          for (int i = 0; i < TN; ++i) {
-            f4* o = od + ((i * TM + j) * 4) * 64;
-            f16x ob = f16x{};
-            if (c0 > 0) {
-#pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                const f4 v = o[q * 64];
-                ob[4 * q] = v[0]; ob[4 * q + 1] = v[1]; ob[4 * q + 2] = v[2]; ob[4 * q + 3] = v[3];
-              }
-            }
-            ob = mfma32x32x16<ACT>(wf[i], xf, ob);
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-              o[q * 64] = f4{ob[4 * q], ob[4 * q + 1], ob[4 * q + 2], ob[4 * q + 3]};
-          }
-        }
-      }
-    }
     return;
   }
   // Epilogue. Accumulator values 4q .. 4q+3 of tile (i, j) are the wave's
@@ -848,50 +810,80 @@ void launch_gemm_dma(GemmArgs a, hipStream_t s) {
 
 // Split-K finish: each thread takes two partial f4 of a tail tile, kBlock
 // apart (4 outputs y[m, n .. n+3] each); sums the splits in order
-// (deterministic), then scale, outliers, bias and one rounding, as in the
-// tile kernels' epilogue. Partial index, fastest first: lane (64), q (4),
+// (deterministic), then scale, outlier columns, bias and one rounding, as in
+// the tile kernels' epilogue. Partial index, fastest first: lane (64), q (4),
 // j (TM), i (2), wave (8), tail tile.
+//
+// Outlier columns (the OUTL instance): a workgroup's partial f4 all lie in
+// one wave's part of one tail tile (rows 32 TM, columns 64), so per 6
+// outlier columns it stages that part's x[m, oc[j]] and w_out[n, j] in LDS
+// (one independent load per thread and column, the indices oc[j] read as
+// scalars), issued before the partial planes' loads so that both latencies
+// overlap. The sum is then added per output in j order, onto the scaled
+// value (as outlier_quad does). Chunks of 6 columns keep the kernel within 64
+// VGPRs (8 waves per SIMD, every workgroup of M = 256, N = 11008 resident at
+// once; chunks of 16 needed 86 VGPRs and took two rounds: 14 against 8 us).
+// Measured at N = 11008, K = 4096, 6 columns: M = 256 45.4 against 50.4 us,
+// M = 128 33.0 against 37.8 us, where the first k-range used to store the
+// tail tile's side-GEMM block as one more partial plane for the reduce to
+// read (11 MB at M = 256), and per-quad global loads (outlier_quad) in the
+// reduce took 56.8 us.
 constexpr int kReduceF4 = 2;   // partial f4 per thread
 
-template <int ACT>
-__device__ __forceinline__ void splitk_finish(const GemmArgs& a, f4 sum, const f4* oplane,
-                                              int m, int nb) {
-  if (m >= a.M || nb >= a.N) return;
-  if (a.n_out > 0) {
-    // outlier block plane (after the `splits` planes): added after the scale
-    const f4 o = *oplane;
-    f4 v;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      v[r] = nb + r < a.N ? sum[r] * act_to_f32<ACT>(a.scales[nb + r]) + o[r] : 0.0f;
-    if (a.bias) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (nb + r < a.N) v[r] += act_to_f32<ACT>(a.bias[nb + r]);
-    }
-    uint16_t* dst = a.y + static_cast<int64_t>(m) * a.N + nb;
-    if ((a.N % 4) == 0 && nb + 3 < a.N) {
-      *reinterpret_cast<uint2*>(dst) = make_uint2(pack2_out<ACT>(v[0], v[1]),
-                                                  pack2_out<ACT>(v[2], v[3]));
-    } else {
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (nb + r < a.N) dst[r] = out1<ACT>(v[r]);
-    }
-    return;
-  }
-  store_quad<ACT>(a, sum, m, nb, (a.N % 4) == 0);
-}
-
-template <int ACT, int TM>
+template <int ACT, int TM, bool OUTL>   // OUTL: n_out > 0
 __global__ __launch_bounds__(kBlock) void k_splitk_reduce(GemmArgs a) {
   constexpr int kWaveF4 = kDmaTN * TM * 4 * 64;
   constexpr int kTileF4 = 8 * kWaveF4;
-  static_assert(kTileF4 % (kBlock * kReduceF4) == 0, "a thread's f4 share a tile");
+  constexpr int R = 32 * TM;           // rows of a wave's part
+  constexpr int OC = 6;                // outlier columns per staged chunk (see above)
+  static_assert(kWaveF4 % (kBlock * kReduceF4) == 0, "a workgroup's f4 share a wave's part");
+  static_assert(R + 64 <= kBlock, "one staging load per thread and column");
+  __shared__ float xs[OUTL ? OC : 1][R];     // x[mw + row, oc[c0 + c]]
+  __shared__ float wsh[OUTL ? OC : 1][64];   // w_out[nw + col, c0 + c]
   const int rest = a.tiles_m * a.tiles_n - a.full_tiles;
   const int64_t per_split = static_cast<int64_t>(rest) * kTileF4;
   const int64_t idx0 = static_cast<int64_t>(blockIdx.x) * (kBlock * kReduceF4) + threadIdx.x;
-  if (idx0 >= per_split) return;   // then every idx0 + u * kBlock is in range
+  // per_split is a multiple of the workgroup's span: uniform per workgroup
+  if (static_cast<int64_t>(blockIdx.x) * (kBlock * kReduceF4) >= per_split) return;
+  const int tid = threadIdx.x;
+  int tm, tn;
+  group_tile(a.full_tiles + static_cast<int>(idx0 / kTileF4), a, tm, tn);
+  const int wave = static_cast<int>((idx0 / kWaveF4) & 7);
+  const int mw = tm * 64 * TM + (wave & 1) * R;      // first row of the wave's part
+  const int nw = tn * 256 + (wave >> 1) * 64;        // first column
+
+  // Staging loads of outlier chunk c0 into registers: thread t < R loads
+  // x[mw + t, oc[c0 + c]], thread R <= t < R + 64 loads w_out[nw + t - R,
+  // c0 + c] (rows and columns clamped; an index outside [0, K) gives 0).
+  float sv[OC];
+  auto stage_load = [&](int c0) {
+    const int C = min(OC, a.n_out - c0);
+#pragma unroll
+    for (int c = 0; c < OC; ++c) {
+      sv[c] = 0.0f;
+      if (c < C) {
+        if (tid < R) {
+          const int64_t k = a.oc[c0 + c];
+          const bool ok = k >= 0 && k < a.K;
+          const int m = min(mw + tid, a.M - 1);
+          const float xv = act_to_f32<ACT>(a.x[static_cast<int64_t>(m) * a.K + (ok ? k : 0)]);
+          sv[c] = ok ? xv : 0.0f;
+        } else if (tid < R + 64) {
+          const int n = min(nw + tid - R, a.N - 1);
+          sv[c] = act_to_f32<ACT>(a.w_out[static_cast<int64_t>(n) * a.n_out + c0 + c]);
+        }
+      }
+    }
+  };
+  auto stage_store = [&]() {
+#pragma unroll
+    for (int c = 0; c < OC; ++c) {
+      if (tid < R) xs[c][tid] = sv[c];
+      else if (tid < R + 64) wsh[c][tid - R] = sv[c];
+    }
+  };
+  if constexpr (OUTL) stage_load(0);
+
   const f4* src = reinterpret_cast<const f4*>(a.part) + idx0;
   // planes summed in order 0, 1, ..., splits - 1 (deterministic); the loads
   // of up to 8 planes are issued before their adds (a plane at a time was
@@ -918,16 +910,65 @@ __global__ __launch_bounds__(kBlock) void k_splitk_reduce(GemmArgs a) {
 #pragma unroll
     for (int u = 0; u < kReduceF4; ++u) sum[u] += v[u];
   }
-  int tm, tn;
-  group_tile(a.full_tiles + static_cast<int>(idx0 / kTileF4), a, tm, tn);
+  int mr[kReduceF4], nr[kReduceF4];   // row / column offsets in the wave's part
 #pragma unroll
   for (int u = 0; u < kReduceF4; ++u) {
     const int w = static_cast<int>((idx0 + u * kBlock) % kWaveF4);
     const int lane = w & 63, q = (w >> 6) & 3, j = (w >> 8) % TM, i = (w >> 8) / TM;
-    const int wave = static_cast<int>(((idx0 + u * kBlock) / kWaveF4) & 7);
-    const int m = tm * 64 * TM + (wave & 1) * 32 * TM + j * 32 + (lane & 31);
-    const int nb = tn * 256 + (wave >> 1) * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
-    splitk_finish<ACT>(a, sum[u], src + a.splits * per_split + u * kBlock, m, nb);
+    mr[u] = j * 32 + (lane & 31);
+    nr[u] = i * 32 + 8 * q + 4 * (lane >> 5);
+  }
+  if constexpr (!OUTL) {
+#pragma unroll
+    for (int u = 0; u < kReduceF4; ++u) {
+      const int m = mw + mr[u], nb = nw + nr[u];
+      if (m < a.M && nb < a.N) store_quad<ACT>(a, sum[u], m, nb, (a.N % 4) == 0);
+    }
+    return;
+  }
+  f4 v[kReduceF4];
+#pragma unroll
+  for (int u = 0; u < kReduceF4; ++u) {
+    const int nb = nw + nr[u];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      v[u][r] = nb + r < a.N ? sum[u][r] * act_to_f32<ACT>(a.scales[nb + r]) : 0.0f;
+  }
+  for (int c0 = 0; c0 < a.n_out; c0 += OC) {
+    if (c0 > 0) {
+      __syncthreads();   // every thread has read the previous chunk
+      stage_load(c0);
+    }
+    stage_store();
+    __syncthreads();
+    const int C = min(OC, a.n_out - c0);
+    for (int c = 0; c < C; ++c) {
+#pragma unroll
+      for (int u = 0; u < kReduceF4; ++u) {
+        const float xv = xs[c][mr[u]];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[u][r] += xv * wsh[c][nr[u] + r];
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kReduceF4; ++u) {
+    const int m = mw + mr[u], nb = nw + nr[u];
+    if (m >= a.M || nb >= a.N) continue;
+    if (a.bias) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (nb + r < a.N) v[u][r] += act_to_f32<ACT>(a.bias[nb + r]);
+    }
+    uint16_t* dst = a.y + static_cast<int64_t>(m) * a.N + nb;
+    if ((a.N % 4) == 0 && nb + 3 < a.N) {
+      *reinterpret_cast<uint2*>(dst) = make_uint2(pack2_out<ACT>(v[u][0], v[u][1]),
+                                                  pack2_out<ACT>(v[u][2], v[u][3]));
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (nb + r < a.N) dst[r] = out1<ACT>(v[u][r]);
+    }
   }
 }
 
@@ -1023,12 +1064,11 @@ struct DmaPlan {
   int tm, full, splits;
 };
 
-// Bytes of split-K partials of a plan: one fp32 tile per tail tile and range,
-// plus one per tail tile for the outlier side-GEMM block when n_out > 0.
-int64_t splitk_bytes(int64_t M, int64_t N, const DmaPlan& p, int64_t n_out = 0) {
+// Bytes of split-K partials of a plan: one fp32 tile per tail tile and range.
+int64_t splitk_bytes(int64_t M, int64_t N, const DmaPlan& p) {
   if (p.splits <= 1) return 0;
   const int64_t tiles = cdiv(M, 64 * p.tm) * cdiv(N, 256);
-  return (tiles - p.full) * (p.splits + (n_out > 0 ? 1 : 0)) * (p.tm * 64) * 256 * 4;
+  return (tiles - p.full) * p.splits * (p.tm * 64) * 256 * 4;
 }
 
 template <int ACT, int TM>
@@ -1043,8 +1083,9 @@ void launch_gemm_dma_splitk(GemmArgs a, const DmaPlan& p, hipStream_t s) {
   const unsigned grid = static_cast<unsigned>(a.full_tiles + rest * a.splits);
   k_gemm_dma<ACT, true, TM><<<dim3(grid), dim3(kDmaThreads), 0, s>>>(a);
   const int64_t n4 = static_cast<int64_t>(rest) * 8 * kDmaTN * TM * 4 * 64;
-  k_splitk_reduce<ACT, TM><<<dim3(static_cast<unsigned>(cdiv(n4, kBlock * kReduceF4))),
-                             dim3(kBlock), 0, s>>>(a);
+  const dim3 rgrid(static_cast<unsigned>(cdiv(n4, kBlock * kReduceF4)));
+  if (a.n_out > 0) k_splitk_reduce<ACT, TM, true><<<rgrid, dim3(kBlock), 0, s>>>(a);
+  else k_splitk_reduce<ACT, TM, false><<<rgrid, dim3(kBlock), 0, s>>>(a);
 }
 
 // Small M (M <= 16 * TM): weight streaming. A workgroup owns 16 * TN weight
@@ -1757,7 +1798,7 @@ Kind choose(int64_t M, int64_t N, int64_t K, int64_t n_out, size_t ws_bytes, Dma
   if (!dma_ok(M, N, K)) return M < 1024 ? kTileMid : kTileLarge;
   plan = dma_plan(M, N, K, true);
   if (plan.splits > 1 &&
-      ws_bytes >= static_cast<size_t>(CBQ_WS_CTRL_BYTES + splitk_bytes(M, N, plan, n_out)))
+      ws_bytes >= static_cast<size_t>(CBQ_WS_CTRL_BYTES + splitk_bytes(M, N, plan)))
     return kTileDmaSplit;
   if (M <= 64) return narrow;
   if (M < 384) return kTileMid;
@@ -2049,7 +2090,7 @@ extern "C" size_t cbq_w8a16_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t n_
   // kernel; with this size it then runs without a split (same results).
   const bool mfma = (act_dtype == kF16 || act_dtype == kBF16) && K % 16 == 0;
   const int64_t bytes =
-      mfma ? splitk_bytes(M, N, split_plan(M, N, K), n_out)
+      mfma ? splitk_bytes(M, N, split_plan(M, N, K))
       : (act_dtype == kF32 && planes_ok(M, N, K, n_out))
           ? std::max(planes_ws_bytes(M, N, K), general_split_bytes(M, N, K))
           : general_split_bytes(M, N, K);

@@ -247,8 +247,7 @@ int cbq_dequant_int8_group_nd(const int8_t* q, const float* scale,
  * last wave of output tiles is short, the fp32 partial tiles of that wave
  * (ranges x tail tiles x 256 / 192 / 128 KiB for tiles of 256 / 192 / 128 x
  * 256; at most 16 ranges and at most one partial tile per CU, i.e. <= 64 MiB
- * on MI355X), with n_out > 0 one more tile per tail tile for the outlier
- * side-GEMM block, else nothing. CBQ_F32 on the matrix-core path (see
+ * on MI355X; the same with outlier columns), else nothing. CBQ_F32 on the matrix-core path (see
  * cbq_w8a16_linear): two bf16 planes of x (4 M K bytes) and the fp32
  * partial tiles of both planes (8 bytes per output of the padded tiles; for
  * M <= 64 times the k-ranges per plane, at most 8: 32 MB at M = 16, N = 4096,
