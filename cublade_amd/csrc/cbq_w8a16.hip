@@ -493,6 +493,14 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * SB];
   static_assert(kOutStageBytes <= NS * SB, "outlier stage fits in LDS");
   uint8_t* const so = smem;
+  // The tile's 256 scales and biases in fp32 (0 past N), loaded while the
+  // first stages' DMA is in flight, so that the epilogue reads them from LDS
+  // instead of waiting on global loads at the end of the tile (which cost
+  // 3-8 us per call at N = 11008, K = 4096: M = 512 / 768 / 1024 / 2048 /
+  // 3072 / 4096 took 56.3 / 73.9 / 92.2 / 173.0 / 247.5 / 323.4 us and take
+  // 53.3 / 71.0 / 89.1 / 167.1 / 242.0 / 315.3 us, bit-identical). Split
+  // tail tiles load them too and do not use them.
+  __shared__ float s_scale[256], s_bias[256];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -674,6 +682,14 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
 #pragma unroll
   for (int t = 0; t < NS; ++t)
     if (t < nk) issue(t, t);
+  if (!PLANES && tid < 256) {   // the two-plane launches carry no scales
+    const int n = n0 + tid;
+    const int nc = min(n, a.N - 1);
+    const float sv = act_to_f32<ACT>(a.scales[nc]);
+    const float bv = a.bias ? act_to_f32<ACT>(a.bias[nc]) : 0.0f;
+    s_scale[tid] = n < a.N ? sv : 0.0f;
+    s_bias[tid] = n < a.N ? bv : 0.0f;
+  }
   if (nk > 0) {
     if (nk > 2) dma_wait_barrier<2 * (XL + WL)>();
     else if (nk > 1) dma_wait_barrier<XL + WL>();
@@ -724,8 +740,8 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
   // outputs (m, n .. n+3) with m = 32 j + r32, n = 32 i + 8 q + 4 h. Each is
   // finished in fp32 (scale, outlier sum, bias, in that order), rounded once,
   // and written to an LDS copy of the wave's 32 TM x 64 output tile; the
-  // tile is then stored with 16-byte row-contiguous stores. The per-lane
-  // scales are loaded once, before any output store.
+  // tile is then stored with 16-byte row-contiguous stores. Scales and
+  // biases come from s_scale / s_bias.
   constexpr int EPS = 72;    // LDS row stride of the output tile (halfs)
   static_assert(8 * TM * 32 * EPS * 2 <= NS * SB, "epilogue tile fits in LDS");
   dma_wait_barrier<0>();     // every wave is done with the operand stages
@@ -741,8 +757,7 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
       for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int n = nw + i * 32 + 8 * q + 4 * h + r;
-          const float sc = n < a.N ? act_to_f32<ACT>(a.scales[n]) : 0.0f;
+          const float sc = s_scale[wn * 64 + i * 32 + 8 * q + 4 * h + r];
 #pragma unroll
           for (int j = 0; j < TM; ++j) acc[i][j][4 * q + r] *= sc;
         }
@@ -762,9 +777,8 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
       float sc[4], bs[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int n = nw + nl + r;
-        sc[r] = outl ? 1.0f : (n < a.N ? act_to_f32<ACT>(a.scales[n]) : 0.0f);   // x 1: exact
-        bs[r] = (a.bias && n < a.N) ? act_to_f32<ACT>(a.bias[n]) : 0.0f;
+        sc[r] = outl ? 1.0f : s_scale[wn * 64 + nl + r];   // x 1: exact
+        bs[r] = s_bias[wn * 64 + nl + r];
       }
 #pragma unroll
       for (int j = 0; j < TM; ++j) {
