@@ -896,6 +896,24 @@ __global__ __launch_bounds__(kBlock) void k_splitk_reduce(GemmArgs a) {
       else if (tid < R + 64) wsh[c][tid - R] = sv[c];
     }
   };
+  int mr[kReduceF4], nr[kReduceF4];   // row / column offsets in the wave's part
+#pragma unroll
+  for (int u = 0; u < kReduceF4; ++u) {
+    const int w = static_cast<int>((idx0 + u * kBlock) % kWaveF4);
+    const int lane = w & 63, q = (w >> 6) & 3, j = (w >> 8) % TM, i = (w >> 8) / TM;
+    mr[u] = j * 32 + (lane & 31);
+    nr[u] = i * 32 + 8 * q + 4 * (lane >> 5);
+  }
+  // The part's 64 scales and biases (fp32, 0 past N): loaded by the first
+  // 64 threads before the partial planes and read from LDS by the finish, so
+  // that it does not wait on global loads after the sums.
+  __shared__ float ssc[64], sbs[64];
+  float sc_t = 0.0f, bs_t = 0.0f;
+  if (tid < 64) {
+    const int n = min(nw + tid, a.N - 1);
+    sc_t = act_to_f32<ACT>(a.scales[n]);
+    bs_t = a.bias ? act_to_f32<ACT>(a.bias[n]) : 0.0f;
+  }
   if constexpr (OUTL) stage_load(0);
 
   const f4* src = reinterpret_cast<const f4*>(a.part) + idx0;
@@ -924,44 +942,35 @@ __global__ __launch_bounds__(kBlock) void k_splitk_reduce(GemmArgs a) {
 #pragma unroll
     for (int u = 0; u < kReduceF4; ++u) sum[u] += v[u];
   }
-  int mr[kReduceF4], nr[kReduceF4];   // row / column offsets in the wave's part
-#pragma unroll
-  for (int u = 0; u < kReduceF4; ++u) {
-    const int w = static_cast<int>((idx0 + u * kBlock) % kWaveF4);
-    const int lane = w & 63, q = (w >> 6) & 3, j = (w >> 8) % TM, i = (w >> 8) / TM;
-    mr[u] = j * 32 + (lane & 31);
-    nr[u] = i * 32 + 8 * q + 4 * (lane >> 5);
+  if (tid < 64) {
+    ssc[tid] = sc_t;
+    sbs[tid] = bs_t;
   }
-  if constexpr (!OUTL) {
-#pragma unroll
-    for (int u = 0; u < kReduceF4; ++u) {
-      const int m = mw + mr[u], nb = nw + nr[u];
-      if (m < a.M && nb < a.N) store_quad<ACT>(a, sum[u], m, nb, (a.N % 4) == 0);
-    }
-    return;
-  }
+  __syncthreads();
   f4 v[kReduceF4];
 #pragma unroll
   for (int u = 0; u < kReduceF4; ++u) {
     const int nb = nw + nr[u];
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      v[u][r] = nb + r < a.N ? sum[u][r] * act_to_f32<ACT>(a.scales[nb + r]) : 0.0f;
+      v[u][r] = nb + r < a.N ? sum[u][r] * ssc[nr[u] + r] : 0.0f;
   }
-  for (int c0 = 0; c0 < a.n_out; c0 += OC) {
-    if (c0 > 0) {
-      __syncthreads();   // every thread has read the previous chunk
-      stage_load(c0);
-    }
-    stage_store();
-    __syncthreads();
-    const int C = min(OC, a.n_out - c0);
-    for (int c = 0; c < C; ++c) {
+  if constexpr (OUTL) {
+    for (int c0 = 0; c0 < a.n_out; c0 += OC) {
+      if (c0 > 0) {
+        __syncthreads();   // every thread has read the previous chunk
+        stage_load(c0);
+      }
+      stage_store();
+      __syncthreads();
+      const int C = min(OC, a.n_out - c0);
+      for (int c = 0; c < C; ++c) {
 #pragma unroll
-      for (int u = 0; u < kReduceF4; ++u) {
-        const float xv = xs[c][mr[u]];
+        for (int u = 0; u < kReduceF4; ++u) {
+          const float xv = xs[c][mr[u]];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[u][r] += xv * wsh[c][nr[u] + r];
+          for (int r = 0; r < 4; ++r) v[u][r] += xv * wsh[c][nr[u] + r];
+        }
       }
     }
   }
@@ -971,8 +980,7 @@ __global__ __launch_bounds__(kBlock) void k_splitk_reduce(GemmArgs a) {
     if (m >= a.M || nb >= a.N) continue;
     if (a.bias) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (nb + r < a.N) v[u][r] += act_to_f32<ACT>(a.bias[nb + r]);
+      for (int r = 0; r < 4; ++r) v[u][r] += sbs[nr[u] + r];
     }
     uint16_t* dst = a.y + static_cast<int64_t>(m) * a.N + nb;
     if ((a.N % 4) == 0 && nb + 3 < a.N) {
