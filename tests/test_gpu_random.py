@@ -6,8 +6,11 @@ pointer is off the 16-byte grid (a contiguous slice of a larger buffer).
 Bar as in test_gpu_quant: bit-exact codes, scales and dequantized outputs
 (any NaN matches any NaN). The W8A16 part draws M, K, N, the activation
 dtype, bias and outlier columns and checks rtol = atol = 1e-2 against the
-oracle's exact accumulation. The cases are fixed by their seeds, so a
-failure names a reproducible case.
+oracle's exact accumulation; its streaming part draws the weight-streaming
+range (M <= 64, K a multiple of 1024, 8-64 MB of int8 weight), checks
+sampled rows against the oracle and every row against a float32 product on
+the GPU. The cases are fixed by their seeds, so a failure names a
+reproducible case.
 """
 from __future__ import annotations
 
@@ -161,3 +164,69 @@ def test_random_w8a16(i):
                               outlier_cols=np.asarray(oc, np.int64) if oc else None,
                               w_out=None if w_out is None else bits(w_out))
     np.testing.assert_allclose(y.float().cpu().numpy(), ref, rtol=1e-2, atol=1e-2)
+
+
+N_STREAM_CASES = 16
+
+
+def _stream_case(i):
+    """Shapes of the weight-streaming range: M <= 64, K a multiple of 1024
+    and a weight of 8-64 MB (k_stream1 / k_stream; K > 4096 also reaches
+    k_skinny and, for M > 24 with K > 8192, the split MFMA tile path)."""
+    rng = np.random.default_rng(9000 + i)
+    Ms = [1, 2, 3, 5, 8, 13, 16, 17, 24, 25, 31, 32, 33, 48, 49, 63, 64]
+    M = Ms[(3 * i) % len(Ms)]
+    K = [1024, 2048, 3072, 4096, 5120, 8192, 12288][i % 7]
+    n_min = -(-(8 << 20) // K)
+    N = int(rng.integers(n_min, max(n_min + 1, (64 << 20) // K)))
+    N -= N % int(rng.choice([1, 1, 16, 256]))
+    N = max(N, n_min)
+    dt = [torch.float16, torch.bfloat16][i % 2]
+    bias = bool(rng.integers(0, 2))
+    n_out = int(rng.choice([0, 0, 1, 2, 5]))
+    return M, K, N, dt, bias, n_out
+
+
+@pytest.mark.parametrize("i", range(N_STREAM_CASES))
+def test_random_w8a16_streaming(i):
+    """int8 codes drawn directly (uniform over [-127, 127]) with scales that
+    keep |y| near 1; four sampled rows against the oracle's exact
+    accumulation and every row against a float32 product of the dequantized
+    weight on the GPU, both at rtol = atol = 1e-2."""
+    from cublade_amd.bindings.hip import w8a16_linear
+    M, K, N, dt, bias, n_out = _stream_case(i)
+    print(f"[random w8a16 streaming {i}] M={M} K={K} N={N} dt={dt} bias={bias} "
+          f"n_out={n_out}", flush=True)
+    g = torch.Generator().manual_seed(11000 + i)
+    x = torch.randn(M, K, generator=g)
+    oc = sorted(torch.randperm(K, generator=g)[:n_out].tolist()) if n_out else []
+    if oc:
+        x[:, oc] = 10.0 * torch.sign(torch.randn(M, len(oc), generator=g))
+    wq = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    if oc:
+        wq[:, oc] = 0
+    s = ((0.5 + torch.rand(N, generator=g)) / (73.0 * K ** 0.5)).to(dt)
+    b = (0.1 * torch.randn(N, generator=g)).to(dt) if bias else None
+    w_out = (0.02 * torch.randn(N, len(oc), generator=g)).to(dt) if oc else None
+    xd = x.to(dt)
+    xg, wg, sg = xd.to(DEV), wq.to(DEV), s.to(DEV)
+    bg = None if b is None else b.to(DEV)
+    og = torch.tensor(oc, dtype=torch.int64, device=DEV) if oc else None
+    wog = None if w_out is None else w_out.to(DEV)
+    y = w8a16_linear(xg, wg, sg, bg, og, wog)
+    assert y.dtype == dt and tuple(y.shape) == (M, N)
+
+    rows = np.unique(np.array([0, M - 1, M // 2, (7 * i) % M], np.int64))
+    ref = oracle.w8a16_linear(bits(xd), CODE_OF[dt], wq.numpy(), bits(s),
+                              bias=None if b is None else bits(b),
+                              outlier_cols=np.asarray(oc, np.int64) if oc else None,
+                              w_out=None if w_out is None else bits(w_out), rows=rows)
+    np.testing.assert_allclose(y.float().cpu().numpy()[rows], ref, rtol=1e-2, atol=1e-2)
+
+    wf = wg.float() * sg.float()[:, None]
+    ref_all = xg.float() @ wf.t()
+    if oc:
+        ref_all += xg.float()[:, og] @ wog.float().t()
+    if bg is not None:
+        ref_all += bg.float()
+    torch.testing.assert_close(y.float(), ref_all, rtol=1e-2, atol=1e-2)
