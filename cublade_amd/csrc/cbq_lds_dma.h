@@ -10,12 +10,15 @@ namespace cbq {
 
 // LDS DMA of 16 bytes per lane: global sbase + voff -> LDS byte address lds +
 // 16 * lane (lds is wave-uniform). M0 carries the LDS address; it is saved
-// and restored inside the statement.
+// and restored inside the statement. An LDS DMA needs one wait state after
+// the write of M0 it reads (the s_nop; the compiler adds the same one to
+// its own M0 writes before such a load).
 __device__ __forceinline__ void lds_dma16(uint32_t voff, const void* sbase, uint32_t lds) {
   uint32_t saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
       "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
       "global_load_lds_dwordx4 %1, %2\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)

@@ -87,10 +87,23 @@ __device__ __forceinline__ void i8x4_to_act(uint32_t w, uint32_t& lo, uint32_t& 
     // keeps the other (exact: every int8 is an fp16). The compiler does not
     // form these selects from shifts and casts itself (it shifts each byte
     // first and packs the halves: 5 instructions per word instead of 4).
+    // Wait states the hardware needs and the compiler cannot insert inside
+    // the statement (it does not look into asm text):
+    // - a sub-dword (dst_sel WORD_n) write needs one before the next VALU
+    //   instruction that touches the register, and the preserving write of
+    //   the high half reads it: lo's and hi's writes alternate so that each
+    //   pair has one instruction between them;
+    // - an MFMA that reads a VGPR needs two after a VALU write of it. The
+    //   compiler counts the statement as a sub-dword write, not as a VALU: it
+    //   keeps one wait state (an s_nop 0 of its own, or any instruction)
+    //   between the statement and the next reader of lo / hi, whatever that
+    //   reader is. The closing s_nop 0 is the second one for an MFMA.
+    //   (Bit-identical outputs; 0.5% at M = 4096 against no wait.)
     asm("v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
-        "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
         "v_cvt_f16_i16_sdwa %1, sext(%2) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
-        "v_cvt_f16_i16_sdwa %1, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3"
+        "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
+        "v_cvt_f16_i16_sdwa %1, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3\n\t"
+        "s_nop 0"
         : "=&v"(lo), "=&v"(hi)
         : "v"(w));
   } else {
