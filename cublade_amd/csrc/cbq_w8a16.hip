@@ -36,6 +36,9 @@
 // over several k-ranges into fp32 partial tiles in the caller's workspace and
 // k_splitk_reduce sums them in a fixed order (no cross-workgroup fences);
 // dma_plan picks the tile height and the split with a fitted time model.
+// For 64 < M < 384, and wherever its one round of tiles is modelled faster
+// than a split, the same kernel runs 128 x 128 tiles instead (two waves
+// along M, four along N, one 32-row weight tile each): no partials at all.
 // Outlier columns run on the matrix cores too: per 16 columns the tile's
 // gathered x columns and w_out rows are staged in LDS in one round of loads,
 // then one rank-16 MFMA update per 32 x 32 block onto the scaled
@@ -465,41 +468,46 @@ constexpr int kDmaThreads = 512;   // 8 waves, two per SIMD
 constexpr int kDmaTN = 2;          // 32-row weight tiles per wave
 
 // acc[i][j] += the side-GEMM block of the staged chunk (see stage_outliers)
-// for the wave's weight rows 32 i .. of its 64 and x rows 32 j .. of its
-// 32 TM (the accumulator layout of k_gemm_dma).
-template <int ACT, int TM>
+// for the wave's weight rows 32 i .. of its 32 TN and x rows 32 j .. of its
+// 32 TM (the accumulator layout of k_gemm_dma; WM waves along M).
+template <int ACT, int TM, int TN, int WM>
 __device__ __forceinline__ void outlier_mfma(const uint8_t* so, int wm, int wn, int lane,
-                                             f16x (&acc)[kDmaTN][TM]) {
-  constexpr int BM = 64 * TM;
+                                             f16x (&acc)[TN][TM]) {
+  constexpr int BM = WM * 32 * TM;
   const int r32 = lane & 31, h = lane >> 5;
-  u32x4 wf[kDmaTN];
+  u32x4 wf[TN];
 #pragma unroll
-  for (int i = 0; i < kDmaTN; ++i)
-    wf[i] = *reinterpret_cast<const u32x4*>(so + BM * 32 + (wn * 64 + i * 32 + r32) * 32 + h * 16);
+  for (int i = 0; i < TN; ++i)
+    wf[i] = *reinterpret_cast<const u32x4*>(so + BM * 32 + (wn * 32 * TN + i * 32 + r32) * 32 + h * 16);
 #pragma unroll
   for (int j = 0; j < TM; ++j) {
     const u32x4 xf = *reinterpret_cast<const u32x4*>(so + (wm * TM * 32 + j * 32 + r32) * 32 + h * 16);
 #pragma unroll
-    for (int i = 0; i < kDmaTN; ++i) acc[i][j] = mfma32x32x16<ACT>(wf[i], xf, acc[i][j]);
+    for (int i = 0; i < TN; ++i) acc[i][j] = mfma32x32x16<ACT>(wf[i], xf, acc[i][j]);
   }
 }
 
-// TM: 32-row x tiles per wave; the workgroup tile is 64 TM x 256 (TM = 4:
-// 256 x 256; TM = 3 or 2: 192 or 128 x 256 for small M and for tile counts
-// that leave the last wave of workgroups short).
+// TM: 32-row x tiles per wave; TNW: 32-row weight tiles per wave; WM waves
+// along M and 8 / WM along N. The workgroup tile is 32 WM TM x 256 TNW /
+// WM: with the default TNW = WM = 2, 64 TM x 256 (TM = 4: 256 x 256; TM = 3
+// or 2: 192 or 128 x 256 for small M and for tile counts that leave the
+// last wave of workgroups short); TNW = 1 with TM = WM = 2 gives 128 x 128
+// (k_gemm_dma128).
 // SPLIT: workgroups [0, full_tiles) take whole tiles 0 .. full_tiles - 1;
 // the others split the remaining tiles over `splits` k-ranges, workgroup
 // full_tiles + b covering tail tile b % rest of k-range b / rest (after the
 // XCD renumbering, so the workgroups of one XCD share a k-range of x).
-template <int ACT, bool SPLIT, int TM, bool PLANES = false>
+template <int ACT, bool SPLIT, int TM, bool PLANES = false, int TNW = kDmaTN, int WM = 2>
 __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
-  constexpr int BM = 64 * TM, BN = 256, BK = 64, NS = 3;
+  constexpr int WN = 8 / WM;   // waves along N
+  constexpr int BM = WM * 32 * TM, BN = WN * 32 * TNW, BK = 64, NS = 3;
   constexpr int XB = BM * BK * 2;          // x stage bytes (32 / 24 / 16 KiB)
   constexpr int WB = BN * BK;              // weight stage bytes (16 KiB)
   constexpr int SB = XB + WB;
   constexpr int XL = XB / (kDmaThreads * 16);   // DMA instructions per thread: TM
-  constexpr int WL = WB / (kDmaThreads * 16);   // 2
-  constexpr int TN = kDmaTN;
+  constexpr int WL = WB / (kDmaThreads * 16);   // 2 (1 for 128 columns)
+  static_assert(!SPLIT || (TNW == kDmaTN && WM == 2), "k_splitk_reduce reads the default layout");
+  constexpr int TN = TNW;
   static_assert(TM >= 2 && TM <= 4, "x tile of 128, 192 or 256 rows");
   // operand stages; after the main loop the outlier staging area (at the
   // start) and the epilogue's output tiles
@@ -518,7 +526,7 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 1, wn = wave >> 1;   // 32 TM x rows, 64 weight rows
+  const int wm = wave % WM, wn = wave / WM;   // 32 TM x rows, 32 TN weight rows
   int tm, tn, split = 0, ptile = 0;
   bool partial = false;
   if constexpr (SPLIT) {
@@ -587,7 +595,7 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
 #pragma unroll
     for (int q = 0; q < 2; ++q)
       xr[e][q] = (wm * TM * 32 + r32) * 128 + (((4 * h + 2 * e + q) ^ ((r32 >> 1) & 7)) << 4);
-    wr[e] = XB + (wn * 64 + r32) * 64 + (((2 * h + e) ^ ((r32 >> 2) & 3)) << 4);
+    wr[e] = XB + (wn * 32 * TN + r32) * 64 + (((2 * h + e) ^ ((r32 >> 2) & 3)) << 4);
   }
 
   f16x acc[TN][TM];
@@ -636,15 +644,22 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
   // tile's widening (tile 0 of the next half after the last tile) and by
   // `extra` (DMA issue / fragment reads); sched_barrier pins the order.
   u32x4 wa[2], wb[2];   // widened weights: current and next tile
-  auto half = [&](Frags& f, Frags* fnext, auto&& extra) {
+  // With one weight tile per wave (TN = 1) the next set's tile is only read
+  // at the half's first slot: its words widen at slots 1, 2, ... (two at the
+  // last slot of a 4-MFMA half), and the buffers alternate per half (par).
+  auto half = [&](Frags& f, Frags* fnext, int par, auto&& extra) {
 #pragma unroll
     for (int i = 0; i < TN; ++i) {
-      u32x4 (&cur)[2] = (i & 1) ? wb : wa;
-      u32x4 (&nxt)[2] = (i & 1) ? wa : wb;
+      u32x4 (&cur)[2] = ((i + par) & 1) ? wb : wa;
+      u32x4 (&nxt)[2] = ((i + par) & 1) ? wa : wb;
 #pragma unroll
       for (int p = 0; p < 2 * TM; ++p) {
         mma_one(f, i, cur, p);
-        if (p < 4) {
+        if constexpr (TN == 1) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (fnext && (c + 1 < 2 * TM ? c + 1 : 2 * TM - 1) == p) cvt_word(*fnext, 0, c, nxt);
+        } else if (p < 4) {
           if (i + 1 < TN) cvt_word(f, i + 1, p, nxt);
           else if (fnext) cvt_word(*fnext, 0, p, nxt);
         }
@@ -672,20 +687,24 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
     constexpr int SC = decltype(sc)::value;
     const int stage_cur = SC >= 0 ? SC : t % NS;
     const int stage_next = SC >= 0 ? (SC + 1) % NS : (t + 1) % NS;
-    half(fr[0], &fr[1], [&](int i, int p) {
+    half(fr[0], &fr[1], 0, [&](int i, int p) {
       const int r = i * 2 * TM + p;
       if (r < 2 * TM + TN) read_one(stage_cur, 1, fr[1], r);
+      if (r == 2 * TM * TN - 1)   // reads past the MFMA slots (TN = 1)
+        for (int rr = r + 1; rr < 2 * TM + TN; ++rr) read_one(stage_cur, 1, fr[1], rr);
     });
     __builtin_amdgcn_sched_barrier(0);
     if (nwait >= 1) dma_wait_barrier<XL + WL>();
     else dma_wait_barrier<0>();
     __builtin_amdgcn_sched_barrier(0);
-    half(fr[1], &fr[0], [&](int i, int p) {
+    half(fr[1], &fr[0], TN & 1, [&](int i, int p) {
       const int r = i * 2 * TM + p;
       if constexpr (decltype(dma)::value) {
         if (r < XL + WL) issue_one(t + NS, stage_cur, r);
       }
       if (r < 2 * TM + TN) read_one(stage_next, 0, fr[0], r);
+      if (r == 2 * TM * TN - 1)
+        for (int rr = r + 1; rr < 2 * TM + TN; ++rr) read_one(stage_next, 0, fr[0], rr);
     });
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -724,14 +743,16 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
     }
     for (; t + NS < nk; ++t) step(t, yes{}, 1, SR{});
     for (; t + 1 < nk; ++t) step(t, no{}, nk - 2 - t, SR{});
-    half(fr[0], &fr[1], [&](int i, int p) {
+    half(fr[0], &fr[1], 0, [&](int i, int p) {
       const int r = i * 2 * TM + p;
       if (r < 2 * TM + TN) read_one((nk - 1) % NS, 1, fr[1], r);
+      if (r == 2 * TM * TN - 1)
+        for (int rr = r + 1; rr < 2 * TM + TN; ++rr) read_one((nk - 1) % NS, 1, fr[1], rr);
     });
-    half(fr[1], nullptr, [&](int, int) {});
+    half(fr[1], nullptr, TN & 1, [&](int, int) {});
   }
 
-  const int mw = m0 + wm * TM * 32, nw = n0 + wn * 64;
+  const int mw = m0 + wm * TM * 32, nw = n0 + wn * 32 * TN;
   if (SPLIT && partial) {
     // Partial tile in lane order: f4 (split, tail tile, wave, i, j, q, lane),
     // one contiguous 1 KiB store per (i, j, q); k_splitk_reduce finishes it
@@ -755,7 +776,7 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
   // and written to an LDS copy of the wave's 32 TM x 64 output tile; the
   // tile is then stored with 16-byte row-contiguous stores. Scales and
   // biases come from s_scale / s_bias.
-  constexpr int EPS = 72;    // LDS row stride of the output tile (halfs)
+  constexpr int EPS = 32 * TN + 8;   // LDS row stride of the output tile (halfs)
   static_assert(8 * TM * 32 * EPS * 2 <= NS * SB, "epilogue tile fits in LDS");
   dma_wait_barrier<0>();     // every wave is done with the operand stages
   uint16_t* ep = reinterpret_cast<uint16_t*>(smem) + wave * (TM * 32 * EPS);
@@ -770,7 +791,7 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
       for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float sc = s_scale[wn * 64 + i * 32 + 8 * q + 4 * h + r];
+          const float sc = s_scale[wn * 32 * TN + i * 32 + 8 * q + 4 * h + r];
 #pragma unroll
           for (int j = 0; j < TM; ++j) acc[i][j][4 * q + r] *= sc;
         }
@@ -778,7 +799,7 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
       if (c0 > 0) __syncthreads();   // every wave has read the previous chunk
       stage_outliers<ACT, BM>(a, m0, n0, c0, so);
       __syncthreads();
-      outlier_mfma<ACT, TM>(so, wm, wn, lane, acc);
+      outlier_mfma<ACT, TM, TN, WM>(so, wm, wn, lane, acc);
     }
     __syncthreads();   // the output tiles below overwrite the stage
   }
@@ -790,8 +811,8 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
       float sc[4], bs[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        sc[r] = outl ? 1.0f : s_scale[wn * 64 + nl + r];   // x 1: exact
-        bs[r] = s_bias[wn * 64 + nl + r];
+        sc[r] = outl ? 1.0f : s_scale[wn * 32 * TN + nl + r];   // x 1: exact
+        bs[r] = s_bias[wn * 32 * TN + nl + r];
       }
 #pragma unroll
       for (int j = 0; j < TM; ++j) {
@@ -807,11 +828,13 @@ __global__ __launch_bounds__(kDmaThreads) void k_gemm_dma(GemmArgs a) {
       }
     }
   }
-  // Row-contiguous stores: 8 lanes cover one 64-wide row (8 outputs each).
+  // Row-contiguous stores: 4 TN lanes cover one 32 TN-wide row (8 outputs
+  // each).
   const bool vec16 = (a.N % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
+  constexpr int LR = 4 * TN;
 #pragma unroll 4
-  for (int u = 0; u < 4 * TM; ++u) {
-    const int row = u * 8 + (lane >> 3), c8 = (lane & 7) * 8;
+  for (int u = 0; u < 2 * TM * TN; ++u) {
+    const int row = u * (64 / LR) + lane / LR, c8 = (lane % LR) * 8;
     const int m = mw + row, n = nw + c8;
     if (m >= a.M || n >= a.N) continue;
     const u32x4 val = *reinterpret_cast<const u32x4*>(&ep[row * EPS + c8]);
@@ -833,6 +856,16 @@ void launch_gemm_dma(GemmArgs a, hipStream_t s) {
   a.tiles_n = static_cast<int>(cdiv(a.N, 256));
   const unsigned grid = static_cast<unsigned>(a.tiles_m) * a.tiles_n;
   k_gemm_dma<ACT, false, TM><<<dim3(grid), dim3(kDmaThreads), 0, s>>>(a);
+}
+
+// 128 x 128 tiles, whole (k_gemm_dma128): 98 VGPRs and 74 KiB of LDS, so two
+// workgroups fit a CU.
+template <int ACT>
+void launch_gemm_dma128(GemmArgs a, hipStream_t s) {
+  a.tiles_m = static_cast<int>(cdiv(a.M, 128));
+  a.tiles_n = static_cast<int>(cdiv(a.N, 128));
+  const unsigned grid = static_cast<unsigned>(a.tiles_m) * a.tiles_n;
+  k_gemm_dma<ACT, false, 2, false, 1, 2><<<dim3(grid), dim3(kDmaThreads), 0, s>>>(a);
 }
 
 // Split-K finish: each thread takes two partial f4 of a tail tile, kBlock
@@ -1735,13 +1768,15 @@ __global__ __launch_bounds__(kBlock) void k_general_reduce(GenArgs a) {
 //                 the last, short wave of tiles split over K (2-16 k-ranges,
 //                 partial tiles in the workspace, k_splitk_reduce) when the
 //                 time model prefers it and the caller's workspace holds the
-//                 partials;
-//   64 < M < 384  else (no workspace, or no k_gemm_dma) k_gemm 128 x 64 x 64,
-//                 2 x 2 waves
-//   M >= 384      else k_gemm_dma without a split; else k_gemm 256 x 256 x
-//                 64, 4 x 2 waves
+//                 partials, unless one round of 128 x 128 tiles
+//                 (k_gemm_dma128, no partials) is modelled faster;
+//   64 < M < 384  else k_gemm_dma128; without k_gemm_dma (K % 64 != 0 or
+//                 offsets past 32 bits) k_gemm 128 x 64 x 64, 2 x 2 waves
+//   M >= 384      else k_gemm_dma without a split, or k_gemm_dma128 where
+//                 modelled faster; without k_gemm_dma k_gemm 256 x 256 x 64,
+//                 4 x 2 waves (M < 1024: 128 x 64 x 64)
 enum Kind { kSkinny1, kSkinny2, kSkinny4, kTileMid, kTileLarge, kTileDma, kStream1, kStream2,
-            kStream4, kTileDmaSplit };
+            kStream4, kTileDmaSplit, kTileDma128 };
 
 // The streaming kernels pay a fixed cost for their large workgroups; below
 // 8 MB of weight the k_skinny kernels are faster.
@@ -1778,7 +1813,7 @@ int64_t dma_step_cost(int tm, int64_t wgs, int64_t cus) {
   return 84 + 28 * busy / cus;
 }
 
-DmaPlan dma_plan(int64_t M, int64_t N, int64_t K, bool allow_split) {
+DmaPlan dma_plan(int64_t M, int64_t N, int64_t K, bool allow_split, int64_t* cost = nullptr) {
   const int64_t cus = device_cus(), nk = K / 64;
   DmaPlan best{4, 0, 1};
   int64_t best_cost = INT64_MAX;
@@ -1802,7 +1837,27 @@ DmaPlan dma_plan(int64_t M, int64_t N, int64_t K, bool allow_split) {
       }
     }
   }
+  if (cost) *cost = best_cost;
   return best;
+}
+
+// Modelled time of the 128 x 128 tiles (k_gemm_dma128) on dma_plan's scale,
+// for M > 64 when the tiles fit one workgroup per CU, else no estimate:
+// 6.9 us plus (0.41 + 0.17 x share of CUs busy) us per 64-k step, as timed
+// on MI355X (op level, fp16) over M = 128..256, N = 8192..28672,
+// K = 2048..8192, times the 1.13 by which dma_plan's model exceeds the
+// measured time of its split plans at those shapes. Measured against the
+// plans it displaces (op level): M = 256, N = 11008, K = 4096 39.7 against
+// 41.6 us (split 128 x 256 tiles); N = 14336 41.8 against 46.9; N = 16384
+// 44.4 against 54.2; M = 128, N = 28672 48.2 against 55.6; K = 2048 23.3
+// against 47.2 (no split: k_gemm). It loses where a split keeps more CUs busy
+// for fewer steps (K = 8192: 67.7 against 64.4; M = 160: 39.4 against 37.0;
+// N = 4096, K = 11008: 95 against 40), which the model leaves to the split.
+int64_t dma128_cost(int64_t M, int64_t N, int64_t K) {
+  const int64_t cus = device_cus();
+  const int64_t tiles = cdiv(M, 128) * cdiv(N, 128);
+  if (M <= 64 || tiles > cus) return INT64_MAX;
+  return 780 + (K / 64) * (46 + 19 * tiles / cus);
 }
 
 // Whether k_gemm_dma is a candidate: M > 64, or 24 < M <= 64 with K above
@@ -1815,10 +1870,14 @@ bool dma_candidate(int64_t M, int64_t N, int64_t K) {
   return (M > 64 || (M > 24 && K > 8 * stream_kc<4>())) && dma_ok(M, N, K);
 }
 
-// The split plan when it applies, else none.
+// The split plan when it applies (and the 128 x 128 tiles are not modelled
+// faster), else none.
 DmaPlan split_plan(int64_t M, int64_t N, int64_t K) {
   if (!dma_candidate(M, N, K)) return DmaPlan{4, 0, 1};
-  return dma_plan(M, N, K, true);
+  int64_t cost = 0;
+  const DmaPlan p = dma_plan(M, N, K, true, &cost);
+  if (p.splits > 1 && dma128_cost(M, N, K) < cost) return DmaPlan{4, 0, 1};
+  return p;
 }
 
 Kind choose(int64_t M, int64_t N, int64_t K, int64_t n_out, size_t ws_bytes, DmaPlan& plan) {
@@ -1831,14 +1890,19 @@ Kind choose(int64_t M, int64_t N, int64_t K, int64_t n_out, size_t ws_bytes, Dma
                               : ((stream && tiles_fit) ? kStream4 : kSkinny4);
   if (M <= 64 && !dma_candidate(M, N, K)) return narrow;
   if (!dma_ok(M, N, K)) return M < 1024 ? kTileMid : kTileLarge;
-  plan = dma_plan(M, N, K, true);
+  int64_t cost = 0;
+  plan = dma_plan(M, N, K, true, &cost);
+  const int64_t cost128 = dma128_cost(M, N, K);
   if (plan.splits > 1 &&
       ws_bytes >= static_cast<size_t>(CBQ_WS_CTRL_BYTES + splitk_bytes(M, N, plan)))
-    return kTileDmaSplit;
+    return cost128 < cost ? kTileDma128 : kTileDmaSplit;
   if (M <= 64) return narrow;
-  if (M < 384) return kTileMid;
-  plan = dma_plan(M, N, K, false);
-  return kTileDma;
+  // no split below 384 rows: the 128 x 128 tiles (measured 2x faster than
+  // k_gemm's 128 x 64 tiles there: 40.0 against 78.5 us at M = 256,
+  // N = 11008, K = 4096; 38.4 against 74.2 us at M = 128, N = K = 4096)
+  if (M < 384) return kTileDma128;
+  plan = dma_plan(M, N, K, false, &cost);
+  return cost128 < cost ? kTileDma128 : kTileDma;
 }
 
 template <int ACT, int BM, int BN, int BK, int WGM, int WGN, int PD>
@@ -1864,6 +1928,7 @@ void launch_kind(Kind k, const GemmArgs& a, const DmaPlan& p, hipStream_t s) {
       else if (p.tm == 3) launch_gemm_dma<ACT, 3>(a, s);
       else launch_gemm_dma<ACT, 4>(a, s);
       break;
+    case kTileDma128: launch_gemm_dma128<ACT>(a, s); break;
     case kTileDmaSplit:
       if (p.tm == 2) launch_gemm_dma_splitk<ACT, 2>(a, p, s);
       else if (p.tm == 3) launch_gemm_dma_splitk<ACT, 3>(a, p, s);

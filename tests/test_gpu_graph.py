@@ -141,8 +141,8 @@ def test_graph_workspace_survives_growth():
         ws1 = _abi.workspace(x.device, 0)
     ptr1, size1 = ws1.data_ptr(), ws1.numel()
     del ws1
-    # M = 256, N = 11008: split-K partials, a workspace far larger than size1
-    N, K, M = 11008, 4096, 256
+    # M = 128, N = 11008: split-K partials, a workspace far larger than size1
+    N, K, M = 11008, 4096, 128
     layer = cuBladeW8A16LinearLayer(K, N, bias=False, dtype=torch.float16)
     layer.quantize((0.02 * torch.randn(N, K, generator=torch.Generator().manual_seed(4)))
                    .half().to(DEV))

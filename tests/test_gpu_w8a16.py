@@ -297,11 +297,17 @@ def test_splitk_large_m_few_tiles(M, K, N):
     (64, 11008, 4096, torch.float16, 2, "M <= 64 with long K: 128-row tiles over 11 ranges"),
     (32, 11008, 4096, torch.bfloat16, 1, "M = 32 with long K: 128-row tiles over 11 ranges"),
     (40, 16384, 1000, torch.bfloat16, 0, "M <= 64 with long K, N tail"),
+    (256, 4096, 11008, torch.float16, 6, "128 x 128 tiles in one round (config 5, M = 256)"),
+    (250, 2048, 14336, torch.bfloat16, 17, "128 x 128 tiles, M tail, two outlier chunks"),
+    (96, 4096, 28672, torch.float16, 0, "128 x 128 tiles, one row of tiles"),
+    (256, 3072, 14330, torch.float16, 1, "128 x 128 tiles, N tail (element stores)"),
+    (383, 2048, 5000, torch.bfloat16, 3, "128 x 128 tiles, M and N tails"),
+    (130, 2048, 28672, torch.float16, 0, "128 x 128 tiles, two rounds' worth (no split below 384 rows)"),
 ])
 def test_dma_plans(M, K, N, dt, n_out, path):
     """Each x-tile height (128, 192, 256 rows) and split plan of the MFMA tile
     path (whole tiles, all tiles over k-ranges, full waves whole plus a split
-    tail; the host's time model picks them per shape): sampled rows against
+    tail, 128 x 128 tiles; the host's time model picks them per shape): sampled rows against
     the oracle, the full output against an fp32 product of the same operands
     (GPU matmul, independent of the kernel's tiling), and against the same
     call with a control-block workspace (no split)."""

@@ -112,10 +112,14 @@ def test_workspace_sizes():
     # a weight under 8 MB keeps the general kernel at M <= 64
     assert L.cbq_w8a16_ws_bytes(16, 1024, 4096, 0, F32) == C + 16 * 16 * 1024 * 4
     assert L.cbq_w8a16_ws_bytes(4096, 11008, 4096, 0, F16) == C
-    # split-K tile path, 256 CUs (also the CPU-only fallback count): 2 k-ranges
-    # x 86 tiles of 128 x 256 (128 KiB of fp32 partials each)
-    assert L.cbq_w8a16_ws_bytes(256, 11008, 4096, 0, F16) == C + 2 * 86 * 128 * 1024
-    assert L.cbq_w8a16_ws_bytes(256, 11008, 4096, 0, _abi.BF16) == C + 2 * 86 * 128 * 1024
+    # split-K tile path, 256 CUs (also the CPU-only fallback count): 4 k-ranges
+    # x 43 tiles of 128 x 256 (128 KiB of fp32 partials each)
+    assert L.cbq_w8a16_ws_bytes(128, 11008, 4096, 0, F16) == C + 4 * 43 * 128 * 1024
+    assert L.cbq_w8a16_ws_bytes(128, 11008, 4096, 0, _abi.BF16) == C + 4 * 43 * 128 * 1024
+    # M = 256: one round of 172 tiles of 128 x 128 is modelled faster than 2
+    # k-ranges x 86 tiles of 128 x 256, and needs no partials
+    assert L.cbq_w8a16_ws_bytes(256, 11008, 4096, 0, F16) == C
+    assert L.cbq_w8a16_ws_bytes(256, 11008, 4096, 6, _abi.BF16) == C
     assert L.cbq_w8a16_ws_bytes(512, 11008, 4096, 3, F16) == C      # 172 whole 128-row tiles
     assert L.cbq_w8a16_ws_bytes(256, 11008, 4000, 0, F16) == C      # K % 64 != 0
     # few tiles (the MLP down projection): 8 k-ranges x 32 tiles of 128 x 256,
