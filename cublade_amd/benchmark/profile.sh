@@ -133,14 +133,14 @@ if want suite; then
     $R counters "$RAW/mfma/suite_results.db" | grep -E "k_gemm_dma|k_stream|k_skinny|k_gemm<|k_mm_dma|Cijk"
     echo
     echo "# dispatches by W8A16 shape (N = 11008, K = 4096, config-5 operands; order: c5 then c5m):"
-    echo "#   M = 16    k_stream1<1, 3>                 (weight streaming, HBM-bound)"
-    echo "#   M = 256   k_gemm_dma<1, true, 2, false>   (128-row tiles, K in 2 ranges, 172 of 256 CUs)"
-    echo "#   M = 768   k_gemm_dma<1, false, 3, false>  first 4 values (172 tiles of 192 rows, one wave)"
-    echo "#   M = 1536  k_gemm_dma<1, true, 4, false>   first 4 values (256 tiles whole + 2 over 16 ranges)"
-    echo "#   M = 4096  k_gemm_dma<1, false, 4, false>  first 4 values (688 tiles, 2.69 waves)"
-    echo "#   M = 1024  k_gemm_dma<1, false, 4, false>  last 4 values (172 tiles of 256 rows, one wave)"
-    echo "#   M = 2048  k_gemm_dma<1, false, 3, false>  last 4 values (473 tiles of 192 rows)"
-    echo "#   M = 3072  k_gemm_dma<1, true, 4, false>   last 4 values (512 tiles whole + the tail split)"
+    echo "#   M = 16    k_stream1<1, 3>                          (weight streaming, HBM-bound)"
+    echo "#   M = 256   k_gemm_dma<1, false, 2, false, 1, 2>     (172 tiles of 128 x 128, one round, no split)"
+    echo "#   M = 768   k_gemm_dma<1, false, 3, false, 2, 2>     first 4 values (172 tiles of 192 rows, one wave)"
+    echo "#   M = 1536  k_gemm_dma<1, true, 4, false, 2, 2>      first 4 values (256 tiles whole + 2 over 16 ranges)"
+    echo "#   M = 4096  k_gemm_dma<1, false, 4, false, 2, 2>     first 4 values (688 tiles, 2.69 waves)"
+    echo "#   M = 1024  k_gemm_dma<1, false, 4, false, 2, 2>     last 4 values (172 tiles of 256 rows, one wave)"
+    echo "#   M = 2048  k_gemm_dma<1, false, 3, false, 2, 2>     last 4 values (473 tiles of 192 rows)"
+    echo "#   M = 3072  k_gemm_dma<1, true, 4, false, 2, 2>      last 4 values (512 tiles whole + the tail split)"
     echo "# dense GEMM (f4): k_mm_dma<0, 0, ...> int8 (B [N, K] read in place, then [K, N]), k_mm_dma<1, 1, ...>"
     echo "# fp16 -> fp32; Cijk_* are hipBLASLt's kernels for torch._int_mm and torch.matmul on the same shapes"
   } > "$OUT/mfma_util.txt" || exit $?
