@@ -9,7 +9,9 @@ dtype, bias and outlier columns and checks rtol = atol = 1e-2 against the
 oracle's exact accumulation; its streaming part draws the weight-streaming
 range (M <= 64, K a multiple of 1024, 8-64 MB of int8 weight), checks
 sampled rows against the oracle and every row against a float32 product on
-the GPU. The cases are fixed by their seeds, so a failure names a
+the GPU; its tile part draws M in (64, 384) with K a multiple of 64 and a
+ragged N (the 128 x 128 tiles or a split plan, and the same call without a
+workspace). The cases are fixed by their seeds, so a failure names a
 reproducible case.
 """
 from __future__ import annotations
@@ -230,3 +232,78 @@ def test_random_w8a16_streaming(i):
     if bg is not None:
         ref_all += bg.float()
     torch.testing.assert_close(y.float(), ref_all, rtol=1e-2, atol=1e-2)
+
+
+N_TILE_CASES = 16
+
+
+def _tile_case(i):
+    """Shapes of the MFMA tile path below 384 rows (128 x 128 tiles, or a
+    split plan where the host's model prefers one): M in (64, 384), K a
+    multiple of 64, N ragged."""
+    rng = np.random.default_rng(13000 + i)
+    M = int(rng.integers(65, 384))
+    K = 64 * int(rng.integers(1, 97))
+    N = int(rng.integers(16, 6000))
+    dt = [torch.float16, torch.bfloat16][i % 2]
+    bias = bool(rng.integers(0, 2))
+    n_out = int(rng.choice([0, 0, 1, 6, 17])) if K >= 32 else 0
+    return M, K, N, dt, bias, n_out
+
+
+@pytest.mark.parametrize("i", range(N_TILE_CASES))
+def test_random_w8a16_tiles(i):
+    """Four sampled rows against the oracle's exact accumulation and every
+    row against a float32 product of the dequantized weight on the GPU, at
+    rtol = atol = 1e-2, with and without a workspace (the split plans need
+    one; the 128 x 128 tiles do not)."""
+    from cublade_amd import _abi
+    from cublade_amd.bindings.hip import w8a16_linear
+    M, K, N, dt, bias, n_out = _tile_case(i)
+    print(f"[random w8a16 tiles {i}] M={M} K={K} N={N} dt={dt} bias={bias} n_out={n_out}",
+          flush=True)
+    g = torch.Generator().manual_seed(15000 + i)
+    x = torch.randn(M, K, generator=g)
+    oc = sorted(torch.randperm(K, generator=g)[:n_out].tolist()) if n_out else []
+    if oc:
+        x[:, oc] = 10.0 * torch.sign(torch.randn(M, len(oc), generator=g))
+    wq = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    if oc:
+        wq[:, oc] = 0
+    s = ((0.5 + torch.rand(N, generator=g)) / (73.0 * K ** 0.5)).to(dt)
+    b = (0.1 * torch.randn(N, generator=g)).to(dt) if bias else None
+    w_out = (0.02 * torch.randn(N, len(oc), generator=g)).to(dt) if oc else None
+    xd = x.to(dt)
+    xg, wg, sg = xd.to(DEV), wq.to(DEV), s.to(DEV)
+    bg = None if b is None else b.to(DEV)
+    og = torch.tensor(oc, dtype=torch.int64, device=DEV) if oc else None
+    wog = None if w_out is None else w_out.to(DEV)
+    y = w8a16_linear(xg, wg, sg, bg, og, wog)
+    assert y.dtype == dt and tuple(y.shape) == (M, N)
+
+    rows = np.unique(np.array([0, M - 1, M // 2, (11 * i) % M], np.int64))
+    ref = oracle.w8a16_linear(bits(xd), CODE_OF[dt], wq.numpy(), bits(s),
+                              bias=None if b is None else bits(b),
+                              outlier_cols=np.asarray(oc, np.int64) if oc else None,
+                              w_out=None if w_out is None else bits(w_out), rows=rows)
+    np.testing.assert_allclose(y.float().cpu().numpy()[rows], ref, rtol=1e-2, atol=1e-2)
+
+    wf = wg.float() * sg.float()[:, None]
+    ref_all = xg.float() @ wf.t()
+    if oc:
+        ref_all += xg.float()[:, og] @ wog.float().t()
+    if bg is not None:
+        ref_all += bg.float()
+    torch.testing.assert_close(y.float(), ref_all, rtol=1e-2, atol=1e-2)
+
+    # the same call with only the control block as workspace (no split)
+    L = _abi.lib()
+    y_one = torch.empty_like(y)
+    ws = torch.zeros(_abi.WS_CTRL_BYTES, dtype=torch.uint8, device=DEV)
+    rc = L.cbq_w8a16_linear(_abi.ptr(xg), CODE_OF[dt], _abi.ptr(wg), _abi.ptr(sg),
+                            None if bg is None else _abi.ptr(bg),
+                            None if og is None else _abi.ptr(og), n_out,
+                            None if wog is None else _abi.ptr(wog), M, N, K, _abi.ptr(ws),
+                            ws.numel(), _abi.ptr(y_one), _abi.stream_handle(xg.device))
+    assert rc == 0
+    torch.testing.assert_close(y_one.float(), ref_all, rtol=1e-2, atol=1e-2)
