@@ -36,8 +36,8 @@
 // over several k-ranges into fp32 partial tiles in the caller's workspace and
 // k_splitk_reduce sums them in a fixed order (no cross-workgroup fences);
 // dma_plan picks the tile height and the split with a fitted time model.
-// For 64 < M < 384, and wherever its one round of tiles is modelled faster
-// than a split, the same kernel runs 128 x 128 tiles instead (two waves
+// Where the time model prefers them (mostly 64 < M < 384 with up to one
+// round of tiles), the same kernel runs 128 x 128 tiles instead (two waves
 // along M, four along N, one 32-row weight tile each): no partials at all.
 // Outlier columns run on the matrix cores too: per 16 columns the tile's
 // gathered x columns and w_out rows are staged in LDS in one round of loads,
@@ -1770,11 +1770,10 @@ __global__ __launch_bounds__(kBlock) void k_general_reduce(GenArgs a) {
 //                 time model prefers it and the caller's workspace holds the
 //                 partials, unless one round of 128 x 128 tiles
 //                 (k_gemm_dma128, no partials) is modelled faster;
-//   64 < M < 384  else k_gemm_dma128; without k_gemm_dma (K % 64 != 0 or
-//                 offsets past 32 bits) k_gemm 128 x 64 x 64, 2 x 2 waves
-//   M >= 384      else k_gemm_dma without a split, or k_gemm_dma128 where
-//                 modelled faster; without k_gemm_dma k_gemm 256 x 256 x 64,
-//                 4 x 2 waves (M < 1024: 128 x 64 x 64)
+//   M > 64        else k_gemm_dma without a split (x tile of dma_plan), or
+//                 k_gemm_dma128 where modelled faster; without k_gemm_dma
+//                 (K % 64 != 0 or offsets past 32 bits) k_gemm 128 x 64 x 64,
+//                 2 x 2 waves (M >= 1024: 256 x 256 x 64, 4 x 2 waves)
 enum Kind { kSkinny1, kSkinny2, kSkinny4, kTileMid, kTileLarge, kTileDma, kStream1, kStream2,
             kStream4, kTileDmaSplit, kTileDma128 };
 
@@ -1842,7 +1841,7 @@ DmaPlan dma_plan(int64_t M, int64_t N, int64_t K, bool allow_split, int64_t* cos
 }
 
 // Modelled time of the 128 x 128 tiles (k_gemm_dma128) on dma_plan's scale,
-// for M > 64 when the tiles fit one workgroup per CU, else no estimate:
+// for M > 64 (else no estimate). When the tiles fit one workgroup per CU:
 // 6.9 us plus (0.41 + 0.17 x share of CUs busy) us per 64-k step, as timed
 // on MI355X (op level, fp16) over M = 128..256, N = 8192..28672,
 // K = 2048..8192, times the 1.13 by which dma_plan's model exceeds the
@@ -1853,11 +1852,17 @@ DmaPlan dma_plan(int64_t M, int64_t N, int64_t K, bool allow_split, int64_t* cos
 // against 47.2 (no split: k_gemm). It loses where a split keeps more CUs busy
 // for fewer steps (K = 8192: 67.7 against 64.4; M = 160: 39.4 against 37.0;
 // N = 4096, K = 11008: 95 against 40), which the model leaves to the split.
+// With more tiles than CUs two workgroups share each CU: 1.2 model units
+// (1.06 us) per 64-k step and round of 2 x CUs tiles, which leaves those
+// shapes to the whole 128-256 row tiles where they are faster (M = 320,
+// N = 22016: 69.0 against 89.1 us; M = 256, N = 65536: 116.4 against
+// 138.0; M = 200, N = 50000, K = 2048: 53.4 against 64.5).
 int64_t dma128_cost(int64_t M, int64_t N, int64_t K) {
   const int64_t cus = device_cus();
-  const int64_t tiles = cdiv(M, 128) * cdiv(N, 128);
-  if (M <= 64 || tiles > cus) return INT64_MAX;
-  return 780 + (K / 64) * (46 + 19 * tiles / cus);
+  const int64_t tiles = cdiv(M, 128) * cdiv(N, 128), nk = K / 64;
+  if (M <= 64) return INT64_MAX;
+  if (tiles <= cus) return 780 + nk * (46 + 19 * tiles / cus);
+  return 780 + nk * 120 * cdiv(tiles, 2 * cus);
 }
 
 // Whether k_gemm_dma is a candidate: M > 64, or 24 < M <= 64 with K above
@@ -1897,10 +1902,10 @@ Kind choose(int64_t M, int64_t N, int64_t K, int64_t n_out, size_t ws_bytes, Dma
       ws_bytes >= static_cast<size_t>(CBQ_WS_CTRL_BYTES + splitk_bytes(M, N, plan)))
     return cost128 < cost ? kTileDma128 : kTileDmaSplit;
   if (M <= 64) return narrow;
-  // no split below 384 rows: the 128 x 128 tiles (measured 2x faster than
-  // k_gemm's 128 x 64 tiles there: 40.0 against 78.5 us at M = 256,
-  // N = 11008, K = 4096; 38.4 against 74.2 us at M = 128, N = K = 4096)
-  if (M < 384) return kTileDma128;
+  // no split: whole tiles of 128-256 rows or the 128 x 128 tiles, by the
+  // model (below 384 rows both are about 2x faster than k_gemm's 128 x 64
+  // tiles: 40.0 against 78.5 us at M = 256, N = 11008, K = 4096 without a
+  // workspace; 38.4 against 74.2 us at M = 128, N = K = 4096)
   plan = dma_plan(M, N, K, false, &cost);
   return cost128 < cost ? kTileDma128 : kTileDma;
 }

@@ -302,7 +302,8 @@ def test_splitk_large_m_few_tiles(M, K, N):
     (96, 4096, 28672, torch.float16, 0, "128 x 128 tiles, one row of tiles"),
     (256, 3072, 14330, torch.float16, 1, "128 x 128 tiles, N tail (element stores)"),
     (383, 2048, 5000, torch.bfloat16, 3, "128 x 128 tiles, M and N tails"),
-    (130, 2048, 28672, torch.float16, 0, "128 x 128 tiles, two rounds' worth (no split below 384 rows)"),
+    (130, 2048, 28672, torch.float16, 0, "128-row tiles whole (224 tiles; 448 of 128 x 128 modelled slower)"),
+    (320, 2048, 22016, torch.bfloat16, 2, "192-row tiles whole below 384 rows (no split)"),
 ])
 def test_dma_plans(M, K, N, dt, n_out, path):
     """Each x-tile height (128, 192, 256 rows) and split plan of the MFMA tile
