@@ -16,13 +16,16 @@
 #    (suite_configs.json; the tracer's per-launch host cost would otherwise show in
 #    host-bound ops), then a kernel trace, then FETCH_SIZE / WRITE_SIZE runs
 #    of configs 1-5 (every suite kernel's HBM bytes per dispatch)
-# 4. rocprof's derived MfmaUtil counter (MFMA busy cycles over active cycles
-#    x SIMDs) for the MFMA kernels: W8A16 (config 5) and the dense GEMM (f4)
+# 4. the GPU clock under load (GRBM_GUI_ACTIVE over each dispatch's duration)
+#    and rocprof's derived MfmaUtil counter (MFMA busy cycles over active
+#    cycles x SIMDs) for the MFMA kernels: W8A16 (config 5) and the dense
+#    GEMM (f4)
 # 5. bare stream ceilings (cublade_amd/benchmark/stream_ceiling.hip) and the
 #    MFMA-only matrix-core rate (cublade_amd/benchmark/mfma_ceiling.hip)
 # Summaries: OUTDIR/bench_c2_kernels.txt, OUTDIR/quant_int8_c2_traffic.json,
 # OUTDIR/dequant_int8_c2_traffic.json, OUTDIR/suite_kernels.txt,
-# OUTDIR/suite_traffic.txt, OUTDIR/suite_configs.json, OUTDIR/mfma_util.txt,
+# OUTDIR/suite_traffic.txt, OUTDIR/suite_configs.json, OUTDIR/clock_grbm.txt,
+# OUTDIR/mfma_util.txt,
 # OUTDIR/stream_ceiling.txt, OUTDIR/mfma_ceiling.txt. Raw
 # databases go to RAWDIR (default OUTDIR/raw; they total about 80 MiB), the
 # programs' output to OUTDIR/logs.
@@ -74,6 +77,9 @@ if want suite; then
   step "counter WRITE_SIZE: suite configs c1-c5"
   timeout -s KILL 300 rocprofv3 --pmc WRITE_SIZE --kernel-trace -d "$RAW/swrite" -o suite -- \
     $PY -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5 --reps 3 --warmup 1 > "$LOGS/swrite.log" 2>&1 || exit $?
+  step "counter GRBM_GUI_ACTIVE: suite configs c2,c5,c5m,f4 (clock under load)"
+  timeout -s KILL 300 rocprofv3 --pmc GRBM_GUI_ACTIVE --kernel-trace -d "$RAW/clk" -o suite -- \
+    $PY -m cublade_amd.benchmark.suite --configs c2,c5,c5m,f4 --reps 3 --warmup 1 > "$LOGS/clk.log" 2>&1 || exit $?
   step "counter MfmaUtil: suite configs c5,c5m,f4"
   timeout -s KILL 300 rocprofv3 --pmc MfmaUtil --kernel-trace -d "$RAW/mfma" -o suite -- \
     $PY -m cublade_amd.benchmark.suite --configs c5,c5m,f4 --reps 3 --warmup 1 > "$LOGS/mfma.log" 2>&1 || exit $?
@@ -124,6 +130,14 @@ if want suite; then
     echo "# commands: rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --kernel-trace -d RAW/sfetch -o suite -- python -u -m cublade_amd.benchmark.suite --configs c1,c2,c3,c4,c5 --reps 3 --warmup 1"
     $R traffic-all "$RAW/sfetch/suite_results.db" "$RAW/swrite/suite_results.db" $CAL
   } > "$OUT/suite_traffic.txt" || exit $?
+  {
+    echo "# average GPU clock per dispatch: GRBM_GUI_ACTIVE (one instance per XCD, summed, / 8) over the"
+    echo "# dispatch's duration from the kernel trace of the same run; short dispatches read high (the"
+    echo "# counter's window is wider than the kernel). W8A16 c5 (M = 16 / 256 / 768 / 1536 / 4096) and c5m"
+    echo "# (M = 1024 / 2048 / 3072), N = 11008, K = 4096; c2; f4 (8192^3; Cijk_* are hipBLASLt's kernels)"
+    echo "# command: rocprofv3 --pmc GRBM_GUI_ACTIVE --kernel-trace -d RAW/clk -o suite -- python -u -m cublade_amd.benchmark.suite --configs c2,c5,c5m,f4 --reps 3 --warmup 1"
+    $R clock "$RAW/clk/suite_results.db" | grep -E "kernel |cbq::|Cijk"
+  } > "$OUT/clock_grbm.txt" || exit $?
   {
     echo "# rocprof derived counter MfmaUtil = sum(SQ_VALU_MFMA_BUSY_CYCLES) / (max(GRBM_GUI_ACTIVE) * SIMDs) * 100,"
     echo "# per kernel: mean and median over dispatches, then the values in dispatch order (the first is the"

@@ -15,6 +15,11 @@
     python -m cublade_amd.benchmark.rocprof traffic-all FETCH.db WRITE.db \
         CAL_FETCH.db CAL_WRITE.db CAL_KIB
 
+    # average GPU clock per dispatch (run with --pmc GRBM_GUI_ACTIVE --kernel-trace):
+    # the counter summed over its instances (one per XCD) over the dispatch's
+    # duration, in MHz, divided by the instance count
+    python -m cublade_amd.benchmark.rocprof clock DIR/NAME_results.db
+
 The calibration runs profile a copy of CAL_KIB KiB (copy_calib.py); the
 factor for each counter is CAL_KIB / (its mean over the copy dispatches).
 Kernel names are shortened to their template signature. Output is plain
@@ -68,6 +73,23 @@ def counter_stats(db: str):
     return res
 
 
+def clock_stats(db: str, counter: str = "GRBM_GUI_ACTIVE", instances: int = 8):
+    """{kernel: [(duration_us, MHz) per dispatch]}: the counter summed over its
+    instances (GRBM_GUI_ACTIVE: one per XCD, 8 on MI355X) over the dispatch's
+    duration from the kernel trace of the same run. Short dispatches read high:
+    the counter's window is wider than the kernel."""
+    con = sqlite3.connect(db)
+    dur = dict(con.execute("select dispatch_id, duration from kernels"))
+    res = defaultdict(list)
+    q = ("select dispatch_id, kernel_name, sum(value) from counters_collection "
+         "where counter_name = ? group by dispatch_id")
+    for did, name, v in con.execute(q, (counter,)):
+        d = dur.get(did)
+        if d:
+            res[_short(name)].append((d / 1e3, v / instances / d * 1e3))
+    return res
+
+
 def _mean_for(stats, kernel_sub, counter):
     vals = [v for (k, c), vs in stats.items() if kernel_sub in k and c == counter for v in vs]
     if not vals:
@@ -118,6 +140,12 @@ def main(argv=None):
         print(f"{'kernel':110s} {'calls':>6s} {'read_MB':>10s} {'write_MB':>10s} {'total_MB':>10s}")
         for k, n, rb, wb in traffic_all(*argv[1:]):
             print(f"{k:110s} {n:6d} {rb / 1e6:10.2f} {wb / 1e6:10.2f} {(rb + wb) / 1e6:10.2f}")
+        return 0
+    if len(argv) == 2 and argv[0] == "clock":
+        print(f"{'kernel':110s} {'calls':>6s}  duration_us / MHz per dispatch")
+        for k, vals in sorted(clock_stats(argv[1]).items()):
+            each = " ".join(f"{d:.1f}/{m:.0f}" for d, m in vals[:8]) + (" ..." if len(vals) > 8 else "")
+            print(f"{k:110s} {len(vals):6d}  {each}")
         return 0
     if len(argv) != 2 or argv[0] not in ("kernels", "counters"):
         print(__doc__)
