@@ -45,16 +45,17 @@ def _check_replays(static_in, make_input, fn, g, out, n=3):
                                w.view(torch.uint8) if w.dtype.itemsize == 1 else w), f"replay {seed}"
 
 
-@pytest.mark.parametrize("M,dt", [(16, torch.float16), (256, torch.float16),
-                                  (4096, torch.float16), (256, torch.float32)])
-def test_graph_w8a16_layer(M, dt):
+@pytest.mark.parametrize("M,dt,N,K", [(16, torch.float16, 4096, 2048), (256, torch.float16, 4096, 2048),
+                                      (4096, torch.float16, 4096, 2048), (256, torch.float32, 4096, 2048),
+                                      (256, torch.bfloat16, 11008, 4096)])
+def test_graph_w8a16_layer(M, dt, N, K):
     """The W8A16 layer at a decode shape (weight streaming), at M = 256
     (split-K: fp32 partials in the workspace, reused by every replay), at
     M = 4096 (256-row MFMA tiles, whose kernel keeps a few spilled registers
-    in scratch memory), and with fp32 activations at M = 256 (three launches:
-    the bf16 planes of x and the partial planes in the workspace)."""
+    in scratch memory), with fp32 activations at M = 256 (three launches:
+    the bf16 planes of x and the partial planes in the workspace), and at
+    config 5's M = 256 (one round of 128 x 128 tiles, no workspace)."""
     from cublade_amd.quantization import cuBladeW8A16LinearLayer
-    N, K = 4096, 2048
     g0 = torch.Generator().manual_seed(M)
     layer = cuBladeW8A16LinearLayer(K, N, bias=True, dtype=dt)
     layer.quantize((0.02 * torch.randn(N, K, generator=g0)).to(dt).to(DEV))
